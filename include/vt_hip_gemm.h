@@ -1,0 +1,128 @@
+/*
+ * vt_hip_gemm.h -- C ABI of libvt_hip_gemm.so, the MI355X (gfx950) exact
+ * int8 x int8 -> int32 GEMM behind the `hip_gemm` specialization.
+ *
+ * Contract (same as the reference's Gemmini GEMM, extended by an explicit
+ * initial partial sum):
+ *     C[b][i][j] = D[b][i][j] + sum_t A[b][i][t] * B[b][t][j]      (D optional)
+ * with int32 accumulation modulo 2^32 (VeriTac/Gemmini/Word.lean:11, :31) over
+ * row-major operands A[i*lda+t], B[t*ldb+j], C[i*ldc+j]
+ * (VeriTac/Gemmini/Semantics.lean:76-77, specializations/gemmini_gemm/
+ * backend.py:569-580). Inside the reference's legality bound
+ * k*16384 <= 2^31-1 (VeriTac/Gemmini/Plan.lean:86-92) plus |D| the result is
+ * the exact integer product; outside it the result is the wrapped int32 sum,
+ * which is what the Lean model's signed32 accumulator computes.
+ *
+ * The reference has no FFI for this path: its specialization API is Python
+ * (specializations/gemmini_gemm/backend.py, specializations/cpu_gemm/
+ * runner.py) and its native layer is emitted C run as a subprocess
+ * (cpu_gemm/runner.py:65-108) or Gemmini command streams on Spike. This
+ * header replaces that native execution layer; the Python specialization
+ * (specializations/hip_gemm/backend.py) binds it with ctypes.
+ *
+ * Conventions:
+ *   - every function returns 0 (VT_OK) or a negative VT_E* code; the message
+ *     of the last failure on the calling thread is vt_last_error();
+ *   - argument and shape validation happens on the host before any device
+ *     call, so invalid input never reaches a kernel;
+ *   - pointers are device pointers owned by the caller (borrowed for the
+ *     call); the library never allocates or frees caller buffers;
+ *   - `stream` is a hipStream_t (NULL = the default stream); work is
+ *     enqueued asynchronously on it.
+ */
+#ifndef VT_HIP_GEMM_H
+#define VT_HIP_GEMM_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VT_ABI_VERSION 1
+
+/* Status codes. */
+#define VT_OK 0
+#define VT_EINVAL (-1)        /* null pointer, negative size, bad stride     */
+#define VT_EUNSUPPORTED (-2)  /* variant cannot run this shape / alignment   */
+#define VT_EHIP (-3)          /* HIP runtime error (launch, allocation, ...) */
+#define VT_ENODEV (-4)        /* no HIP device, or the device is not gfx950  */
+
+/* Kernel variants. VT_VARIANT_AUTO picks one from the shape. */
+#define VT_VARIANT_AUTO 0
+#define VT_VARIANT_MFMA_256x256 1  /* compute-bound: 256x256 tile, 4 waves,
+                                      v_mfma_i32_32x32x32_i8                  */
+#define VT_VARIANT_MFMA_128x128 2  /* 128x128 tile, 4 waves, same MFMA        */
+#define VT_VARIANT_SKINNY 3        /* M <= 16 decode shapes: B streamed once,
+                                      v_mfma_i32_16x16x64_i8, K split         */
+#define VT_VARIANT_GENERIC 4       /* any shape/stride/alignment, VALU        */
+#define VT_VARIANT_MFMA_256x128 5  /* 256x128 tile, 4 waves                   */
+#define VT_VARIANT_COUNT 6
+
+/*
+ * vt_gemm_i8 -- batched exact int8 GEMM.
+ *
+ * Replaces the execution of one GEMM by the reference's specializations:
+ * `run_commands` (specializations/gemmini_gemm/backend.py:433-562) and the
+ * emitted scalar kernel `veritac_scalar_ref` (backend.py:712-720) for the
+ * Gemmini contract, and the emitted loop nest timed by `benchmark_matmul`
+ * (specializations/cpu_gemm/runner.py:111-232). Batched B-reuse
+ * (specializations/gemmini_gemm/lowering.py:18-40) is stride_b == 0.
+ *
+ *   A  int8  [batch][M][lda]  (stride_a elements between batches)
+ *   B  int8  [batch][K][ldb]  (stride_b elements; 0 = one B shared by all)
+ *   D  int32 [batch][M][ldd]  initial partial sum, or NULL for zero
+ *   C  int32 [batch][M][ldc]  output (may alias D exactly: in-place C += A.B)
+ *   M, N, K >= 0 (M == 0 or N == 0: nothing to do; K == 0: C = D or 0)
+ *   lda >= K, ldb >= N, ldd >= N, ldc >= N
+ *   variant: VT_VARIANT_*; k_split: K slices for VT_VARIANT_SKINNY
+ *            (0 = choose automatically; ignored by other variants)
+ *
+ * The MFMA and skinny variants need N % 16 == 0, K % 16 == 0, lda and ldb
+ * multiples of 16 and 16-byte-aligned A and B; VT_VARIANT_AUTO falls back to
+ * VT_VARIANT_GENERIC otherwise, an explicit variant returns VT_EUNSUPPORTED.
+ */
+int vt_gemm_i8(const int8_t *A, const int8_t *B, const int32_t *D, int32_t *C,
+               int64_t M, int64_t N, int64_t K,
+               int64_t lda, int64_t ldb, int64_t ldd, int64_t ldc,
+               int64_t batch, int64_t stride_a, int64_t stride_b,
+               int64_t stride_d, int64_t stride_c,
+               int32_t variant, int32_t k_split, void *stream);
+
+/*
+ * vt_gemm_select -- the variant (and K split) VT_VARIANT_AUTO would launch.
+ * Mirrors the reference's candidate selection (`optimize`,
+ * backend.py:1072-1093) at the native layer; no device call.
+ */
+int vt_gemm_select(int64_t M, int64_t N, int64_t K, int64_t batch,
+                   int64_t lda, int64_t ldb, int32_t aligned16,
+                   int32_t *variant_out, int32_t *k_split_out);
+
+/*
+ * vt_variant_info -- static resources of one variant: tile sizes, threads per
+ * workgroup, LDS bytes per workgroup. Mirrors `required_resources`
+ * (backend.py:97-104). No device call.
+ */
+int vt_variant_info(int32_t variant, int32_t *tile_m, int32_t *tile_n,
+                    int32_t *tile_k, int32_t *threads, int32_t *lds_bytes);
+
+/* Name of a variant ("mfma_256x256", ...) or NULL for an unknown id. */
+const char *vt_variant_name(int32_t variant);
+
+/* Message of the last failure on the calling thread ("" if none). */
+const char *vt_last_error(void);
+
+/* hipStreamSynchronize(stream), reporting asynchronous kernel errors. */
+int vt_sync(void *stream);
+
+/* Number of usable gfx950 devices (0 if none); no error on a GPU-less host. */
+int vt_device_count(void);
+
+/* VT_ABI_VERSION of the loaded library. */
+int vt_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VT_HIP_GEMM_H */

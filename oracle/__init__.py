@@ -1,0 +1,36 @@
+"""CPU oracle for the exact int8 x int8 -> int32 GEMM contract.
+
+TEST INFRASTRUCTURE ONLY. Nothing in the product (``veritac_amd``,
+``specializations``) imports, links or runs anything under ``oracle/``.
+Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` use it, and only as the checker or the timed CPU baseline.
+
+Contents
+--------
+``gemm_oracle``  numpy / pure-Python restatements of the reference's scalar
+                 oracles and deterministic input generators (each function
+                 cites the reference file:line it restates).
+``ref_gemm.c``   C restatement of the reference's emitted scalar kernel
+                 ``veritac_scalar_ref`` with an optional initial partial sum
+                 and OpenMP over output rows; built by ``oracle/Makefile``
+                 into ``oracle/_build/libvt_oracle.so``.
+``cref``         ctypes loader for that library.
+
+Pinning (how each function is checked, see tests/test_oracle.py):
+  scalar_matmul / reference_matmul / gemm_i8 / ref_gemm.c
+      - the 24 full-output Spike COUT vectors recorded by the reference
+        (tests/golden/spike_cout.json, independent of the reference's Python);
+      - the reference's hand known-answer tests (2x2 extrema, 2x2 mixed sign,
+        [[19,22],[43,50]]);
+      - brute force on tiny inputs, int64 matmul vs exact float64 BLAS,
+        K-tiling invariance, a planted-mistake check (dropped partial sum).
+  lcg8_stream / fill_inputs
+      - the reference's own LCG known-answer test and the lcg COUT vectors.
+  deterministic_inputs ("lcg" mode, byte-128 mapping)
+      - closed-form restatement of backend.py:583-593, cross-checked against
+        an independent C-style uint32 implementation in ref_gemm.c
+        (vt_ref_lcg_fill) and against its relation to lcg8_stream
+        (value = byte - 128 for the same state sequence). No recorded
+        reference vector uses this stream, so beyond that relation it is
+        "parity unpinned" (no fixture fixes its absolute values).
+"""

@@ -1,0 +1,28 @@
+import os
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU and the built HIP library")
+
+
+@pytest.fixture(scope="session")
+def golden():
+    import json
+    with open(os.path.join(ROOT, "tests", "golden", "spike_cout.json")) as fh:
+        return json.load(fh)
+
+
+def decode_cout(hex_text):
+    """8 hex digits per int32 (run_raw_spike.py:409-423 parse rule)."""
+    vals = []
+    for i in range(0, len(hex_text), 8):
+        w = int(hex_text[i:i + 8], 16)
+        vals.append(w - (1 << 32) if w >= (1 << 31) else w)
+    return vals

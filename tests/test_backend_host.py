@@ -1,0 +1,180 @@
+"""hip_gemm backend host logic on the CPU: plan validation (mirrors the
+reference's tests/test_gemmini.py:96-161 and test_gemmini_checker.py:26-67),
+candidate selection, input generators, and fail-closed execution with an
+injected runner."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import gemm_oracle as go
+from veritac_amd import HipGemmError
+from veritac_amd.specializations.hip_gemm import backend as hg
+from veritac_amd.specializations.hip_gemm import inputs
+
+
+def plan(**kw):
+    p = hg.make_plan(32, 32, 32, variant="mfma_128x128")
+    p.update(kw)
+    return p
+
+
+def test_minimum_plans_validate():
+    for v in hg.VARIANTS:
+        for shape in ((16, 16, 16), (32, 32, 32), (48, 32, 64)):
+            if v == "skinny":
+                shape = (min(shape[0], 16),) + shape[1:]
+            p = hg.make_plan(*shape, variant=v)
+            ok, reason = hg.validate_plan(p)
+            assert ok, (v, shape, reason)
+
+
+@pytest.mark.parametrize("name", ["m", "n", "k", "batch", "dim", "d_max_abs", "k_split"])
+@pytest.mark.parametrize("value", [0.5, True, None, "32", [], {}])
+def test_malformed_integer_fields_rejected(name, value):
+    ok, reason = hg.validate_plan(plan(**{name: value}))
+    assert not ok and name in reason
+
+
+def test_missing_fields_and_non_dict_rejected():
+    for name in ("m", "n", "k", "batch", "dim", "variant", "has_d", "b_shared"):
+        p = plan()
+        del p[name]
+        assert not hg.validate_plan(p)[0]
+    for value in (None, [], "plan", 42):
+        assert hg.validate_plan(value) == (False, "plan must be a JSON object")
+    assert not hg.validate_plan(plan(has_d=1))[0]
+
+
+@pytest.mark.parametrize("changes", [dict(m=0), dict(n=0), dict(k=0), dict(dim=0), dict(dim=8),
+                                     dict(n=17), dict(k=33), dict(k=131072), dict(batch=0),
+                                     dict(variant="unknown"), dict(variant="auto"),
+                                     dict(k_split=-1), dict(k_split=2), dict(d_max_abs=5)])
+def test_bad_shapes_and_arithmetic_bound(changes):
+    assert not hg.validate_plan(plan(**changes))[0]
+
+
+def test_overflow_bound_boundary():
+    # k*16384 <= 2^31-1 (Plan.lean:86-92): k=131056 accepted, k=131072 rejected
+    assert hg.validate_plan(plan(k=131056))[0]
+    assert not hg.validate_plan(plan(k=131072))[0]
+    # with an initial partial sum the bound includes |D|
+    assert hg.validate_plan(plan(k=256, has_d=True, d_max_abs=1 << 20))[0]
+    assert not hg.validate_plan(plan(k=131056, has_d=True, d_max_abs=1 << 20))[0]
+
+
+def test_variant_specific_rules():
+    assert hg.validate_plan(plan(m=1, variant="skinny"))[0]
+    assert hg.validate_plan(plan(m=16, variant="skinny", k_split=3))[0]
+    assert not hg.validate_plan(plan(m=17, variant="skinny"))[0]
+    assert hg.validate_plan(plan(m=5, n=7, k=9, variant="generic"))[0]
+    assert not hg.validate_plan(plan(m=5, n=7, k=9, variant="mfma_256x256"))[0]
+
+
+def test_make_plan_auto_and_optimize():
+    p = hg.make_plan(16, 14336, 4096)
+    assert p["variant"] == "skinny" and p["k_split"] >= 1
+    assert hg.make_plan(8192, 8192, 8192)["variant"] == "mfma_256x256"
+    assert hg.make_plan(5, 7, 9)["variant"] == "generic"
+    res = hg.optimize(8192, 8192, 8192)
+    names = [c["plan"]["variant"] for c in res["candidates"]]
+    assert names == list(hg.VARIANTS)
+    skinny = res["candidates"][names.index("skinny")]
+    assert not skinny["valid"] and "m <= 16" in skinny["invalid_reason"]
+    assert res["winner"]["variant"] == "mfma_256x256"
+    res = hg.optimize(16, 14336, 4096)
+    assert res["winner"]["variant"] == "skinny"
+    with pytest.raises(HipGemmError):
+        hg.make_plan(0, 16, 16)
+
+
+def test_modeled_counts_are_consistent():
+    p = hg.make_plan(64, 512, 1024, batch=64, b_shared=True, variant="mfma_256x256")
+    c = hg.modeled_counts(p)
+    assert c["ops"] == 2 * 64 * 64 * 512 * 1024
+    assert c["bytes_algorithmic"] == 64 * 64 * 1024 + 1024 * 512 + 4 * 64 * 64 * 512
+    assert c["workgroups"] == (64 * 64 // 256) * (512 // 256)
+    p = hg.make_plan(256, 256, 256, has_d=True, d_max_abs=1 << 20, variant="mfma_128x128")
+    assert hg.modeled_counts(p)["bytes_algorithmic"] == 2 * 65536 + 8 * 65536
+
+
+def test_skinny_split_mirrors_native_rule():
+    p = hg.make_plan(16, 14336, 4096, variant="skinny")
+    ks, chunk = hg.skinny_split(p)
+    assert chunk % 64 == 0 and ks * chunk >= 4096 and (ks - 1) * chunk < 4096
+    p1 = dict(p, k_split=1)
+    ks1, chunk1 = hg.skinny_split(p1)
+    assert ks1 == 1 and chunk1 == 4096
+    lds, wgs = hg.required_resources(dict(p, k=131056, k_split=1))
+    assert lds <= hg.LDS_PER_CU
+
+
+def fake_runner(plan, A, B, D, C, stream):
+    """Host-side stand-in for the device: computes through the oracle (tests only)."""
+    out = go.gemm_i8(A.numpy(), B.numpy(), None if D is None else D.numpy())
+    C.copy_(torch.from_numpy(out))
+
+
+def test_run_with_injected_runner():
+    A, B = inputs.deterministic_inputs(32, 48, 64, 7)
+    p = hg.make_plan(32, 48, 64, variant="mfma_128x128")
+    C = hg.run(p, torch.from_numpy(A), torch.from_numpy(B), runner=fake_runner)
+    assert np.array_equal(C.numpy(), go.gemm_i8(A, B))
+
+
+def test_run_fails_closed():
+    A = torch.zeros(32, 32, dtype=torch.int8)
+    B = torch.zeros(32, 32, dtype=torch.int8)
+    p = plan()
+    with pytest.raises(HipGemmError, match="no CPU path"):
+        hg.run(p, A, B)                                  # CPU tensors, no runner
+    with pytest.raises(HipGemmError, match="invalid plan"):
+        hg.run(plan(k=33), A, B, runner=fake_runner)
+    with pytest.raises(HipGemmError, match="shape"):
+        hg.run(plan(n=48), A, B, runner=fake_runner)
+    with pytest.raises(HipGemmError, match="int8"):
+        hg.run(p, A.int(), B, runner=fake_runner)
+    with pytest.raises(HipGemmError, match="D"):
+        hg.run(p, A, B, D=torch.zeros(32, 32, dtype=torch.int32), runner=fake_runner)
+    with pytest.raises(HipGemmError, match="has_d"):
+        hg.run(plan(has_d=True, d_max_abs=1), A, B, runner=fake_runner)
+    with pytest.raises(HipGemmError, match="unit stride"):
+        hg.run(p, A.t(), B, runner=fake_runner)
+
+
+def test_run_flat_validates_like_the_interpreter():
+    p = hg.make_plan(16, 16, 16, variant="generic")
+    with pytest.raises(HipGemmError, match="out of"):
+        hg.run_flat(p, [200] * 256, [0] * 256)
+    with pytest.raises(HipGemmError, match="values"):
+        hg.run_flat(p, [0] * 10, [0] * 256)
+    with pytest.raises(HipGemmError):
+        hg.run_flat(p, [1.0] * 256, [0] * 256)
+
+
+def test_product_generators_match_oracle():
+    for mode in ("lcg", "max", "minmax", "min", "zero"):
+        for seed in (0, 7, 917, 987654321):
+            A, B = inputs.deterministic_inputs(5, 9, 6000 if mode == "lcg" and seed == 7 else 3,
+                                               seed, mode)
+            oa, ob = go.deterministic_inputs(A.shape[0], B.shape[1], A.shape[1], seed, mode)
+            assert A.reshape(-1).tolist() == oa and B.reshape(-1).tolist() == ob
+    for mode in ("zeros", "extrema", "lcg"):
+        A, B = inputs.spike_inputs(mode, 16, 32, 48)
+        a, b = go.fill_inputs(mode, 16 * 48, 48 * 32)
+        assert A.reshape(-1).tolist() == [go.to_int8(v) for v in a]
+        assert B.reshape(-1).tolist() == [go.to_int8(v) for v in b]
+
+
+def test_config_inputs_properties():
+    c1 = inputs.config_inputs(1, seed=1)
+    assert c1["A"].shape == (64, 64) and c1["D"] is None and c1["A"].dtype == np.int8
+    c2 = inputs.config_inputs(2, seed=1)
+    assert c2["D"].dtype == np.int32 and np.abs(c2["D"].astype(np.int64)).max() <= 1 << 20
+    c3 = inputs.config_inputs(3, seed=1)
+    assert c3["A"].shape == (64, 512, 1024) and c3["B"].shape == (1024, 1024)
+    c4 = inputs.config_inputs(4, seed=1, m=1)
+    assert c4["A"].shape == (1, 4096) and c4["A"].min() >= -127
+    assert c4["B"].shape == (4096, 14336) and 25 < c4["B"].astype(np.float64).std() < 39
+    again = inputs.config_inputs(2, seed=1)
+    assert np.array_equal(again["A"], c2["A"]) and np.array_equal(again["D"], c2["D"])
+    assert inputs.config_shape(5) == (1, 8192, 8192, 8192, False, False)

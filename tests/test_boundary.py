@@ -1,0 +1,105 @@
+"""C-ABI boundary on a host without a GPU: the library loads, exports every
+symbol include/vt_hip_gemm.h declares, validates arguments before any device
+call, and fails closed (VT_ENODEV) when no gfx950 device exists."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import veritac_amd
+from veritac_amd import _lib
+from veritac_amd.specializations.hip_gemm import backend as hg
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "vt_hip_gemm.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(vt_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = veritac_amd.load_library()
+    declared = header_functions()
+    assert declared == sorted(_lib.EXPORTS)
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert lib.vt_abi_version() == 1
+
+
+def test_variant_table_matches_backend():
+    for name in hg.VARIANTS:
+        info = _lib.variant_info(name)
+        assert (info["tile_m"], info["tile_n"], info["tile_k"], info["threads"],
+                info["lds_bytes"]) == hg.TILES[name], name
+        assert veritac_amd.load_library().vt_variant_name(_lib.VARIANT_IDS[name]).decode() == name
+    assert veritac_amd.load_library().vt_variant_name(99) is None
+
+
+def test_native_selection_for_benchmark_configs():
+    assert _lib.select_variant(16, 14336, 4096)[0] == "skinny"
+    assert _lib.select_variant(1, 14336, 4096)[0] == "skinny"
+    assert _lib.select_variant(8192, 8192, 8192) == ("mfma_256x256", 0)
+    assert _lib.select_variant(512, 1024, 1024, 64)[0].startswith("mfma")
+    assert _lib.select_variant(64, 64, 64)[0] == "mfma_128x128"
+    assert _lib.select_variant(64, 60, 64, aligned=False)[0] == "generic"
+
+
+def call(M=4, N=16, K=16, lda=None, ldb=None, ldd=None, ldc=None, batch=1, variant=0,
+         k_split=0, A=1 << 20, B=1 << 21, D=None, C=1 << 22, strides=(0, 0, 0, 0)):
+    lib = veritac_amd.load_library()
+    return lib.vt_gemm_i8(A, B, D, C, M, N, K, K if lda is None else lda,
+                          N if ldb is None else ldb, N if ldd is None else ldd,
+                          N if ldc is None else ldc, batch, *strides, variant, k_split, None)
+
+
+@pytest.mark.parametrize("kw", [
+    dict(M=-1), dict(N=-2), dict(K=-3), dict(batch=-1), dict(C=None), dict(A=None),
+    dict(B=None), dict(lda=8), dict(ldb=8), dict(ldc=8), dict(D=1 << 23, ldd=4),
+    dict(variant=99), dict(k_split=-1), dict(batch=2, strides=(64, 0, 0, 0)),
+    dict(strides=(-16, 0, 0, 0)),
+])
+def test_invalid_arguments_rejected_before_device(kw):
+    assert call(**kw) == _lib.VT_EINVAL
+    assert _lib.last_error()
+
+
+def test_explicit_vector_variant_refuses_unaligned_shapes():
+    assert call(N=20, variant=1) == _lib.VT_EUNSUPPORTED
+    assert call(K=20, lda=20, variant=3) == _lib.VT_EUNSUPPORTED
+    assert call(M=17, variant=3) == _lib.VT_EUNSUPPORTED
+    assert call(A=(1 << 20) + 1, variant=2) == _lib.VT_EUNSUPPORTED
+
+
+def test_empty_problems_are_noops():
+    assert call(M=0, C=None, A=None, B=None) == _lib.VT_OK
+    assert call(N=0, C=None) == _lib.VT_OK
+    assert call(batch=0) == _lib.VT_OK
+
+
+@pytest.mark.skipif(veritac_amd.load_library().vt_device_count() > 0, reason="GPU present")
+def test_fails_closed_without_gpu():
+    assert veritac_amd.load_library().vt_device_count() == 0
+    assert call() == _lib.VT_ENODEV
+    assert "device" in _lib.last_error()
+    assert veritac_amd.load_library().vt_sync(None) == _lib.VT_ENODEV
+    with pytest.raises(_lib.HipGemmError):
+        _lib.gemm_raw(1 << 20, 1 << 21, None, 1 << 22, 4, 16, 16, 16, 16, 16, 16)
+
+
+def test_missing_library_fails_closed(tmp_path, monkeypatch):
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setenv("VT_HIP_GEMM_LIB", str(tmp_path / "nope.so"))
+    with pytest.raises(_lib.HipGemmError):
+        _lib.load_library()
+    bad = tmp_path / "bad.so"
+    bad.write_bytes(b"not an ELF")
+    monkeypatch.setenv("VT_HIP_GEMM_LIB", str(bad))
+    with pytest.raises(_lib.HipGemmError):
+        _lib.load_library()
+    monkeypatch.delenv("VT_HIP_GEMM_LIB")
+    monkeypatch.setattr(_lib, "_lib", None)
+    assert _lib.load_library() is not None

@@ -1,0 +1,278 @@
+"""Bit-exact parity of the HIP kernels with the CPU oracle (needs a gfx950 GPU).
+
+Every call goes through the C ABI (veritac_amd._lib -> libvt_hip_gemm.so).
+Outputs are poisoned with INT32_MIN before each launch (the reference's
+emitted-C harness does the same, backend.py:756-760) so unwritten cells show.
+Small and medium shapes are compared element by element with the oracle;
+the full-size benchmark shapes are checked with exact int64/float64
+properties (row and column checksums, Freivalds products, full sampled rows
+and columns) that any wrong element fails with overwhelming probability.
+"""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from conftest import decode_cout
+from oracle import cref
+from oracle import gemm_oracle as go
+from veritac_amd import _lib
+from veritac_amd.specializations.hip_gemm import backend as hg
+from veritac_amd.specializations.hip_gemm import inputs
+
+pytestmark = pytest.mark.gpu
+
+INT32_MIN = -2**31
+VEC_VARIANTS = ("mfma_256x256", "mfma_256x128", "mfma_128x128")
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    lib = _lib.load_library()
+    assert lib.vt_device_count() >= 1, "GPU visible but not gfx950"
+    return torch.device("cuda", 0)
+
+
+def say(*args):
+    print(*args, flush=True)
+
+
+def gpu_gemm(dev, A, B, D=None, variant="auto", k_split=0, batch_shared=False):
+    """Run C = D + A.B through the C ABI with explicit pointers and strides."""
+    At = torch.from_numpy(np.ascontiguousarray(A)).to(dev)
+    Bt = torch.from_numpy(np.ascontiguousarray(B)).to(dev)
+    Dt = torch.from_numpy(np.ascontiguousarray(D)).to(dev) if D is not None else None
+    batched = At.dim() == 3
+    b = At.shape[0] if batched else 1
+    M, K = At.shape[-2:]
+    N = Bt.shape[-1]
+    C = torch.full((b, M, N) if batched else (M, N), INT32_MIN, dtype=torch.int32, device=dev)
+    _lib.gemm_raw(At.data_ptr(), Bt.data_ptr(), Dt.data_ptr() if Dt is not None else None,
+                  C.data_ptr(), M, N, K, K, N, N, N, b,
+                  M * K if batched else 0, (K * N if Bt.dim() == 3 else 0),
+                  M * N if (batched and Dt is not None) else 0, M * N if batched else 0,
+                  variant, k_split, None)
+    _lib.sync(None)
+    return C.cpu().numpy()
+
+
+# ---------------------------------------------------------------------------
+# Golden vectors (recorded Spike outputs) through every kernel
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("variant", ["auto", "mfma_128x128", "mfma_256x256", "mfma_256x128",
+                                     "skinny", "generic"])
+def test_spike_golden_vectors(dev, golden, variant):
+    for run in golden["runs"]:
+        m, n, k = run["plan"]["m"], run["plan"]["n"], run["plan"]["k"]
+        if variant == "skinny" and m > 16:
+            continue
+        for mode in golden["modes"]:
+            say("golden", run["name"], mode, variant)
+            A, B = inputs.spike_inputs(mode, m, n, k)
+            want = np.array(decode_cout(run["cout"][mode]), np.int32).reshape(m, n)
+            assert np.array_equal(gpu_gemm(dev, A, B, variant=variant), want), (run["name"], mode)
+
+
+# ---------------------------------------------------------------------------
+# The benchmark configurations
+# ---------------------------------------------------------------------------
+
+def test_config1_64cube(dev):
+    for seed in (0, 1, 2):
+        c = inputs.config_inputs(1, seed=seed)
+        say("config1 seed", seed)
+        for variant in ("auto", "mfma_128x128", "generic"):
+            assert np.array_equal(gpu_gemm(dev, c["A"], c["B"], variant=variant),
+                                  go.gemm_i8(c["A"], c["B"])), (seed, variant)
+
+
+def test_config2_partial_sum_256(dev):
+    for seed in (0, 5):
+        c = inputs.config_inputs(2, seed=seed)
+        want = go.gemm_i8_ktiled(c["A"], c["B"], c["D"], k_tile=16)
+        assert np.array_equal(want, go.gemm_i8_int64(c["A"], c["B"], c["D"]))
+        for variant in ("auto",) + VEC_VARIANTS + ("generic",):
+            say("config2 seed", seed, variant)
+            assert np.array_equal(gpu_gemm(dev, c["A"], c["B"], c["D"], variant=variant), want)
+
+
+def test_config2_mutation_is_detected(dev):
+    """A planted mistake in the oracle (D dropped) must not match the GPU."""
+    c = inputs.config_inputs(2, seed=3)
+    got = gpu_gemm(dev, c["A"], c["B"], c["D"])
+    assert np.array_equal(got, go.gemm_i8(c["A"], c["B"], c["D"]))
+    assert not np.array_equal(got, go.gemm_i8(c["A"], c["B"]))          # D dropped
+    bad_tiles = go.gemm_i8_int64(c["A"][:, 16:], c["B"][16:, :], c["D"])  # first K tile lost
+    assert not np.array_equal(got, bad_tiles)
+
+
+def test_config3_batched_b_reuse(dev):
+    c = inputs.config_inputs(3, seed=0)
+    A, B = c["A"], c["B"]
+    want = go.gemm_i8_f64(A, B)
+    for variant in ("auto", "mfma_256x256", "mfma_128x128"):
+        say("config3", variant)
+        got = gpu_gemm(dev, A, B, variant=variant)
+        assert np.array_equal(got, want), variant
+
+
+@pytest.mark.parametrize("m", [1, 16])
+def test_config4_decode(dev, m):
+    c = inputs.config_inputs(4, seed=m, m=m)
+    want = go.gemm_i8_f64(c["A"], c["B"])
+    for ks in (0, 1, 2, 4, 7):
+        say("config4 m", m, "k_split", ks)
+        got = gpu_gemm(dev, c["A"], c["B"], variant="skinny", k_split=ks)
+        assert np.array_equal(got, want), ks
+    assert np.array_equal(gpu_gemm(dev, c["A"], c["B"]), want)
+
+
+def _exact_properties(A, B, C, rng, samples=48):
+    """Exact checks of C == A.B for large shapes (no int32 wrap in contract)."""
+    Af = A.astype(np.float64)
+    Bf = B.astype(np.float64)
+    Cf = C.astype(np.float64)
+    # row and column checksums (checksum of checksums)
+    assert np.array_equal(Cf.sum(axis=1), Af @ Bf.sum(axis=1))
+    assert np.array_equal(Cf.sum(axis=0), Af.sum(axis=0) @ Bf)
+    # Freivalds with random small-integer vectors (exact in float64)
+    for _ in range(2):
+        x = rng.integers(-3, 4, size=B.shape[1]).astype(np.float64)
+        assert np.array_equal(Cf @ x, Af @ (Bf @ x))
+    # full sampled rows and columns against the exact product
+    rows = rng.choice(A.shape[0], size=samples, replace=False)
+    cols = rng.choice(B.shape[1], size=samples, replace=False)
+    assert np.array_equal(C[rows], go.gemm_i8_f64(A[rows], B))
+    assert np.array_equal(C[:, cols], go.gemm_i8_f64(A, B[:, cols]))
+
+
+def test_config5_8192_adversarial(dev):
+    c = inputs.config_inputs(5, seed=0)
+    A, B = c["A"], c["B"]
+    assert np.count_nonzero((A == -128) | (A == 127)) > A.size * 0.45
+    say("config5 auto")
+    got = gpu_gemm(dev, A, B)
+    assert (got != INT32_MIN).all()
+    _exact_properties(A, B, got, np.random.default_rng(0))
+
+
+def test_extremes_at_the_overflow_edge(dev):
+    # all -128: every output is K*16384; at K=8192 that is 134217728 (< 2^31)
+    for (m, n, k) in ((256, 256, 8192), (16, 256, 8192), (300, 144, 4096)):
+        A = np.full((m, k), -128, np.int8)
+        B = np.full((k, n), -128, np.int8)
+        for variant in ("auto", "generic"):
+            say("extremes", m, n, k, variant)
+            got = gpu_gemm(dev, A, B, variant=variant)
+            assert (got == k * 16384).all()
+        A2 = np.where(np.arange(m * k).reshape(m, k) % 2 == 0, -128, 127).astype(np.int8)
+        B2 = np.where(np.arange(k * n).reshape(k, n) % 3 == 0, 127, -128).astype(np.int8)
+        assert np.array_equal(gpu_gemm(dev, A2, B2), go.gemm_i8_f64(A2, B2))
+
+
+# ---------------------------------------------------------------------------
+# Edge shapes, tails, strides, in-place and repeated calls
+# ---------------------------------------------------------------------------
+
+EDGE_SHAPES = [(1, 16, 16), (17, 48, 80), (129, 144, 64), (300, 272, 208), (255, 256, 320),
+               (257, 128, 1040), (33, 16, 4112), (512, 512, 64), (16, 14352, 4160),
+               (3, 2064, 1024), (640, 384, 48)]
+
+
+@pytest.mark.parametrize("shape", EDGE_SHAPES)
+def test_edge_shapes_all_variants(dev, shape):
+    m, n, k = shape
+    rng = np.random.default_rng(m * 7 + n * 3 + k)
+    A = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    B = rng.integers(-128, 128, (k, n), dtype=np.int8)
+    D = rng.integers(-(1 << 20), (1 << 20) + 1, (m, n), dtype=np.int32)
+    want = go.gemm_i8(A, B)
+    want_d = go.gemm_i8(A, B, D)
+    variants = ["auto", "generic"] + list(VEC_VARIANTS) + (["skinny"] if m <= 16 else [])
+    for variant in variants:
+        say("edge", shape, variant)
+        assert np.array_equal(gpu_gemm(dev, A, B, variant=variant), want), variant
+        assert np.array_equal(gpu_gemm(dev, A, B, D, variant=variant), want_d), variant
+
+
+def test_unaligned_shapes_use_generic(dev):
+    rng = np.random.default_rng(11)
+    for (m, n, k) in ((5, 7, 9), (33, 20, 50), (2, 3, 1)):
+        A = rng.integers(-128, 128, (m, k), dtype=np.int8)
+        B = rng.integers(-128, 128, (k, n), dtype=np.int8)
+        say("unaligned", m, n, k)
+        assert np.array_equal(gpu_gemm(dev, A, B), go.gemm_i8(A, B))
+        with pytest.raises(_lib.HipGemmError):
+            gpu_gemm(dev, A, B, variant="mfma_128x128")
+
+
+def test_strided_operands_and_inplace(dev):
+    rng = np.random.default_rng(5)
+    m, n, k = 200, 160, 96
+    lda, ldb, ldc = k + 32, n + 16, n + 48
+    Abuf = torch.from_numpy(rng.integers(-128, 128, (m, lda), dtype=np.int8)).to(dev)
+    Bbuf = torch.from_numpy(rng.integers(-128, 128, (k, ldb), dtype=np.int8)).to(dev)
+    D0 = rng.integers(-1000, 1000, (m, ldc), dtype=np.int32)
+    A = Abuf[:, :k].cpu().numpy()
+    B = Bbuf[:, :n].cpu().numpy()
+    want = go.gemm_i8(A, B, D0[:, :n])
+    for variant in ("auto", "mfma_128x128", "mfma_256x128", "generic"):
+        say("strided in-place", variant)
+        Cbuf = torch.from_numpy(D0.copy()).to(dev)
+        # in place: D and C are the same buffer
+        _lib.gemm_raw(Abuf.data_ptr(), Bbuf.data_ptr(), Cbuf.data_ptr(), Cbuf.data_ptr(),
+                      m, n, k, lda, ldb, ldc, ldc, variant=variant)
+        _lib.sync(None)
+        got = Cbuf.cpu().numpy()
+        assert np.array_equal(got[:, :n], want), variant
+        assert np.array_equal(got[:, n:], D0[:, n:]), variant   # padding untouched
+
+
+def test_batched_unshared_and_shared(dev):
+    rng = np.random.default_rng(9)
+    b, m, n, k = 5, 48, 144, 80
+    A = rng.integers(-128, 128, (b, m, k), dtype=np.int8)
+    Bs = rng.integers(-128, 128, (b, k, n), dtype=np.int8)
+    D = rng.integers(-50, 50, (b, m, n), dtype=np.int32)
+    for variant in ("auto", "mfma_128x128", "generic"):
+        say("batched", variant)
+        assert np.array_equal(gpu_gemm(dev, A, Bs, D, variant=variant), go.gemm_i8(A, Bs, D))
+        assert np.array_equal(gpu_gemm(dev, A, Bs[0], variant=variant), go.gemm_i8(A, Bs[0]))
+    A16 = A[:, :16, :]
+    assert np.array_equal(gpu_gemm(dev, np.ascontiguousarray(A16), Bs, variant="skinny", k_split=2),
+                          go.gemm_i8(A16, Bs))
+
+
+def test_skinny_repeated_calls_reset_counters(dev):
+    rng = np.random.default_rng(21)
+    for it in range(4):
+        m = (1, 16, 7, 16)[it]
+        A = rng.integers(-127, 128, (m, 2048), dtype=np.int8)
+        B = rng.integers(-128, 128, (2048, 4096), dtype=np.int8)
+        say("skinny repeat", it, m)
+        assert np.array_equal(gpu_gemm(dev, A, B, variant="skinny", k_split=4), go.gemm_i8(A, B))
+
+
+def test_backend_run_on_side_stream(dev):
+    rng = np.random.default_rng(2)
+    A = torch.from_numpy(rng.integers(-128, 128, (384, 256), dtype=np.int8)).to(dev)
+    B = torch.from_numpy(rng.integers(-128, 128, (256, 512), dtype=np.int8)).to(dev)
+    plan = hg.make_plan(384, 512, 256)
+    s = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(s):
+        C = hg.run(plan, A, B)
+    s.synchronize()
+    assert np.array_equal(C.cpu().numpy(), go.gemm_i8(A.cpu().numpy(), B.cpu().numpy()))
+    flat = hg.run_flat(hg.make_plan(16, 16, 16), [1] * 256, [-2] * 256)
+    assert flat == [-32] * 256
+
+
+def test_cpu_reference_agrees_on_gpu_box(dev):
+    """The C oracle built for this host agrees with the GPU on a mid-size case."""
+    rng = np.random.default_rng(4)
+    A = rng.integers(-128, 128, (96, 512), dtype=np.int8)
+    B = rng.integers(-128, 128, (512, 320), dtype=np.int8)
+    assert np.array_equal(gpu_gemm(dev, A, B), cref.gemm_i8(A, B, order="ikj"))

@@ -1,0 +1,154 @@
+"""ctypes binding of libvt_hip_gemm.so (declarations in include/vt_hip_gemm.h).
+
+The library path is veritac_amd/libvt_hip_gemm.so unless the VT_HIP_GEMM_LIB
+environment variable names another file (the analogue of the reference's
+VERITAC_GEMMINI_CHECK_BIN override, specializations/gemmini_gemm/
+backend.py:156-161). A missing or unloadable library raises HipGemmError:
+there is no fallback path.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+DEFAULT_LIB = os.path.join(PKG_DIR, "libvt_hip_gemm.so")
+ABI_VERSION = 1
+
+VT_OK = 0
+VT_EINVAL = -1
+VT_EUNSUPPORTED = -2
+VT_EHIP = -3
+VT_ENODEV = -4
+STATUS_NAMES = {VT_OK: "ok", VT_EINVAL: "invalid argument", VT_EUNSUPPORTED: "unsupported",
+                VT_EHIP: "HIP error", VT_ENODEV: "no gfx950 device"}
+
+# variant name -> id (include/vt_hip_gemm.h VT_VARIANT_*)
+VARIANT_IDS = {
+    "auto": 0,
+    "mfma_256x256": 1,
+    "mfma_128x128": 2,
+    "skinny": 3,
+    "generic": 4,
+    "mfma_256x128": 5,
+}
+VARIANTS = tuple(VARIANT_IDS)
+
+# Every function include/vt_hip_gemm.h declares.
+EXPORTS = ("vt_gemm_i8", "vt_gemm_select", "vt_variant_info", "vt_variant_name",
+           "vt_last_error", "vt_sync", "vt_device_count", "vt_abi_version")
+
+
+class HipGemmError(RuntimeError):
+    """Raised by the hip_gemm boundary on any refusal or device failure."""
+
+    def __init__(self, message, code=None):
+        super().__init__(message)
+        self.code = code
+
+
+_lock = threading.Lock()
+_lib = None
+
+
+def library_path():
+    return os.environ.get("VT_HIP_GEMM_LIB") or DEFAULT_LIB
+
+
+def _declare(lib):
+    i64, i32, p = ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p
+    pi32 = ctypes.POINTER(ctypes.c_int32)
+    lib.vt_gemm_i8.argtypes = [p, p, p, p, i64, i64, i64, i64, i64, i64, i64,
+                               i64, i64, i64, i64, i64, i32, i32, p]
+    lib.vt_gemm_i8.restype = ctypes.c_int
+    lib.vt_gemm_select.argtypes = [i64, i64, i64, i64, i64, i64, i32, pi32, pi32]
+    lib.vt_gemm_select.restype = ctypes.c_int
+    lib.vt_variant_info.argtypes = [i32, pi32, pi32, pi32, pi32, pi32]
+    lib.vt_variant_info.restype = ctypes.c_int
+    lib.vt_variant_name.argtypes = [i32]
+    lib.vt_variant_name.restype = ctypes.c_char_p
+    lib.vt_last_error.argtypes = []
+    lib.vt_last_error.restype = ctypes.c_char_p
+    lib.vt_sync.argtypes = [p]
+    lib.vt_sync.restype = ctypes.c_int
+    lib.vt_device_count.argtypes = []
+    lib.vt_device_count.restype = ctypes.c_int
+    lib.vt_abi_version.argtypes = []
+    lib.vt_abi_version.restype = ctypes.c_int
+
+
+def load_library():
+    """Load (once) and return the native library; raise HipGemmError if absent."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        path = library_path()
+        if not os.path.isfile(path):
+            raise HipGemmError("libvt_hip_gemm.so not found at %r (build it with "
+                               "`python -m veritac_amd.build`)" % path, VT_ENODEV)
+        try:
+            lib = ctypes.CDLL(path)
+        except OSError as exc:
+            raise HipGemmError("cannot load %r: %s" % (path, exc), VT_ENODEV) from exc
+        missing = [n for n in EXPORTS if not hasattr(lib, n)]
+        if missing:
+            raise HipGemmError("%r lacks symbols %s" % (path, missing), VT_ENODEV)
+        _declare(lib)
+        if lib.vt_abi_version() != ABI_VERSION:
+            raise HipGemmError("ABI version %d != %d" % (lib.vt_abi_version(), ABI_VERSION))
+        _lib = lib
+        return lib
+
+
+def last_error():
+    msg = load_library().vt_last_error()
+    return msg.decode() if msg else ""
+
+
+def check(status, what="vt_gemm_i8"):
+    if status != VT_OK:
+        raise HipGemmError("%s: %s (%s)" % (what, last_error(), STATUS_NAMES.get(status, status)),
+                           status)
+    return status
+
+
+def select_variant(m, n, k, batch=1, lda=None, ldb=None, aligned=True):
+    """(variant name, k_split) that VT_VARIANT_AUTO launches for this shape."""
+    lib = load_library()
+    v, ks = ctypes.c_int32(), ctypes.c_int32()
+    check(lib.vt_gemm_select(m, n, k, batch, k if lda is None else lda,
+                             n if ldb is None else ldb, int(bool(aligned)),
+                             ctypes.byref(v), ctypes.byref(ks)), "vt_gemm_select")
+    names = {i: nm for nm, i in VARIANT_IDS.items()}
+    return names[v.value], ks.value
+
+
+def variant_info(name):
+    """Static resources of a variant: tile_m, tile_n, tile_k, threads, lds_bytes."""
+    lib = load_library()
+    vals = [ctypes.c_int32() for _ in range(5)]
+    check(lib.vt_variant_info(VARIANT_IDS[name], *[ctypes.byref(v) for v in vals]),
+          "vt_variant_info")
+    return dict(zip(("tile_m", "tile_n", "tile_k", "threads", "lds_bytes"),
+                    (v.value for v in vals)))
+
+
+def device_count():
+    return load_library().vt_device_count()
+
+
+def gemm_raw(A_ptr, B_ptr, D_ptr, C_ptr, M, N, K, lda, ldb, ldd, ldc, batch=1,
+             stride_a=0, stride_b=0, stride_d=0, stride_c=0, variant="auto",
+             k_split=0, stream=None):
+    """One vt_gemm_i8 call on raw device pointers (integers); raises on failure."""
+    lib = load_library()
+    vid = VARIANT_IDS[variant] if isinstance(variant, str) else int(variant)
+    st = lib.vt_gemm_i8(A_ptr, B_ptr, D_ptr, C_ptr, M, N, K, lda, ldb, ldd, ldc, batch,
+                        stride_a, stride_b, stride_d, stride_c, vid, k_split, stream)
+    return check(st)
+
+
+def sync(stream=None):
+    return check(load_library().vt_sync(stream), "vt_sync")

@@ -1,0 +1,416 @@
+"""hip_gemm backend: plans, validation, candidates and execution of the exact
+int8 x int8 -> int32 GEMM on MI355X (gfx950).
+
+Same verbs and conventions as the reference's Gemmini backend
+(specializations/gemmini_gemm/backend.py):
+
+  make_plan / required_resources / validate_plan   backend.py:1064, :97, :107
+  gen_candidates / modeled_counts / modeled_objective / optimize
+                                                   backend.py:336, :346, :370, :1072
+  run (raises HipGemmError like run_commands raises GemminiError)
+                                                   backend.py:380, :433-562
+
+Conventions kept from the reference:
+  * validate_plan returns (ok, reason) and never raises on bad input;
+  * execution fails closed: an invalid plan, mismatched operands, a missing
+    native library or no gfx950 device raise HipGemmError -- there is no CPU
+    fallback;
+  * the native library path can be overridden with VT_HIP_GEMM_LIB
+    (cf. VERITAC_GEMMINI_CHECK_BIN, backend.py:156-161);
+  * modeled counts are analytic models for candidate ranking, never
+    measurements (backend.py:46-49).
+
+Plan schema (all ints strict, bools strict):
+  {"m", "n", "k", "batch", "dim", "b_shared", "has_d", "d_max_abs",
+   "variant", "k_split"}
+The contract extends the reference's full-tile DIM=16 GEMM: m may be any
+positive size (the decode shapes have m = 1), n and k must be multiples of
+DIM for the MFMA and skinny variants, and the overflow bound is
+k*16384 + d_max_abs <= 2^31-1 (Plan.lean:86-92 plus the initial partial sum).
+"""
+from __future__ import annotations
+
+import math
+
+from ... import _lib
+from ..._lib import HipGemmError
+
+DIM = 16
+ELEM_MIN, ELEM_MAX = -128, 127
+ACC_ELEMENT_MAX = 2**31 - 1
+INT8_DOMAIN_CONSTRAINT = "inputs are int8 in [-128,127] and k*16384 + |D| <= 2147483647"
+MAX_EXTENT = 2**40
+
+VARIANTS = ("mfma_256x256", "mfma_256x128", "mfma_128x128", "skinny", "generic")
+SUPPORTED_VARIANTS = ("auto",) + VARIANTS
+
+# variant -> (tile_m, tile_n, tile_k, threads, lds_bytes); mirrors the native
+# table returned by vt_variant_info (checked by the tests).
+TILES = {
+    "mfma_256x256": (256, 256, 64, 256, 2 * (256 * 64 + 64 * 256)),
+    "mfma_256x128": (256, 128, 64, 256, 2 * (256 * 64 + 64 * 128)),
+    "mfma_128x128": (128, 128, 64, 256, 2 * (128 * 64 + 64 * 128)),
+    "skinny": (16, 128, 64, 256, 2 * 64 * 128),
+    "generic": (4, 64, 1, 256, 0),
+}
+SKINNY_MAX_M = 16
+LDS_PER_CU = 160 * 1024
+
+# MI355X datasheet figures used by the analytic model and the rooflines.
+PEAK_INT8_OPS = 256 * 2.4e9 * 8192      # dense INT8 MFMA, ops/s (~5.03e15)
+PEAK_HBM_BYTES = 8.0e12                 # HBM3E, bytes/s
+NUM_CUS = 256
+
+_INT_FIELDS = ("m", "n", "k", "batch", "dim", "d_max_abs", "k_split")
+_BOOL_FIELDS = ("b_shared", "has_d")
+
+
+def _is_int(v):
+    return isinstance(v, int) and not isinstance(v, bool)
+
+
+# ---------------------------------------------------------------------------
+# Plans
+# ---------------------------------------------------------------------------
+
+def skinny_split(plan):
+    """(k_split, k_chunk) the skinny kernel launches for this plan.
+
+    Mirrors launch_skinny in csrc/vt_hip_gemm.hip: the requested split (or the
+    automatic one) is turned into 64-row-aligned slices that fit in LDS.
+    """
+    k, ks = plan["k"], plan["k_split"]
+    if ks <= 0:
+        ks = _auto_k_split(plan["n"], k, plan["batch"])
+    chunk = -(-k // ks)
+    chunk = -(-chunk // 64) * 64
+    lds = 16 * (chunk + 16) + TILES["skinny"][4]
+    limit = LDS_PER_CU - 256
+    if lds > limit:
+        chunk = ((limit - TILES["skinny"][4]) // 16 - 16) // 64 * 64
+    return -(-k // chunk), chunk
+
+
+def _auto_k_split(n, k, batch):
+    tiles = -(-n // TILES["skinny"][1]) * batch
+    ks = -(-512 // tiles)
+    ks = min(ks, max(k // 512, 1))
+    return max(1, min(ks, 64))
+
+
+def required_resources(plan):
+    """(lds_bytes per workgroup, workgroups) the plan's variant launches.
+
+    The analogue of backend.py:97-104 (scratchpad / accumulator rows) for a
+    gfx950 launch: LDS is the on-chip buffer a workgroup needs, workgroups
+    the grid size.
+    """
+    variant = plan["variant"]
+    tm, tn, _, _, lds = TILES[variant]
+    m, n, batch = plan["m"], plan["n"], plan["batch"]
+    if variant.startswith("mfma"):
+        if plan["b_shared"] and batch > 1:      # stacked-M fold
+            m, batch = m * batch, 1
+        return lds, -(-m // tm) * -(-n // tn) * batch
+    if variant == "skinny":
+        ks, chunk = skinny_split(plan)
+        return lds + 16 * (chunk + 16), -(-n // tn) * ks * batch
+    return 0, -(-n // tn) * min(-(-m // tm), 65535) * min(batch, 65535)
+
+
+def make_plan(m, n, k, *, batch=1, b_shared=False, has_d=False, d_max_abs=0,
+              variant="auto", k_split=0):
+    """A plan for C[batch] = D + A[batch].B; "auto" resolves the variant natively.
+
+    Mirrors backend.py:1064-1069. variant="auto" asks the native library
+    (vt_gemm_select) which kernel it would launch, so the plan records the
+    concrete variant and K split.
+    """
+    plan = {"m": m, "n": n, "k": k, "batch": batch, "dim": DIM,
+            "b_shared": bool(b_shared), "has_d": bool(has_d), "d_max_abs": d_max_abs,
+            "variant": variant, "k_split": k_split}
+    if variant == "auto":
+        ok, reason = validate_plan(dict(plan, variant="generic"))
+        if not ok:
+            raise HipGemmError("cannot plan: " + reason)
+        vec = n % DIM == 0 and k % DIM == 0
+        name, ks = _lib.select_variant(m, n, k, batch, k, n, vec)
+        plan["variant"] = name
+        if name == "skinny" and k_split == 0:
+            plan["k_split"] = ks
+    return plan
+
+
+def validate_plan(plan):
+    """Structural, divisibility, overflow and resource validation -> (ok, reason).
+
+    Mirrors backend.py:107-149: never raises, rejects bools and non-integers
+    for integer fields, checks the overflow bound and the buffer extents.
+    """
+    if not isinstance(plan, dict):
+        return False, "plan must be a JSON object"
+    for key in _INT_FIELDS:
+        if key not in plan or not _is_int(plan[key]):
+            return False, "plan field %r must be an integer" % key
+    for key in _BOOL_FIELDS:
+        if key not in plan or not isinstance(plan[key], bool):
+            return False, "plan field %r must be a boolean" % key
+    variant = plan.get("variant")
+    if variant not in VARIANTS:
+        return False, ("unsupported variant %r (supported: %s)" % (variant, list(VARIANTS)))
+    m, n, k, batch, dim = plan["m"], plan["n"], plan["k"], plan["batch"], plan["dim"]
+    if dim != DIM:
+        return False, "dim must equal DIM=%d (got %d)" % (DIM, dim)
+    for name, val in (("m", m), ("n", n), ("k", k), ("batch", batch)):
+        if val <= 0:
+            return False, "%s=%d must be positive" % (name, val)
+    if plan["d_max_abs"] < 0:
+        return False, "d_max_abs must be >= 0"
+    if not plan["has_d"] and plan["d_max_abs"] != 0:
+        return False, "d_max_abs must be 0 without an initial partial sum"
+    if plan["k_split"] < 0:
+        return False, "k_split must be >= 0"
+    bound = k * 16384 + plan["d_max_abs"]
+    if bound > ACC_ELEMENT_MAX:
+        return False, ("overflow bound violated: k*16384 + d_max_abs = %d > 2147483647 (%s)"
+                       % (bound, INT8_DOMAIN_CONSTRAINT))
+    if max(m, n, k) >= MAX_EXTENT or batch * max(m * n, m * k) >= 2**62:
+        return False, "buffer extent exceeds the supported indexing range"
+    if variant != "generic":
+        for name, val in (("n", n), ("k", k)):
+            if val % dim != 0:
+                return False, ("%s=%d must be divisible by dim=%d for variant %r"
+                               % (name, val, dim, variant))
+    if variant == "skinny":
+        if m > SKINNY_MAX_M:
+            return False, "variant 'skinny' needs m <= %d (got %d)" % (SKINNY_MAX_M, m)
+        if batch > 65535:
+            return False, "variant 'skinny' supports batch <= 65535"
+    elif variant != "generic" and plan["k_split"] != 0:
+        return False, "k_split applies to variant 'skinny' only"
+    lds, workgroups = required_resources(plan)
+    if lds > LDS_PER_CU:
+        return False, "LDS %d bytes > %d per CU" % (lds, LDS_PER_CU)
+    if workgroups > 2**31 - 1:
+        return False, "grid of %d workgroups exceeds the launch limit" % workgroups
+    return True, "ok"
+
+
+# ---------------------------------------------------------------------------
+# Analytic model (NOT a measurement)
+# ---------------------------------------------------------------------------
+
+# Fraction of the dense INT8 peak each variant is modeled at when compute-bound.
+_MODEL_MFMA_EFF = {"mfma_256x256": 0.70, "mfma_256x128": 0.60, "mfma_128x128": 0.45,
+                   "skinny": 0.25, "generic": 0.002}
+
+
+def algorithmic_bytes(plan):
+    """A once + B once (shared B counted once) + C written + D read."""
+    m, n, k, b = plan["m"], plan["n"], plan["k"], plan["batch"]
+    a_bytes = b * m * k
+    b_bytes = k * n if (plan["b_shared"] or b == 1) else b * k * n
+    c_bytes = 4 * b * m * n
+    d_bytes = c_bytes if plan["has_d"] else 0
+    return a_bytes + b_bytes + c_bytes + d_bytes
+
+
+def modeled_counts(plan):
+    """Analytic ops / bytes / workgroups for a valid plan (a model, not a measurement)."""
+    m, n, k, b = plan["m"], plan["n"], plan["k"], plan["batch"]
+    variant = plan["variant"]
+    tm, tn = TILES[variant][:2]
+    lds, wgs = required_resources(plan)
+    ops = 2 * b * m * n * k
+    alg = algorithmic_bytes(plan)
+    if variant.startswith("mfma"):
+        m_eff, b_eff = (m * b, 1) if (plan["b_shared"] and b > 1) else (m, b)
+        tiles_m, tiles_n = -(-m_eff // tm), -(-n // tn)
+        # every tile reads its A row-panel and B column-panel once
+        c_and_d = 4 * b * m * n * (2 if plan["has_d"] else 1)
+        l2_bytes = b_eff * (tiles_n * m_eff * k + tiles_m * k * n) + c_and_d
+    elif variant == "skinny":
+        ks, _ = skinny_split(plan)
+        partial = 2 * 4 * b * 16 * n * ks if ks > 1 else 0
+        l2_bytes = alg + partial + b * -(-n // tn) * 16 * k
+    else:
+        l2_bytes = b * (m * n * k + -(-m // 4) * n * k) + 4 * b * m * n
+    return {"ops": ops, "macs": ops // 2, "bytes_algorithmic": alg, "bytes_l2_modeled": l2_bytes,
+            "workgroups": wgs, "lds_bytes": lds,
+            "arithmetic_intensity": ops / alg if alg else math.inf}
+
+
+def modeled_objective(plan, counts):
+    """(modeled seconds, workgroups); least is best. A model, not a measurement.
+
+    Compute time prices the padded tile work (rows/columns a tile covers past
+    m and n still run MFMAs) at a per-variant fraction of the dense INT8 peak
+    with whole-chip wave quantisation; memory time prices the algorithmic
+    bytes at the HBM peak scaled down when the grid has fewer workgroups than
+    CUs to keep loads in flight.
+    """
+    m, n, k, b = plan["m"], plan["n"], plan["k"], plan["batch"]
+    variant = plan["variant"]
+    tm, tn = TILES[variant][:2]
+    if variant.startswith("mfma") and plan["b_shared"] and b > 1:
+        m, b = m * b, 1
+    padded_ops = 2 * b * (-(-m // tm) * tm) * (-(-n // tn) * tn) * k
+    wgs = counts["workgroups"]
+    waves = -(-wgs // NUM_CUS)
+    fill = wgs / (waves * NUM_CUS) if wgs else 1.0
+    eff = _MODEL_MFMA_EFF[variant] * (fill if variant.startswith("mfma") else 1.0)
+    t_compute = padded_ops / (PEAK_INT8_OPS * eff)
+    t_memory = counts["bytes_algorithmic"] / (PEAK_HBM_BYTES * min(1.0, wgs / NUM_CUS))
+    return (max(t_compute, t_memory), wgs)
+
+
+def gen_candidates(m, n, k, *, batch=1, b_shared=False, has_d=False, d_max_abs=0):
+    """One plan per variant (the reference's per-schedule plans, backend.py:1080-1082)."""
+    return [make_plan(m, n, k, batch=batch, b_shared=b_shared, has_d=has_d,
+                      d_max_abs=d_max_abs, variant=v) for v in VARIANTS]
+
+
+def optimize(m, n, k, *, batch=1, b_shared=False, has_d=False, d_max_abs=0,
+             measure=False, num_runs=10):
+    """Validate every variant, score it, pick the least modeled (or measured) time.
+
+    Mirrors backend.py:1072-1093: returns {"candidates": [...], "winner": plan}
+    with one entry per variant {plan, valid, invalid_reason, counts, objective}.
+    With measure=True the valid candidates are also timed on the GPU
+    (runner.benchmark_gemm) and the winner is the fastest measured one; the
+    modeled objective is kept alongside.
+    """
+    candidates = []
+    for plan in gen_candidates(m, n, k, batch=batch, b_shared=b_shared, has_d=has_d,
+                               d_max_abs=d_max_abs):
+        ok, reason = validate_plan(plan)
+        entry = {"plan": plan, "valid": ok, "invalid_reason": None if ok else reason,
+                 "counts": None, "objective": None, "measured_ms": None}
+        if ok:
+            counts = modeled_counts(plan)
+            entry["counts"] = counts
+            entry["objective"] = modeled_objective(plan, counts)
+        candidates.append(entry)
+    eligible = [c for c in candidates if c["valid"]]
+    if measure and eligible:
+        from . import runner
+        for c in eligible:
+            res = runner.benchmark_gemm(c["plan"], num_runs=num_runs, warmup=2, rotate=False)
+            c["measured_ms"] = res["gpu_time_ms"]
+        winner = min(eligible, key=lambda c: c["measured_ms"])["plan"]
+    else:
+        winner = min(eligible, key=lambda c: c["objective"])["plan"] if eligible else None
+    return {"candidates": candidates, "winner": winner}
+
+
+# ---------------------------------------------------------------------------
+# Execution
+# ---------------------------------------------------------------------------
+
+def _torch():
+    import torch
+    return torch
+
+
+def _operand_shapes(plan):
+    m, n, k, b = plan["m"], plan["n"], plan["k"], plan["batch"]
+    a = (m, k) if b == 1 else (b, m, k)
+    bb = (k, n) if (b == 1 or plan["b_shared"]) else (b, k, n)
+    c = (m, n) if b == 1 else (b, m, n)
+    return a, bb, c
+
+
+def _check_tensor(name, t, shape, dtype, device):
+    torch = _torch()
+    if not isinstance(t, torch.Tensor):
+        raise HipGemmError("%s must be a torch tensor" % name)
+    if t.dtype != dtype:
+        raise HipGemmError("%s must be %s (got %s)" % (name, dtype, t.dtype))
+    if tuple(t.shape) != tuple(shape):
+        raise HipGemmError("%s has shape %s, plan needs %s" % (name, tuple(t.shape), tuple(shape)))
+    if t.device != device:
+        raise HipGemmError("%s is on %s, expected %s" % (name, t.device, device))
+    if t.dim() and t.stride(-1) != 1:
+        raise HipGemmError("%s must have unit stride in its last dimension" % name)
+
+
+def native_runner(plan, A, B, D, C, stream):
+    """Default device runner: one vt_gemm_i8 call through the C ABI."""
+    m, n, k, b = plan["m"], plan["n"], plan["k"], plan["batch"]
+    lda = A.stride(-2)
+    ldb = B.stride(-2)
+    ldc = C.stride(-2)
+    ldd = D.stride(-2) if D is not None else n
+    sa = A.stride(0) if b > 1 else 0
+    sb = B.stride(0) if (b > 1 and B.dim() == 3) else 0
+    sc = C.stride(0) if b > 1 else 0
+    sd = D.stride(0) if (D is not None and b > 1) else 0
+    _lib.gemm_raw(A.data_ptr(), B.data_ptr(), D.data_ptr() if D is not None else None,
+                  C.data_ptr(), m, n, k, lda, ldb, ldd, ldc, b, sa, sb, sd, sc,
+                  plan["variant"], plan["k_split"], stream)
+
+
+def run(plan, A, B, D=None, *, out=None, stream=None, runner=None):
+    """C = D + A.B on the GPU for device tensors; returns C (int32).
+
+    Fails closed like run_commands (backend.py:433-445): the plan is
+    validated first and any mismatch raises HipGemmError before a kernel is
+    launched. `runner` (plan, A, B, D, C, stream) replaces the native call
+    (dependency injection for host-only tests); `stream` is a raw hipStream_t
+    handle, default torch's current stream.
+    """
+    ok, reason = validate_plan(plan)
+    if not ok:
+        raise HipGemmError("invalid plan: " + reason)
+    torch = _torch()
+    if not isinstance(A, torch.Tensor):
+        raise HipGemmError("A must be a torch tensor")
+    device = A.device
+    a_shape, b_shape, c_shape = _operand_shapes(plan)
+    _check_tensor("A", A, a_shape, torch.int8, device)
+    _check_tensor("B", B, b_shape, torch.int8, device)
+    if plan["has_d"]:
+        if D is None:
+            raise HipGemmError("plan has_d=True but D is None")
+        _check_tensor("D", D, c_shape, torch.int32, device)
+    elif D is not None:
+        raise HipGemmError("plan has_d=False but D was given")
+    if out is None:
+        out = torch.empty(c_shape, dtype=torch.int32, device=device)
+    else:
+        _check_tensor("out", out, c_shape, torch.int32, device)
+    if runner is None:
+        if device.type != "cuda":
+            raise HipGemmError("operands must be on a gfx950 GPU (got %s); hip_gemm has "
+                               "no CPU path" % device)
+        runner = native_runner
+        if stream is None:
+            with torch.cuda.device(device):
+                stream = torch.cuda.current_stream(device).cuda_stream
+    runner(plan, A, B, D, out, stream)
+    return out
+
+
+def run_flat(plan, A, B, D=None):
+    """Flat-list form of run (the reference's ownership convention,
+    backend.py:394 / :562): int lists in, a fresh int list out."""
+    torch = _torch()
+    import numpy as np
+    a_shape, b_shape, c_shape = _operand_shapes(plan)
+    for name, vals, n in (("A", A, math.prod(a_shape)), ("B", B, math.prod(b_shape))):
+        if len(vals) != n:
+            raise HipGemmError("%s has %d values, plan needs %d" % (name, len(vals), n))
+        for v in vals:
+            if not _is_int(v) or not ELEM_MIN <= v <= ELEM_MAX:
+                raise HipGemmError("int8 input out of [-128,127]: %r" % (v,))
+    dev = torch.device("cuda", torch.cuda.current_device()) if torch.cuda.is_available() else None
+    if dev is None:
+        raise HipGemmError("no GPU available: hip_gemm has no CPU path")
+    At = torch.from_numpy(np.asarray(A, dtype=np.int8).reshape(a_shape)).to(dev)
+    Bt = torch.from_numpy(np.asarray(B, dtype=np.int8).reshape(b_shape)).to(dev)
+    Dt = None
+    if D is not None:
+        Dt = torch.from_numpy(np.asarray(D, dtype=np.int32).reshape(c_shape)).to(dev)
+    C = run(plan, At, Bt, Dt)
+    torch.cuda.synchronize(dev)
+    return C.cpu().reshape(-1).tolist()
