@@ -162,6 +162,25 @@ def bench_decode(dev, steps, warmup):
     }
 
 
+def bench_copy(dev, steps, warmup):
+    """A plain 1 GiB device-to-device copy (torch's copy kernel): the known
+    byte count against which the profiler's FETCH_SIZE / WRITE_SIZE are scaled."""
+    import torch
+    n = 1 << 30
+    src = torch.ones(n, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(warmup):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    return {"workload": "copy 1 GiB", "bytes_read": n, "bytes_written": n,
+            "ms_per_copy": dt * 1e3, "gbps_read_plus_write": 2 * n / dt / 1e9}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -170,6 +189,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode-shape figure")
     ap.add_argument("--variant", default="auto", help="kernel variant for the headline GEMM")
+    ap.add_argument("--workload", choices=("all", "gemm", "decode", "copy"), default="all",
+                    help="all: the JSON line below; gemm / decode: only that kernel (for "
+                         "profiler runs); copy: a plain 1 GiB device copy (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -183,6 +205,12 @@ def main():
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.workload == "copy":
+        print(json.dumps(bench_copy(dev, args.steps, args.warmup)), flush=True)
+        return
+    if args.workload == "decode":
+        print(json.dumps(bench_decode(dev, args.steps, args.warmup)), flush=True)
+        return
     log("generating config 5 inputs")
     c = inputs.config_inputs(5, seed=0)
     M = N = K = 8192
@@ -226,6 +254,9 @@ def main():
     }
     del sets
     torch.cuda.empty_cache()
+    if args.workload == "gemm":
+        print(json.dumps(result), flush=True)
+        sys.exit(0 if parity_ok else 1)
     if not args.no_decode:
         log("decode shape")
         result["secondary"] = bench_decode(dev, max(args.steps, 100), args.warmup)

@@ -100,10 +100,13 @@ def test_modeled_counts_are_consistent():
 def test_skinny_split_mirrors_native_rule():
     p = hg.make_plan(16, 14336, 4096, variant="skinny")
     ks, chunk = hg.skinny_split(p)
-    assert chunk % 64 == 0 and ks * chunk >= 4096 and (ks - 1) * chunk < 4096
-    p1 = dict(p, k_split=1)
-    ks1, chunk1 = hg.skinny_split(p1)
-    assert ks1 == 1 and chunk1 == 4096
+    assert (ks, chunk) == (1, 4096)          # 224 column slabs fill the chip
+    for req in (2, 3, 4, 7):
+        ks, chunk = hg.skinny_split(dict(p, k_split=req))
+        assert chunk % hg.SKINNY_PIPE_ROWS == 0 and ks * chunk >= 4096 and (ks - 1) * chunk < 4096
+    p = hg.make_plan(16, 2048, 8192, variant="skinny")    # 32 slabs: split K
+    ks, chunk = hg.skinny_split(p)
+    assert ks == 8 and chunk == 1024
     lds, wgs = hg.required_resources(dict(p, k=131056, k_split=1))
     assert lds <= hg.LDS_PER_CU
 

@@ -86,18 +86,25 @@ __device__ __forceinline__ int32_t add_wrap(int32_t a, int32_t b) {
   return (int32_t)((uint32_t)a + (uint32_t)b);
 }
 
-// Swizzle of the 16-byte chunk index of a row-major [k][n] B slice with
-// `chunks` 16-byte chunks per row: keeps the 8 rows one ds_read_b64_tr_b8
-// touches in 8 distinct 16-byte bank groups.
+// LDS swizzles. gfx950's LDS serves 256 bytes per cycle (64 banks of 4 bytes):
+// 16 lanes of a 16-byte access or 32 lanes of an 8-byte access. The swizzles
+// below keep every such group on distinct banks, and also every half group
+// (the 128-byte case), for the access patterns of the kernels:
+//   A slice [m][64 B], ds_read_b128 of one 16-byte chunk from 16 consecutive
+//     rows: chunk c of row r is stored at c ^ (((r >> 1) ^ (r >> 3)) & 3);
+//   B slice [k][n], ds_read_b64_tr_b8 of 8 consecutive rows by 16 lanes, two
+//     16-lane groups reading adjacent chunks (c, c ^ 1) of the same rows:
+//     chunk c of row r is stored at c ^ b_swz(r).
 template <int CHUNKS>
 __device__ __forceinline__ int b_swz(int row) {
   static_assert(CHUNKS >= 4, "B slice needs at least 4 chunks per row");
-  return CHUNKS >= 8 ? (row & 7) : ((row >> 1) & 3);
+  if (CHUNKS >= 16) return ((row & 7) << 1) | ((row >> 2) & 1);
+  if (CHUNKS == 8) return row & 7;
+  return (row >> 1) & 3;
 }
 
-// A slice [m][64 bytes]: chunk c of row r lives at c ^ ((r >> 1) & 3).
 __device__ __forceinline__ int a_off(int row, int c) {
-  return row * 64 + ((c ^ ((row >> 1) & 3)) << 4);
+  return row * 64 + ((c ^ (((row >> 1) ^ (row >> 3)) & 3)) << 4);
 }
 
 // ---------------------------------------------------------------------------
@@ -126,9 +133,10 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma_kernel(GemmArgs p) {
   constexpr int A_BYTES = BM * BK, B_BYTES = BK * BN;
   static_assert(CA >= 1 && CB >= 1 && BCH >= 8, "tile too small");
 
-  __shared__ __attribute__((aligned(16))) int8_t smem[2 * (A_BYTES + B_BYTES)];
+  constexpr int NBUF = 3;                     // LDS slice buffers
+  __shared__ __attribute__((aligned(16))) int8_t smem[NBUF * (A_BYTES + B_BYTES)];
   int8_t *const As0 = smem;                  // A slice buffer b at As0 + b*A_BYTES
-  int8_t *const Bs0 = smem + 2 * A_BYTES;    // B slice buffer b at Bs0 + b*B_BYTES
+  int8_t *const Bs0 = smem + NBUF * A_BYTES; // B slice buffer b at Bs0 + b*B_BYTES
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -156,48 +164,60 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma_kernel(GemmArgs p) {
   const int8_t *Ab = p.A + bidx * p.sa;
   const int8_t *Bb = p.B + bidx * p.sb;
 
-  // Per-thread global source addresses for one 64-deep k slice.
-  const int8_t *a_src[CA];
+  // Per-thread global source offsets for one 64-deep k slice, relative to a
+  // wave-uniform base that advances by one slice per step (the host checks
+  // that every offset fits in 32 bits).
+  uint32_t a_goff[CA];
   int a_lds[CA], a_k[CA];
 #pragma unroll
   for (int i = 0; i < CA; ++i) {
     const int row = (tid >> 2) + 64 * i, c = tid & 3;
     int grow = m0 + row;
     if (EDGE) grow = min(grow, M - 1);
-    a_src[i] = Ab + (int64_t)grow * p.lda + c * 16;
+    a_goff[i] = (uint32_t)((int64_t)grow * p.lda + c * 16);
     a_lds[i] = a_off(row, c);
     a_k[i] = c * 16;
   }
-  int b_row[CB], b_col[CB], b_lds[CB];
+  int b_row[CB], b_lds[CB];
+  uint32_t b_goff[CB];
 #pragma unroll
   for (int i = 0; i < CB; ++i) {
     const int row = tid / BCH + (256 / BCH) * i, c = tid % BCH;
     int col = n0 + c * 16;
     if (EDGE) col = min(col, N - 16);
     b_row[i] = row;
-    b_col[i] = col;
+    b_goff[i] = (uint32_t)((int64_t)row * p.ldb + col);
     b_lds[i] = row * BN + ((c ^ b_swz<BCH>(row)) << 4);
   }
 
-  v4i ra[CA], rb[CB];
-  auto load_slice = [&](int kt) {
-    const int k0 = kt * BK;
+  const int KT = (K + BK - 1) / BK;
+  // Global -> VGPR staging of k slice kt into (ra, rb). Slices past the last
+  // one re-read the last slice (L2-resident); on the edge path their A part
+  // is zero, so a padding step computes nothing, and elsewhere they are never
+  // computed. The main loop thus has no data-dependent branches.
+  auto load_slice = [&](int kt, v4i *ra, v4i *rb) {
+    const int k0 = min(kt, KT - 1) * BK;
+    const int8_t *abase = Ab + k0;
+    const int8_t *bbase = Bb + (int64_t)k0 * p.ldb;
 #pragma unroll
     for (int i = 0; i < CA; ++i) {
-      if (EDGE && k0 + a_k[i] >= K) {
+      if (EDGE && kt * BK + a_k[i] >= K) {
         ra[i] = v4i{0, 0, 0, 0};
       } else {
-        ra[i] = *(const v4i *)(a_src[i] + k0);
+        ra[i] = *(const v4i *)(abase + a_goff[i]);
       }
     }
 #pragma unroll
     for (int i = 0; i < CB; ++i) {
-      int krow = k0 + b_row[i];
-      if (EDGE) krow = min(krow, K - 1);
-      rb[i] = *(const v4i *)(Bb + (int64_t)krow * p.ldb + b_col[i]);
+      if (EDGE && k0 + b_row[i] >= K) {
+        // rows past K: re-read row K-1 (A is zero there)
+        rb[i] = *(const v4i *)(Bb + (int64_t)(K - 1 - b_row[i]) * p.ldb + b_goff[i]);
+      } else {
+        rb[i] = *(const v4i *)(bbase + b_goff[i]);
+      }
     }
   };
-  auto store_slice = [&](int buf) {
+  auto store_slice = [&](int buf, const v4i *ra, const v4i *rb) {
 #pragma unroll
     for (int i = 0; i < CA; ++i) st_lds_b128(As0 + buf * A_BYTES, a_lds[i], ra[i]);
 #pragma unroll
@@ -232,34 +252,86 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma_kernel(GemmArgs p) {
       b_frag[ks][ni] = r0 * BN + ((nc ^ b_swz<BCH>(r0)) << 4) + (j & 1) * 8;
     }
 
-  const int KT = (K + BK - 1) / BK;
-  load_slice(0);
-  store_slice(0);
-  lds_barrier();
-  for (int kt = 0; kt < KT; ++kt) {
-    const int cur = kt & 1;
-    const int8_t *As = As0 + cur * A_BYTES;
-    const int8_t *Bs = Bs0 + cur * B_BYTES;
-    if (kt + 1 < KT) load_slice(kt + 1);
+  // Fragments of one 32-deep k step: MI A blocks and NI B blocks.
+  v4i fa0[MI], fb0[NI], fa1[MI], fb1[NI];
+  auto read_frags = [&](int buf, int ks, v4i *fa, v4i *fb) {
+    const int8_t *As = As0 + buf * A_BYTES;
+    const int8_t *Bs = Bs0 + buf * B_BYTES;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      v4i a[MI], b[NI];
+    for (int mi = 0; mi < MI; ++mi) fa[mi] = ld_lds_b128(As, a_frag[ks][mi]);
 #pragma unroll
-      for (int mi = 0; mi < MI; ++mi) a[mi] = ld_lds_b128(As, a_frag[ks][mi]);
-#pragma unroll
-      for (int ni = 0; ni < NI; ++ni) {
-        const v2i lo = ld_lds_tr8(Bs, b_frag[ks][ni]);
-        const v2i hi = ld_lds_tr8(Bs, b_frag[ks][ni] + 8 * BN);
-        b[ni] = v4i{lo.x, lo.y, hi.x, hi.y};
-      }
-#pragma unroll
-      for (int mi = 0; mi < MI; ++mi)
-#pragma unroll
-        for (int ni = 0; ni < NI; ++ni)
-          acc[mi][ni] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[mi], b[ni], acc[mi][ni], 0, 0, 0);
+    for (int ni = 0; ni < NI; ++ni) {
+      const v2i lo = ld_lds_tr8(Bs, b_frag[ks][ni]);
+      const v2i hi = ld_lds_tr8(Bs, b_frag[ks][ni] + 8 * BN);
+      fb[ni] = v4i{lo.x, lo.y, hi.x, hi.y};
     }
-    if (kt + 1 < KT) store_slice(cur ^ 1);
+  };
+  auto mfma_block = [&](const v4i *fa, const v4i *fb) {
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < NI; ++ni)
+        acc[mi][ni] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[mi], fb[ni], acc[mi][ni], 0, 0, 0);
+  };
+
+  // Pipeline over three LDS buffers and two VGPR staging sets. Step kt
+  // computes slice kt from buffer kt%3 while slice kt+2 goes VGPR -> LDS and
+  // slice kt+4 goes global -> VGPR, so a global load has two steps to land.
+  // Slice kt+1 was completed before the previous barrier, so its first
+  // fragments are read before this step's barrier and the MFMA pipe does not
+  // wait on LDS latency across steps. The single barrier per step also
+  // guarantees every wave has finished reading buffer kt%3 before step kt+1
+  // overwrites it with slice kt+3.
+  v4i ra0[CA], rb0[CB], ra1[CA], rb1[CB];
+  load_slice(0, ra0, rb0);
+  store_slice(0, ra0, rb0);
+  load_slice(1, ra1, rb1);
+  store_slice(1, ra1, rb1);
+  load_slice(2, ra0, rb0);
+  load_slice(3, ra1, rb1);
+  lds_barrier();
+  read_frags(0, 0, fa0, fb0);
+  int b0 = 0, b1 = 1, b2 = 2;   // buffers of slices kt, kt+1, kt+2
+  constexpr int NMFMA = MI * NI, NREAD = MI + 2 * NI, NSTORE = CA + CB;
+  auto step = [&](int kt, v4i *ra, v4i *rb) {
+    // First half step: fragments of k 32..63 load under the MFMAs of k 0..31.
+    read_frags(b0, 1, fa1, fb1);
+    mfma_block(fa0, fb0);
+#pragma unroll
+    for (int i = 0; i < NMFMA; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                   // MFMA
+      if (2 * i < NREAD) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // Second half step: slice kt+2 to LDS, slice kt+4 from memory and the
+    // next step's first fragments, interleaved with the MFMAs of k 32..63.
+    store_slice(b2, ra, rb);
+    load_slice(kt + 4, ra, rb);
+    read_frags(b1, 0, fa0, fb0);
+    mfma_block(fa1, fb1);
+#pragma unroll
+    for (int i = 0; i < NMFMA; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);                   // MFMA
+      if (i < NSTORE) {
+        __builtin_amdgcn_sched_group_barrier(0x200, 1, 1);                 // DS write
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 1);                 // VMEM read
+      } else if (2 * (i - NSTORE) < NREAD) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);                 // DS read
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
     lds_barrier();
+    const int bt = b0;
+    b0 = b1;
+    b1 = b2;
+    b2 = bt;
+  };
+  // Two steps per iteration (one per staging set). An odd step count only
+  // occurs on the edge path (the host routes K % 128 != 0 there), where the
+  // padding step multiplies zero A columns.
+  for (int kt = 0; kt < KT; kt += 2) {
+    step(kt, ra0, rb0);
+    step(kt + 1, ra1, rb1);
   }
 
   // Epilogue. 32x32 accumulator layout: element e of lane l is
@@ -284,7 +356,7 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma_kernel(GemmArgs p) {
 }
 
 // ---------------------------------------------------------------------------
-// Skinny (decode) kernel: M <= 16
+// Skinny (decode) kernels: M <= 16
 // ---------------------------------------------------------------------------
 
 struct SkinnyArgs {
@@ -296,66 +368,72 @@ struct SkinnyArgs {
   int64_t sa, sb, sd, sc;
   int M, N, K;
   int tiles_n;     // ceil(N / NB)
-  int k_split;     // K slices per column slab
-  int k_chunk;     // rows per slice (multiple of 64)
-  int32_t *ws;     // [batch][k_split][16][N] partials (k_split > 1)
-  int *counters;   // [batch][tiles_n] arrival counters, zero between launches
+  int k_split;     // K slices per column slab (workgroups along K)
+  int k_chunk;     // rows per slice, a multiple of the stage rows x U
+  int32_t *ws;     // [batch][k_split][M][N] partials when k_split > 1
 };
 
-constexpr int SKINNY_U = 8;   // 64-row B slices in flight per thread
-
-template <int NB, bool HAS_D>
-__global__ __launch_bounds__(256) void skinny_kernel(SkinnyArgs p) {
-  constexpr int BCH = NB / 16;          // 16-byte chunks per B row (= n-blocks)
-  constexpr int CB = 64 * BCH / 256;    // B chunks per thread per slice
-  constexpr int NBW = BCH / 4;          // n-blocks per wave
-  constexpr int U = SKINNY_U;
-  static_assert(CB >= 1 && NBW >= 1, "NB must be >= 64");
+// One workgroup = WAVES waves streams an NB-column slab of B over one K slice.
+// Every thread moves one 16-byte chunk per stage, so a stage is R = WAVES*1024/NB
+// rows; U stages are in flight in registers. Within a stage, wave w multiplies
+// the 64-row k-block w / (NB/16) against n-block w % (NB/16) with one
+// v_mfma_i32_16x16x64_i8 (M padded to 16 by zero rows of the LDS-resident A
+// slice). At the end the R/64 waves that share an n-block are summed through LDS.
+template <int NB, int WAVES, int U, bool HAS_D>
+__global__ __launch_bounds__(64 * WAVES) void skinny_kernel(SkinnyArgs p) {
+  constexpr int THREADS = 64 * WAVES;
+  constexpr int NBLK = NB / 16;               // 16-column blocks = chunks per row
+  constexpr int R = THREADS * 16 / NB;        // rows per stage
+  constexpr int KB = R / 64;                  // 64-row k-blocks per stage
+  constexpr int STAGE_BYTES = R * NB;
+  static_assert(KB * NBLK == WAVES && R % 64 == 0, "one MFMA per wave per stage");
 
   extern __shared__ __attribute__((aligned(16))) int8_t dsmem[];
-  const int a_stride = p.k_chunk + 16;  // +16 bytes: rows land in distinct banks
-  int8_t *As = dsmem;
-  int8_t *const Bs0 = dsmem + 16 * a_stride;   // B slice buffer b at Bs0 + b*64*NB
+  const int a_stride = p.k_chunk + 16;        // +16 bytes: rows land in distinct banks
+  int8_t *const As = dsmem;
+  int8_t *const Bs0 = dsmem + 16 * a_stride;  // stage buffer b at Bs0 + b*STAGE_BYTES
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int tile = blockIdx.x / p.k_split;
-  const int split = blockIdx.x - tile * p.k_split;
+  // XCD-aware order: workgroup w runs on XCD w % 8; give each XCD a contiguous
+  // range of (split, slab) indices so slabs that share 128-byte lines of a B
+  // row are fetched into the same L2.
+  const int total = gridDim.x;
+  const int w = blockIdx.x;
+  const int q = total >> 3, r = total & 7, x = w & 7;
+  const int wl = x * q + (x < r ? x : r) + (w >> 3);
+  const int tile = wl % p.tiles_n;
+  const int split = wl / p.tiles_n;
   const int bidx = blockIdx.y;
   const int n0 = tile * NB;
   const int M = p.M, N = p.N, K = p.K;
   const int kbeg = split * p.k_chunk;
-  const int klen = min(p.k_chunk, K - kbeg);   // > 0 by construction
-  const int T = (klen + 63) / 64;
-
+  // Every slice runs k_chunk/R stages (a multiple of U); rows past K read
+  // clamped B rows against zero A columns, so the loop has no data-dependent
+  // branches and the compiler keeps U stages of loads in flight.
+  const int T = p.k_chunk / R;
   const int8_t *Ab = p.A + bidx * p.sa;
   const int8_t *Bb = p.B + bidx * p.sb;
 
-  // B slice addressing (row-major [64][NB] per slice).
-  int b_row[CB], b_col[CB], b_lds[CB];
-#pragma unroll
-  for (int i = 0; i < CB; ++i) {
-    const int row = tid / BCH + (256 / BCH) * i, c = tid % BCH;
-    b_row[i] = row;
-    b_col[i] = min(n0 + c * 16, N - 16);
-    b_lds[i] = row * NB + ((c ^ b_swz<BCH>(row)) << 4);
-  }
-  v4i rb[U][CB];
-  auto load_slice = [&](int s, v4i *dst) {
-#pragma unroll
-    for (int i = 0; i < CB; ++i) {
-      const int krow = min(kbeg + s * 64 + b_row[i], K - 1);
-      dst[i] = *(const v4i *)(Bb + (int64_t)krow * p.ldb + b_col[i]);
-    }
+  const int brow = tid / NBLK, bc = tid % NBLK;
+  const int8_t *bsrc = Bb + min(n0 + bc * 16, N - 16);
+  const int b_lds = brow * NB + ((bc ^ b_swz<NBLK>(brow)) << 4);
+  // Loads for stages >= T (issued by the last U stages) re-read the slice's
+  // last row, which is resident in L2, and are discarded.
+  const int krow_last = min(kbeg + p.k_chunk - 1, K - 1);
+  // B is streamed exactly once: non-temporal loads keep it from displacing
+  // the L2-resident A slice and workspace.
+  auto load_stage = [&](int s) -> v4i {
+    const int krow = min(kbeg + s * R + brow, krow_last);
+    return __builtin_nontemporal_load((const v4i *)(bsrc + (int64_t)krow * p.ldb));
   };
-  // Put the first U slices in flight before touching A.
+  v4i rb[U];
 #pragma unroll
-  for (int u = 0; u < U; ++u)
-    if (u < T) load_slice(u, rb[u]);
+  for (int u = 0; u < U; ++u) rb[u] = load_stage(u);
 
   // A slice -> LDS, [16][k_chunk] with zero rows past M and zero k past K.
   {
-    const int cpr = p.k_chunk / 16;   // chunks per row
-    for (int i = tid; i < 16 * cpr; i += 256) {
+    const int cpr = p.k_chunk / 16;
+    for (int i = tid; i < 16 * cpr; i += THREADS) {
       const int row = i / cpr, c = i - row * cpr;
       const int k = kbeg + c * 16;
       v4i v = v4i{0, 0, 0, 0};
@@ -365,103 +443,94 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkinnyArgs p) {
   }
 
   const int g = lane >> 4, j = lane & 15;
-  int b_frag[NBW];
-#pragma unroll
-  for (int nb = 0; nb < NBW; ++nb) {
-    const int cc = wave * NBW + nb;
-    const int r0 = g * 16 + (j >> 1);
-    b_frag[nb] = r0 * NB + ((cc ^ b_swz<BCH>(r0)) << 4) + (j & 1) * 8;
-  }
-  const int a_frag = (lane & 15) * a_stride + g * 16;
+  const int nblk = wave % NBLK, kb = wave / NBLK;
+  const int r0 = kb * 64 + g * 16 + (j >> 1);
+  const int b_frag = r0 * NB + ((nblk ^ b_swz<NBLK>(r0)) << 4) + (j & 1) * 8;
+  const int a_frag = (lane & 15) * a_stride + kb * 64 + g * 16;
 
-  v4i acc[NBW];
-#pragma unroll
-  for (int nb = 0; nb < NBW; ++nb) acc[nb] = v4i{0, 0, 0, 0};
-
+  v4i acc = v4i{0, 0, 0, 0};
   for (int t0 = 0; t0 < T; t0 += U) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int s = t0 + u;
-      if (s < T) {
-        int8_t *const Bs = Bs0 + (s & 1) * (64 * NB);
-#pragma unroll
-        for (int i = 0; i < CB; ++i) st_lds_b128(Bs, b_lds[i], rb[u][i]);
-        if (s + U < T) load_slice(s + U, rb[u]);
-        lds_barrier();
-        const v4i a = ld_lds_b128(As, a_frag + s * 64);
-#pragma unroll
-        for (int nb = 0; nb < NBW; ++nb) {
-          const v2i lo = ld_lds_tr8(Bs, b_frag[nb]);
-          const v2i hi = ld_lds_tr8(Bs, b_frag[nb] + 8 * NB);
-          const v4i b = v4i{lo.x, lo.y, hi.x, hi.y};
-          acc[nb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc[nb], 0, 0, 0);
-        }
-      }
+      int8_t *const Bs = Bs0 + (u & 1) * STAGE_BYTES;
+      st_lds_b128(Bs, b_lds, rb[u]);
+      rb[u] = load_stage(s + U);
+      lds_barrier();
+      const v4i a = ld_lds_b128(As, a_frag + s * R);
+      const v2i lo = ld_lds_tr8(Bs, b_frag);
+      const v2i hi = ld_lds_tr8(Bs, b_frag + 8 * NB);
+      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, v4i{lo.x, lo.y, hi.x, hi.y}, acc, 0, 0, 0);
     }
   }
 
-  // 16x16 accumulator layout: element e of lane l is row 4*(l/16) + e,
-  // column l%16.
-  const int32_t *Db = HAS_D ? p.D + bidx * p.sd : nullptr;
-  int32_t *Cb = p.C + bidx * p.sc;
+  // Sum the KB partials of each n-block through LDS (stage buffers are free
+  // after the barrier). 16x16 accumulator layout: element e of lane l is
+  // row 4*(l/16) + e, column l%16.
+  int32_t *red = (int32_t *)Bs0;
+  lds_barrier();
+  *(LDS_AS v4i *)((LDS_AS int32_t *)red + (wave * 64 + lane) * 4) = acc;
+  lds_barrier();
+  if (kb != 0) return;
+#pragma unroll
+  for (int q = 1; q < KB; ++q) {
+    const v4i o = *(const LDS_AS v4i *)((const LDS_AS int32_t *)red + ((wave + q * NBLK) * 64 + lane) * 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] = add_wrap(acc[e], o[e]);
+  }
+  const int col = n0 + nblk * 16 + j;
+  if (col >= N) return;
   if (p.k_split == 1) {
-#pragma unroll
-    for (int nb = 0; nb < NBW; ++nb) {
-      const int col = n0 + (wave * NBW + nb) * 16 + j;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int row = g * 4 + e;
-        if (row < M && col < N) {
-          int32_t v = acc[nb][e];
-          if (HAS_D) v = add_wrap(v, Db[(int64_t)row * p.ldd + col]);
-          Cb[(int64_t)row * p.ldc + col] = v;
-        }
-      }
-    }
-    return;
-  }
-
-  // K split: publish this slice's partial, the last arriver reduces.
-  int32_t *wsb = p.ws + (int64_t)bidx * p.k_split * 16 * N;
-#pragma unroll
-  for (int nb = 0; nb < NBW; ++nb) {
-    const int col = n0 + (wave * NBW + nb) * 16 + j;
+    const int32_t *Db = HAS_D ? p.D + bidx * p.sd : nullptr;
+    int32_t *Cb = p.C + bidx * p.sc;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int row = g * 4 + e;
-      if (row < M && col < N) wsb[((int64_t)split * 16 + row) * N + col] = acc[nb][e];
-    }
-  }
-  __threadfence();
-  __syncthreads();
-  __shared__ int last;
-  if (tid == 0) {
-    int *ctr = p.counters + (int64_t)bidx * p.tiles_n + tile;
-    const int prev = atomicAdd(ctr, 1);
-    last = (prev == p.k_split - 1);
-    if (last) *ctr = 0;   // every slice has arrived: reset for the next launch
-  }
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-#pragma unroll
-  for (int nb = 0; nb < NBW; ++nb) {
-    const int col = n0 + (wave * NBW + nb) * 16 + j;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int row = g * 4 + e;
-      if (row < M && col < N) {
-        int32_t v = HAS_D ? Db[(int64_t)row * p.ldd + col] : 0;
-        for (int s = 0; s < p.k_split; ++s) {
-          const int32_t part = (s == split)
-              ? acc[nb][e]
-              : wsb[((int64_t)s * 16 + row) * N + col];
-          v = add_wrap(v, part);
-        }
+      if (row < M) {
+        int32_t v = acc[e];
+        if (HAS_D) v = add_wrap(v, Db[(int64_t)row * p.ldd + col]);
         Cb[(int64_t)row * p.ldc + col] = v;
       }
     }
+  } else {
+    int32_t *wsb = p.ws + ((int64_t)bidx * p.k_split + split) * M * N;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int row = g * 4 + e;
+      if (row < M) wsb[(int64_t)row * N + col] = acc[e];
+    }
   }
+}
+
+// C = D + sum over the K slices of the skinny partials. Launched on the same
+// stream right after skinny_kernel, so stream order makes the partials visible.
+struct ReduceArgs {
+  const int32_t *ws;   // [batch][k_split][M][N]
+  const int32_t *D;
+  int32_t *C;
+  int64_t ldd, ldc, sd, sc;
+  int M, N, k_split;
+};
+
+template <bool HAS_D>
+__global__ __launch_bounds__(256) void skinny_reduce_kernel(ReduceArgs p) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;   // over M*N/4 (N % 16 == 0)
+  const int64_t per = (int64_t)p.M * p.N / 4;
+  if (i >= per) return;
+  const int bidx = blockIdx.y;
+  const int64_t e = i * 4;
+  const int row = (int)(e / p.N), col = (int)(e - (int64_t)row * p.N);
+  const int32_t *w = p.ws + (int64_t)bidx * p.k_split * p.M * p.N + e;
+  v4i s = *(const v4i *)w;
+  for (int q = 1; q < p.k_split; ++q) {
+    const v4i o = *(const v4i *)(w + (int64_t)q * p.M * p.N);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) s[t] = add_wrap(s[t], o[t]);
+  }
+  int32_t *c = p.C + bidx * p.sc + (int64_t)row * p.ldc + col;
+  const int32_t *d = HAS_D ? p.D + bidx * p.sd + (int64_t)row * p.ldd + col : nullptr;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) c[t] = HAS_D ? add_wrap(s[t], d[t]) : s[t];
 }
 
 // ---------------------------------------------------------------------------
@@ -529,19 +598,18 @@ const VariantInfo kVariants[VT_VARIANT_COUNT] = {
     {"auto", 0, 0, 0, 0, 0},
     {"mfma_256x256", 256, 256, 64, 256, 2 * (256 * 64 + 64 * 256)},
     {"mfma_128x128", 128, 128, 64, 256, 2 * (128 * 64 + 64 * 128)},
-    {"skinny", 16, 128, 64, 256, 2 * 64 * 128},
+    {"skinny", 16, 64, 256, 1024, 2 * 16 * 1024},
     {"generic", 4, 64, 1, 256, 0},
     {"mfma_256x128", 256, 128, 64, 256, 2 * (256 * 64 + 64 * 128)},
 };
 
-constexpr int kSkinnyNB = 128;
-constexpr int kMaxSkinnyLds = 160 * 1024 - 256;   // leave room for static LDS
+// Default skinny configuration: 64-column slabs, 16 waves, 4 stages in flight.
+constexpr int kSkinnyNB = 64, kSkinnyWaves = 16, kSkinnyU = 4;
+constexpr int kMaxSkinnyLds = 160 * 1024;
 
 struct Workspace {
   int32_t *partials = nullptr;
   size_t partial_bytes = 0;
-  int *counters = nullptr;
-  size_t counter_count = 0;
 };
 
 struct DeviceState {
@@ -578,26 +646,21 @@ int current_device(int *dev_out, DeviceState **st_out) {
   return VT_OK;
 }
 
-// Workspace for the skinny kernel's K split on (device, stream). Counters are
-// zeroed once at allocation; each launch leaves them zero again.
-int get_workspace(DeviceState *st, void *stream, size_t partial_bytes, size_t counters,
-                  Workspace **out) {
+// Workspace for the skinny kernel's K-split partials on (device, stream).
+// Calls on one stream are ordered, so a stream's workspace is never shared by
+// two launches in flight.
+int get_workspace(DeviceState *st, void *stream, size_t partial_bytes, Workspace **out) {
   std::lock_guard<std::mutex> lk(g_mu);
   Workspace &w = st->ws[stream];
-  if (w.partial_bytes < partial_bytes || w.counter_count < counters) {
-    if (w.partials || w.counters) {
+  if (w.partial_bytes < partial_bytes) {
+    if (w.partials) {
       VT_HIP_CHECK(hipStreamSynchronize((hipStream_t)stream));
-      if (w.partials) VT_HIP_CHECK(hipFree(w.partials));
-      if (w.counters) VT_HIP_CHECK(hipFree(w.counters));
+      VT_HIP_CHECK(hipFree(w.partials));
       w = Workspace();
     }
     const size_t pb = partial_bytes > (1u << 20) ? partial_bytes : (1u << 20);
-    const size_t cc = counters > 4096 ? counters : 4096;
     VT_HIP_CHECK(hipMalloc((void **)&w.partials, pb));
-    VT_HIP_CHECK(hipMalloc((void **)&w.counters, cc * sizeof(int)));
-    VT_HIP_CHECK(hipMemset(w.counters, 0, cc * sizeof(int)));
     w.partial_bytes = pb;
-    w.counter_count = cc;
   }
   *out = &w;
   return VT_OK;
@@ -619,10 +682,15 @@ bool vector_ok(const Problem &q) {
          aligned16(q.B) && q.M < (1ll << 30) && q.N < (1ll << 30) && q.K < (1ll << 30);
 }
 
+// Workgroups along K for the skinny kernel: 1 when the column slabs alone
+// give most CUs a workgroup, else enough slices for ~256 workgroups, each at
+// least one unrolled pipeline (stage rows x U) long.
 int choose_k_split(int64_t N, int64_t K, int64_t batch) {
   const int64_t tiles = (N + kSkinnyNB - 1) / kSkinnyNB * batch;
-  int64_t ks = (512 + tiles - 1) / tiles;     // aim for >= 2 workgroups per CU
-  const int64_t max_by_k = K / 512 > 0 ? K / 512 : 1;   // slices >= 512 rows
+  if (tiles >= 192) return 1;
+  const int64_t pipe = (int64_t)kSkinnyWaves * 1024 / kSkinnyNB * kSkinnyU;
+  int64_t ks = (256 + tiles - 1) / tiles;
+  const int64_t max_by_k = (K + pipe - 1) / pipe;
   if (ks > max_by_k) ks = max_by_k;
   if (ks < 1) ks = 1;
   if (ks > 64) ks = 64;
@@ -675,7 +743,7 @@ int launch_mfma(const Problem &q, hipStream_t stream) {
   a.group_m = 4;
   const int64_t blocks = (int64_t)a.tiles_m * a.tiles_n * r.batch;
   if (blocks > 0x7fffffff) return fail(VT_EUNSUPPORTED, "grid of %lld tiles too large", (long long)blocks);
-  const bool edge = (r.M % BM) || (r.N % BN) || (r.K % 64);
+  const bool edge = (r.M % BM) || (r.N % BN) || (r.K % 128);
   const bool has_d = r.D != nullptr;
   dim3 grid((unsigned)blocks), block(256);
   if (edge) {
@@ -689,18 +757,21 @@ int launch_mfma(const Problem &q, hipStream_t stream) {
   return VT_OK;
 }
 
-int launch_skinny(const Problem &q, int k_split, DeviceState *st, void *stream) {
-  constexpr int NB = kSkinnyNB;
+template <int NB, int WAVES, int U>
+int launch_skinny_cfg(const Problem &q, int k_split, DeviceState *st, void *stream) {
+  constexpr int R = WAVES * 1024 / NB;           // rows per stage
+  constexpr int64_t kAlign = (int64_t)R * U;     // rows per unrolled pipeline
+  constexpr int64_t kStageLds = 2 * (int64_t)R * NB;
   if (q.M > 16) return fail(VT_EUNSUPPORTED, "skinny variant needs M <= 16 (M=%lld)", (long long)q.M);
   if (k_split <= 0) k_split = choose_k_split(q.N, q.K, q.batch);
-  // Slice length: multiple of 64 rows; recompute the split count it implies.
+  // Slice length: a multiple of the pipeline length; recompute the split
+  // count it implies; shrink slices whose A part would not fit in LDS.
   int64_t chunk = (q.K + k_split - 1) / k_split;
-  chunk = (chunk + 63) / 64 * 64;
-  int64_t lds = 16 * (chunk + 16) + 2 * 64 * NB;
+  chunk = (chunk + kAlign - 1) / kAlign * kAlign;
+  int64_t lds = 16 * (chunk + 16) + kStageLds;
   if (lds > kMaxSkinnyLds) {
-    // Too long a slice for LDS: shrink it.
-    chunk = ((kMaxSkinnyLds - 2 * 64 * NB) / 16 - 16) / 64 * 64;
-    lds = 16 * (chunk + 16) + 2 * 64 * NB;
+    chunk = ((kMaxSkinnyLds - kStageLds) / 16 - 16) / kAlign * kAlign;
+    lds = 16 * (chunk + 16) + kStageLds;
   }
   const int ks = (int)((q.K + chunk - 1) / chunk);
   SkinnyArgs a;
@@ -712,37 +783,51 @@ int launch_skinny(const Problem &q, int k_split, DeviceState *st, void *stream) 
   a.k_split = ks;
   a.k_chunk = (int)chunk;
   a.ws = nullptr;
-  a.counters = nullptr;
   if ((int64_t)a.tiles_n * ks > 0x7fffffff || q.batch > 65535)
     return fail(VT_EUNSUPPORTED, "skinny grid too large");
   if (ks > 1) {
     Workspace *w = nullptr;
-    const size_t pbytes = (size_t)q.batch * ks * 16 * q.N * sizeof(int32_t);
-    const size_t nctr = (size_t)q.batch * a.tiles_n;
-    int rc = get_workspace(st, stream, pbytes, nctr, &w);
+    const size_t pbytes = (size_t)q.batch * ks * q.M * q.N * sizeof(int32_t);
+    int rc = get_workspace(st, stream, pbytes, &w);
     if (rc) return rc;
     a.ws = w->partials;
-    a.counters = w->counters;
   }
-  dim3 grid((unsigned)(a.tiles_n * ks), (unsigned)q.batch), block(256);
   // Allow dynamic LDS up to the per-CU size (once per kernel instantiation).
   static std::once_flag lds_attr_once;
-  hipError_t attr_err = hipSuccess;
+  static hipError_t attr_err = hipSuccess;
   std::call_once(lds_attr_once, [&] {
-    hipError_t e1 = hipFuncSetAttribute((const void *)skinny_kernel<NB, true>,
+    hipError_t e1 = hipFuncSetAttribute((const void *)skinny_kernel<NB, WAVES, U, true>,
                                         hipFuncAttributeMaxDynamicSharedMemorySize, kMaxSkinnyLds);
-    hipError_t e2 = hipFuncSetAttribute((const void *)skinny_kernel<NB, false>,
+    hipError_t e2 = hipFuncSetAttribute((const void *)skinny_kernel<NB, WAVES, U, false>,
                                         hipFuncAttributeMaxDynamicSharedMemorySize, kMaxSkinnyLds);
     attr_err = e1 != hipSuccess ? e1 : e2;
   });
   if (attr_err != hipSuccess)
     return fail(VT_EHIP, "hipFuncSetAttribute(skinny LDS) failed: %s", hipGetErrorString(attr_err));
-  if (q.D)
-    hipLaunchKernelGGL((skinny_kernel<NB, true>), grid, block, (size_t)lds, (hipStream_t)stream, a);
+  hipStream_t s = (hipStream_t)stream;
+  dim3 grid((unsigned)(a.tiles_n * ks), (unsigned)q.batch), block(64 * WAVES);
+  // With a K split the slices write partials and the reduction applies D.
+  if (q.D && ks == 1)
+    hipLaunchKernelGGL((skinny_kernel<NB, WAVES, U, true>), grid, block, (size_t)lds, s, a);
   else
-    hipLaunchKernelGGL((skinny_kernel<NB, false>), grid, block, (size_t)lds, (hipStream_t)stream, a);
+    hipLaunchKernelGGL((skinny_kernel<NB, WAVES, U, false>), grid, block, (size_t)lds, s, a);
   VT_HIP_CHECK(hipGetLastError());
+  if (ks > 1) {
+    ReduceArgs r;
+    r.ws = a.ws; r.D = q.D; r.C = q.C;
+    r.ldd = q.ldd; r.ldc = q.ldc; r.sd = q.sd; r.sc = q.sc;
+    r.M = (int)q.M; r.N = (int)q.N; r.k_split = ks;
+    const int64_t per = q.M * q.N / 4;
+    dim3 rgrid((unsigned)((per + 255) / 256), (unsigned)q.batch);
+    if (q.D) hipLaunchKernelGGL(skinny_reduce_kernel<true>, rgrid, dim3(256), 0, s, r);
+    else hipLaunchKernelGGL(skinny_reduce_kernel<false>, rgrid, dim3(256), 0, s, r);
+    VT_HIP_CHECK(hipGetLastError());
+  }
   return VT_OK;
+}
+
+int launch_skinny(const Problem &q, int k_split, DeviceState *st, void *stream) {
+  return launch_skinny_cfg<kSkinnyNB, kSkinnyWaves, kSkinnyU>(q, k_split, st, stream);
 }
 
 int launch_generic(const Problem &q, hipStream_t stream) {

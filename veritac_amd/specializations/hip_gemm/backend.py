@@ -50,10 +50,11 @@ TILES = {
     "mfma_256x256": (256, 256, 64, 256, 2 * (256 * 64 + 64 * 256)),
     "mfma_256x128": (256, 128, 64, 256, 2 * (256 * 64 + 64 * 128)),
     "mfma_128x128": (128, 128, 64, 256, 2 * (128 * 64 + 64 * 128)),
-    "skinny": (16, 128, 64, 256, 2 * 64 * 128),
+    "skinny": (16, 64, 256, 1024, 2 * 16 * 1024),
     "generic": (4, 64, 1, 256, 0),
 }
 SKINNY_MAX_M = 16
+SKINNY_PIPE_ROWS = 256 * 4  # stage rows x stages in flight (kSkinny* in the HIP source)
 LDS_PER_CU = 160 * 1024
 
 # MI355X datasheet figures used by the analytic model and the rooflines.
@@ -76,25 +77,28 @@ def _is_int(v):
 def skinny_split(plan):
     """(k_split, k_chunk) the skinny kernel launches for this plan.
 
-    Mirrors launch_skinny in csrc/vt_hip_gemm.hip: the requested split (or the
-    automatic one) is turned into 64-row-aligned slices that fit in LDS.
+    Mirrors launch_skinny_cfg in csrc/vt_hip_gemm.hip: the requested split (or
+    the automatic one) becomes slices of a whole number of pipelines
+    (SKINNY_PIPE_ROWS rows) whose A part fits in LDS.
     """
     k, ks = plan["k"], plan["k_split"]
     if ks <= 0:
         ks = _auto_k_split(plan["n"], k, plan["batch"])
+    align = SKINNY_PIPE_ROWS
+    stage_lds = TILES["skinny"][4]
     chunk = -(-k // ks)
-    chunk = -(-chunk // 64) * 64
-    lds = 16 * (chunk + 16) + TILES["skinny"][4]
-    limit = LDS_PER_CU - 256
-    if lds > limit:
-        chunk = ((limit - TILES["skinny"][4]) // 16 - 16) // 64 * 64
+    chunk = -(-chunk // align) * align
+    if 16 * (chunk + 16) + stage_lds > LDS_PER_CU:
+        chunk = ((LDS_PER_CU - stage_lds) // 16 - 16) // align * align
     return -(-k // chunk), chunk
 
 
 def _auto_k_split(n, k, batch):
     tiles = -(-n // TILES["skinny"][1]) * batch
-    ks = -(-512 // tiles)
-    ks = min(ks, max(k // 512, 1))
+    if tiles >= 192:
+        return 1
+    ks = -(-256 // tiles)
+    ks = min(ks, -(-k // SKINNY_PIPE_ROWS))
     return max(1, min(ks, 64))
 
 
@@ -231,7 +235,7 @@ def modeled_counts(plan):
         l2_bytes = b_eff * (tiles_n * m_eff * k + tiles_m * k * n) + c_and_d
     elif variant == "skinny":
         ks, _ = skinny_split(plan)
-        partial = 2 * 4 * b * 16 * n * ks if ks > 1 else 0
+        partial = 2 * 4 * b * m * n * ks if ks > 1 else 0
         l2_bytes = alg + partial + b * -(-n // tn) * 16 * k
     else:
         l2_bytes = b * (m * n * k + -(-m // 4) * n * k) + 4 * b * m * n
