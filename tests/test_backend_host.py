@@ -100,13 +100,15 @@ def test_modeled_counts_are_consistent():
 def test_skinny_split_mirrors_native_rule():
     p = hg.make_plan(16, 14336, 4096, variant="skinny")
     ks, chunk = hg.skinny_split(p)
-    assert (ks, chunk) == (1, 4096)          # 224 column slabs fill the chip
-    for req in (2, 3, 4, 7):
+    assert (ks, chunk) == (4, 1024)          # 56 column slabs x 4 K slices
+    for req in (1, 2, 3, 4, 7):
         ks, chunk = hg.skinny_split(dict(p, k_split=req))
         assert chunk % hg.SKINNY_PIPE_ROWS == 0 and ks * chunk >= 4096 and (ks - 1) * chunk < 4096
-    p = hg.make_plan(16, 2048, 8192, variant="skinny")    # 32 slabs: split K
+    p = hg.make_plan(16, 2048, 8192, variant="skinny")    # 8 slabs: split K
     ks, chunk = hg.skinny_split(p)
-    assert ks == 8 and chunk == 1024
+    assert ks == 22 and chunk == 384        # 28 requested -> 384-row slices
+    p = hg.make_plan(16, 65536, 4096, variant="skinny")   # 256 slabs: no split
+    assert hg.skinny_split(p) == (1, 4096)
     lds, wgs = hg.required_resources(dict(p, k=131056, k_split=1))
     assert lds <= hg.LDS_PER_CU
 

@@ -276,3 +276,45 @@ def test_cpu_reference_agrees_on_gpu_box(dev):
     A = rng.integers(-128, 128, (96, 512), dtype=np.int8)
     B = rng.integers(-128, 128, (512, 320), dtype=np.int8)
     assert np.array_equal(gpu_gemm(dev, A, B), cref.gemm_i8(A, B, order="ikj"))
+
+
+FULL_TILE_SHAPES = [(256, 256, 64), (256, 512, 192), (512, 256, 1088), (768, 512, 4096),
+                    (256, 256, 128)]
+
+
+@pytest.mark.parametrize("shape", FULL_TILE_SHAPES)
+def test_full_tile_dma_path(dev, shape):
+    """Shapes made of whole 256x256 tiles take the direct-to-LDS kernel."""
+    m, n, k = shape
+    rng = np.random.default_rng(m + 3 * n + 7 * k)
+    A = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    B = rng.integers(-128, 128, (k, n), dtype=np.int8)
+    D = rng.integers(-(1 << 20), (1 << 20) + 1, (m, n), dtype=np.int32)
+    say("full tile", shape)
+    assert np.array_equal(gpu_gemm(dev, A, B, variant="mfma_256x256"), go.gemm_i8(A, B))
+    assert np.array_equal(gpu_gemm(dev, A, B, D, variant="mfma_256x256"), go.gemm_i8(A, B, D))
+    # batched, one B per batch (no stacked-M fold), with D
+    A3 = rng.integers(-128, 128, (3, m, k), dtype=np.int8)
+    B3 = rng.integers(-128, 128, (3, k, n), dtype=np.int8)
+    D3 = rng.integers(-99, 99, (3, m, n), dtype=np.int32)
+    assert np.array_equal(gpu_gemm(dev, A3, B3, D3, variant="mfma_256x256"), go.gemm_i8(A3, B3, D3))
+
+
+def test_full_tile_repeated_launches_are_stable(dev):
+    """Many back-to-back launches of the pipelined kernels give identical,
+    exact results (a stage published too early would show as a mismatch)."""
+    rng = np.random.default_rng(77)
+    m = n = 1024
+    k = 2048
+    A = torch.from_numpy(rng.integers(-128, 128, (m, k), dtype=np.int8)).to(dev)
+    B = torch.from_numpy(rng.integers(-128, 128, (k, n), dtype=np.int8)).to(dev)
+    want = go.gemm_i8(A.cpu().numpy(), B.cpu().numpy())
+    for variant in ("mfma_256x256", "mfma_256x128", "mfma_128x128"):
+        outs = [torch.full((m, n), INT32_MIN, dtype=torch.int32, device=dev) for _ in range(20)]
+        for C in outs:
+            _lib.gemm_raw(A.data_ptr(), B.data_ptr(), None, C.data_ptr(), m, n, k, k, n, n, n,
+                          variant=variant)
+        _lib.sync(None)
+        say("repeat", variant)
+        for C in outs:
+            assert np.array_equal(C.cpu().numpy(), want), variant

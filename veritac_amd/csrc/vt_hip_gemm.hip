@@ -107,6 +107,34 @@ __device__ __forceinline__ int a_off(int row, int c) {
   return row * 64 + ((c ^ (((row >> 1) ^ (row >> 3)) & 3)) << 4);
 }
 
+// Epilogue shared by the MFMA kernels. 32x32 accumulator layout: element e
+// of lane l is row 8*(e/4) + 4*(l/32) + e%4 and column l%32 of the block, so
+// one store instruction writes two full 128-byte row segments of C.
+template <int MI, int NI, bool EDGE, bool HAS_D>
+__device__ __forceinline__ void store_tile(const v16i (&acc)[MI][NI], int32_t *Cb,
+                                           const int32_t *Db, int64_t ldc, int64_t ldd,
+                                           int row0, int col0, int M, int N, int lane) {
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi) {
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni) {
+      const int col = col0 + ni * 32 + (lane & 31);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int row = row0 + mi * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+        if (!EDGE || (row < M && col < N)) {
+          int32_t v = acc[mi][ni][e];
+          if (HAS_D) v = add_wrap(v, Db[(int64_t)row * ldd + col]);
+          Cb[(int64_t)row * ldc + col] = v;
+        }
+      }
+    }
+    // One 32-row block at a time: keeps the D loads from being hoisted for
+    // the whole tile at once (they would not fit in registers).
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Compute-bound MFMA kernel
 // ---------------------------------------------------------------------------
@@ -120,6 +148,7 @@ struct GemmArgs {
   int64_t sa, sb, sd, sc;
   int M, N, K;
   int tiles_m, tiles_n, group_m;
+  int batch_count;   // batches (the persistent kernel walks all their tiles)
 };
 
 template <int BM, int BN, bool EDGE, bool HAS_D>
@@ -334,25 +363,239 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma_kernel(GemmArgs p) {
     step(kt + 1, ra1, rb1);
   }
 
-  // Epilogue. 32x32 accumulator layout: element e of lane l is
-  // row 8*(e/4) + 4*(l/32) + e%4, column l%32.
-  int32_t *Cb = p.C + bidx * p.sc;
-  const int32_t *Db = HAS_D ? p.D + bidx * p.sd : nullptr;
+  store_tile<MI, NI, EDGE, HAS_D>(acc, p.C + bidx * p.sc, HAS_D ? p.D + bidx * p.sd : nullptr,
+                                  p.ldc, p.ldd, m0 + wm * WTM, n0 + wn * WTN, M, N, lane);
+}
+
+// ---------------------------------------------------------------------------
+// Full-tile MFMA kernel with direct-to-LDS loads (256 x 256 tiles)
+// ---------------------------------------------------------------------------
+
+// gfx950 LDS DMA: each lane of the wave fetches the 16 global bytes at
+// base + voff and the wave writes them, in lane order, to the 1 KB of LDS
+// starting at m0. The LDS stores are tracked by vmcnt like any global load;
+// the caller waits with s_waitcnt vmcnt before a barrier publishes them.
+__device__ __forceinline__ void dma_b128(const int8_t *base, uint32_t voff, uint32_t m0) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(voff), "s"(base), "s"(m0));
+}
+
+// Same contract as gemm_mfma_kernel<256, 256, false, HAS_D> (full tiles only:
+// M % 256 == 0, N % 256 == 0, K % 64 == 0), but the k slices go global -> LDS
+// by DMA (no VGPR staging, no ds_write instructions) and the kernel is
+// persistent: one workgroup per CU walks its tiles in order and the slice
+// stream runs on across tile boundaries, so the last steps of a tile already
+// fetch the first slices of the next one and a tile change costs only its
+// C stores.
+//
+// Slices are numbered globally, g = (tile iteration) * KT + kt. Four LDS
+// stages: step g computes slice g from stage g%4, reads the first fragments of
+// slice g+1 early, and issues the DMA of slice g+3 into stage (g+3)%4 (last
+// read in step g-1). The wait at the end of step g (vmcnt(8): only slice
+// g+3's eight DMAs per wave may still be in flight) plus the barrier publish
+// slice g+2 before step g+1 reads its fragments early.
+template <bool HAS_D>
+__global__ __launch_bounds__(256, 1) void gemm_dma_kernel(GemmArgs p) {
+  constexpr int BM = 256, BN = 256, BK = 64;
+  constexpr int WTM = BM / 2, WTN = BN / 2, MI = WTM / 32, NI = WTN / 32;
+  constexpr int BCH = BN / 16;
+  constexpr int A_BYTES = BM * BK, B_BYTES = BK * BN, STAGE = A_BYTES + B_BYTES;
+  constexpr int NSTAGE = 4;
+  __shared__ __attribute__((aligned(1024))) int8_t smem[NSTAGE * STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // This workgroup computes logical tiles wl, wl + G, wl + 2G, ... where wl
+  // is its XCD-contiguous rank (workgroup w runs on XCD w % 8), so the tiles
+  // in flight on one XCD form a compact block that shares its L2.
+  const int G = gridDim.x;
+  const int w = blockIdx.x;
+  const int q = G >> 3, r = G & 7, x = w & 7;
+  const int wl = x * q + (x < r ? x : r) + (w >> 3);
+  const int per_batch = p.tiles_m * p.tiles_n;
+  const int total_tiles = per_batch * p.batch_count;
+  if (wl >= total_tiles) return;
+  const int ntiles = (total_tiles - 1 - wl) / G + 1;
+  const int group = p.group_m * p.tiles_n;
+  // Tile iteration -> (batch, row origin, column origin).
+  auto tile_coords = [&](int it, int &bidx, int &m0, int &n0) {
+    const int lt = wl + it * G;
+    bidx = lt / per_batch;
+    const int t = lt - bidx * per_batch;
+    const int gid = t / group;
+    const int first_m = gid * p.group_m;
+    const int gm = min(p.tiles_m - first_m, p.group_m);
+    const int within = t - gid * group;
+    m0 = (first_m + within % gm) * BM;
+    n0 = (within / gm) * BN;
+  };
+
+  const int64_t lda = p.lda, ldb = p.ldb;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(LDS_AS int8_t *)smem;
+  const int KT = p.K / BK;
+  const int last_g = ntiles * KT - 1;
+
+  // DMA sources. Wave w fills A blocks 4w..4w+3 (16 rows of 64 bytes each)
+  // and B blocks 4w..4w+3 (4 rows of 256 bytes each); lane L lands at byte
+  // 16*L of its block, so it fetches the logical chunk that the swizzle maps
+  // to that position (XOR swizzles are their own inverse). Lane offsets are
+  // relative to the tile's origin, which goes into the wave-uniform base.
+  uint32_t a_lane[4], b_lane[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int arow = (wave * 4 + i) * 16 + (lane >> 2);
+    const int ac = (lane & 3) ^ (((arow >> 1) ^ (arow >> 3)) & 3);
+    a_lane[i] = (uint32_t)((int64_t)arow * lda + ac * 16);
+    const int brow = (wave * 4 + i) * 4 + (lane >> 4);
+    const int bc = (lane & 15) ^ b_swz<BCH>(brow);
+    b_lane[i] = (uint32_t)((int64_t)brow * ldb + bc * 16);
+  }
+  // The slice the next DMA fetches, as (tile iteration, k slice), advanced one
+  // slice per DMA round; tile origins are recomputed only at tile changes.
+  // Slices past the last one re-read it (their stages are never read).
+  int d_it = 0, d_kt = 0;
+  const int8_t *a_tile = nullptr, *b_tile = nullptr;
+  auto set_tile = [&](int it) {
+    int bidx, m0, n0;
+    tile_coords(it, bidx, m0, n0);
+    a_tile = p.A + bidx * p.sa + (int64_t)m0 * lda;
+    b_tile = p.B + bidx * p.sb + n0;
+  };
+  set_tile(0);
+  auto next_bases = [&](const int8_t *&abase, const int8_t *&bbase) {
+    abase = a_tile + d_kt * BK;
+    bbase = b_tile + (int64_t)(d_kt * BK) * ldb;
+    if (d_it * KT + d_kt < last_g) {
+      if (++d_kt == KT) {
+        d_kt = 0;
+        set_tile(++d_it);
+      }
+    }
+  };
+  auto issue_slice = [&](int stage) {
+    const int8_t *abase, *bbase;
+    next_bases(abase, bbase);
+    const uint32_t ma = lds0 + stage * STAGE + wave * 4 * 1024;
+    const uint32_t mb = ma + A_BYTES;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dma_b128(abase, a_lane[i], ma + i * 1024);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dma_b128(bbase, b_lane[i], mb + i * 1024);
+  };
+
+  const int g = lane >> 4, j = lane & 15;
+  int a_frag[2][MI], b_frag[2][NI];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi)
+      a_frag[ks][mi] = a_off(wm * WTM + mi * 32 + (lane & 31), ks * 2 + (lane >> 5));
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni) {
+      const int nc = (wn * WTN + ni * 32) / 16 + (g & 1);
+      const int r0 = ks * 32 + (g >> 1) * 16 + (j >> 1);
+      b_frag[ks][ni] = r0 * BN + ((nc ^ b_swz<BCH>(r0)) << 4) + (j & 1) * 8;
+    }
+  }
+  v16i acc[MI][NI];
 #pragma unroll
   for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
-    for (int ni = 0; ni < NI; ++ni) {
-      const int col = n0 + wn * WTN + ni * 32 + (lane & 31);
+    for (int ni = 0; ni < NI; ++ni)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int row = m0 + wm * WTM + mi * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
-        if (!EDGE || (row < M && col < N)) {
-          int32_t v = acc[mi][ni][e];
-          if (HAS_D) v = add_wrap(v, Db[(int64_t)row * p.ldd + col]);
-          Cb[(int64_t)row * p.ldc + col] = v;
-        }
-      }
+      for (int e = 0; e < 16; ++e) acc[mi][ni][e] = 0;
+
+  // Fragments of one 32-deep k step as 12 LDS reads ("units"): units 0..3
+  // are the A blocks (ds_read_b128), units 4..11 the lo/hi halves of the B
+  // blocks (ds_read_b64_tr_b8).
+  constexpr int NUNIT = MI + 2 * NI;
+  static_assert(NUNIT == 12, "the barrier wait count assumes 12 fragment reads");
+  v4i fa0[MI], fa1[MI];
+  v2i fl0[NI], fh0[NI], fl1[NI], fh1[NI];
+  auto read_unit = [&](int stage, int ks, int u, v4i *fa, v2i *fl, v2i *fh) {
+    const int8_t *As = smem + stage * STAGE;
+    const int8_t *Bs = As + A_BYTES;
+    if (u < MI) {
+      fa[u] = ld_lds_b128(As, a_frag[ks][u]);
+    } else {
+      const int ni = (u - MI) >> 1;
+      if (((u - MI) & 1) == 0) fl[ni] = ld_lds_tr8(Bs, b_frag[ks][ni]);
+      else fh[ni] = ld_lds_tr8(Bs, b_frag[ks][ni] + 8 * BN);
     }
+  };
+  auto mfma = [&](int mi, int ni, const v4i *fa, const v2i *fl, const v2i *fh) {
+    const v4i b = v4i{fl[ni].x, fl[ni].y, fh[ni].x, fh[ni].y};
+    acc[mi][ni] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[mi], b, acc[mi][ni], 0, 0, 0);
+  };
+
+  issue_slice(0);
+  issue_slice(1);
+  issue_slice(2);
+  asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");   // slices 0, 1 landed
+#pragma unroll
+  for (int u = 0; u < NUNIT; ++u) read_unit(0, 0, u, fa0, fl0, fh0);
+
+  int gs = 0;   // global slice index
+  for (int it = 0; it < ntiles; ++it) {
+    // Explicit schedule, one MFMA per scheduling region (in fragment read
+    // order, so each MFMA waits only for its own operands), each followed by
+    // two fragment reads or one DMA.
+    for (int kt = 0; kt < KT; ++kt, ++gs) {
+      const int s0 = gs & 3, s1 = (gs + 1) & 3, s3 = (gs + 3) & 3;
+      const int8_t *abase, *bbase;
+      next_bases(abase, bbase);   // slice gs+3
+      const uint32_t ma = lds0 + s3 * STAGE + wave * 4 * 1024;
+      const uint32_t mb = ma + A_BYTES;
+      // First half step: MFMAs of k 0..31 (slice gs); the k 32..63 fragments
+      // of slice gs and the DMA of slice gs+3 go out between them.
+#pragma unroll
+      for (int i = 0; i < MI * NI; ++i) {
+        mfma(i / NI, i % NI, fa0, fl0, fh0);
+        if (i < NUNIT / 2) {
+          read_unit(s0, 1, 2 * i, fa1, fl1, fh1);
+          read_unit(s0, 1, 2 * i + 1, fa1, fl1, fh1);
+        } else if (i - NUNIT / 2 < 4) {
+          const int d = i - NUNIT / 2;
+          dma_b128(abase, a_lane[d], ma + d * 1024);
+        } else if (i - NUNIT / 2 < 8) {
+          const int d = i - NUNIT / 2 - 4;
+          dma_b128(bbase, b_lane[d], mb + d * 1024);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // Second half step: MFMAs of k 32..63; slice gs+1's first fragments
+      // (published by the previous barrier) go out between them. All reads
+      // of stage s0 were issued above, ahead of these reads of stage s1.
+#pragma unroll
+      for (int i = 0; i < MI * NI; ++i) {
+        mfma(i / NI, i % NI, fa1, fl1, fh1);
+        if (i < NUNIT / 2) {
+          read_unit(s1, 0, 2 * i, fa0, fl0, fh0);
+          read_unit(s1, 0, 2 * i + 1, fa0, fl0, fh0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // Slice gs+2 has landed (only slice gs+3's eight DMAs per wave remain
+      // in flight; older stores are waited for as well) and every read of
+      // stage s0 has completed (only the 12 reads of stage s1 remain), so
+      // after the barrier step gs+1 may refill stage s0.
+      asm volatile("s_waitcnt vmcnt(8) lgkmcnt(12)\n\ts_barrier" ::: "memory");
+    }
+    int bidx, m0, n0;
+    tile_coords(it, bidx, m0, n0);
+    store_tile<MI, NI, false, HAS_D>(acc, p.C + bidx * p.sc, HAS_D ? p.D + bidx * p.sd : nullptr,
+                                     p.ldc, p.ldd, m0 + wm * WTM, n0 + wn * WTN, p.M, p.N, lane);
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[mi][ni][e] = 0;
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 // ---------------------------------------------------------------------------
@@ -598,13 +841,14 @@ const VariantInfo kVariants[VT_VARIANT_COUNT] = {
     {"auto", 0, 0, 0, 0, 0},
     {"mfma_256x256", 256, 256, 64, 256, 2 * (256 * 64 + 64 * 256)},
     {"mfma_128x128", 128, 128, 64, 256, 2 * (128 * 64 + 64 * 128)},
-    {"skinny", 16, 64, 256, 1024, 2 * 16 * 1024},
+    {"skinny", 16, 256, 64, 1024, 2 * 16 * 1024},
     {"generic", 4, 64, 1, 256, 0},
     {"mfma_256x128", 256, 128, 64, 256, 2 * (256 * 64 + 64 * 128)},
 };
 
-// Default skinny configuration: 64-column slabs, 16 waves, 4 stages in flight.
-constexpr int kSkinnyNB = 64, kSkinnyWaves = 16, kSkinnyU = 4;
+// Default skinny configuration: 256-column slabs (full 128-byte lines of B
+// per row), 16 waves, 2 stages in flight per thread.
+constexpr int kSkinnyNB = 256, kSkinnyWaves = 16, kSkinnyU = 2;
 constexpr int kMaxSkinnyLds = 160 * 1024;
 
 struct Workspace {
@@ -615,6 +859,7 @@ struct Workspace {
 struct DeviceState {
   bool probed = false;
   bool ok = false;
+  int num_cus = 256;
   std::string arch;
   std::map<void *, Workspace> ws;   // per stream
 };
@@ -635,6 +880,7 @@ int current_device(int *dev_out, DeviceState **st_out) {
     if (hipGetDeviceProperties(&prop, dev) != hipSuccess)
       return fail(VT_ENODEV, "hipGetDeviceProperties(%d) failed", dev);
     st.arch = prop.gcnArchName;
+    st.num_cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
     st.ok = strncmp(prop.gcnArchName, "gfx950", 6) == 0;
     st.probed = true;
   }
@@ -683,13 +929,13 @@ bool vector_ok(const Problem &q) {
 }
 
 // Workgroups along K for the skinny kernel: 1 when the column slabs alone
-// give most CUs a workgroup, else enough slices for ~256 workgroups, each at
+// give most CUs a workgroup, else enough slices for ~224 workgroups, each at
 // least one unrolled pipeline (stage rows x U) long.
 int choose_k_split(int64_t N, int64_t K, int64_t batch) {
   const int64_t tiles = (N + kSkinnyNB - 1) / kSkinnyNB * batch;
   if (tiles >= 192) return 1;
   const int64_t pipe = (int64_t)kSkinnyWaves * 1024 / kSkinnyNB * kSkinnyU;
-  int64_t ks = (256 + tiles - 1) / tiles;
+  int64_t ks = (224 + tiles - 1) / tiles;
   const int64_t max_by_k = (K + pipe - 1) / pipe;
   if (ks > max_by_k) ks = max_by_k;
   if (ks < 1) ks = 1;
@@ -724,8 +970,18 @@ int select_variant(const Problem &q, bool vec, int32_t *variant, int32_t *k_spli
   return VT_OK;
 }
 
+int launch_generic(const Problem &q, hipStream_t stream);
+
+// The MFMA kernels address A and B with 32-bit lane offsets from a per-slice
+// base: every row offset inside one batch must stay below 2^32.
+bool offsets_fit_32(const Problem &q, int64_t m_rows) {
+  const int64_t a_span = m_rows * q.lda;
+  const int64_t b_span = q.K * q.ldb;
+  return a_span < (1ll << 32) - 4096 && b_span < (1ll << 32) - 4096;
+}
+
 template <int BM, int BN>
-int launch_mfma(const Problem &q, hipStream_t stream) {
+int launch_mfma(const Problem &q, hipStream_t stream, int num_cus) {
   // Fold contiguous shared-B batches into one stacked-M GEMM.
   Problem r = q;
   if (r.batch > 1 && r.sb == 0 && r.sa == r.M * r.lda && r.sc == r.M * r.ldc &&
@@ -733,6 +989,7 @@ int launch_mfma(const Problem &q, hipStream_t stream) {
     r.M *= r.batch;
     r.batch = 1;
   }
+  if (!offsets_fit_32(r, (r.M + BM - 1) / BM * BM)) return launch_generic(q, stream);
   GemmArgs a;
   a.A = r.A; a.B = r.B; a.D = r.D; a.C = r.C;
   a.lda = r.lda; a.ldb = r.ldb; a.ldd = r.ldd; a.ldc = r.ldc;
@@ -743,9 +1000,18 @@ int launch_mfma(const Problem &q, hipStream_t stream) {
   a.group_m = 4;
   const int64_t blocks = (int64_t)a.tiles_m * a.tiles_n * r.batch;
   if (blocks > 0x7fffffff) return fail(VT_EUNSUPPORTED, "grid of %lld tiles too large", (long long)blocks);
-  const bool edge = (r.M % BM) || (r.N % BN) || (r.K % 128);
   const bool has_d = r.D != nullptr;
   dim3 grid((unsigned)blocks), block(256);
+  a.batch_count = (int)r.batch;
+  if (BM == 256 && BN == 256 && !has_d && !(r.M % BM) && !(r.N % BN) && !(r.K % 64)) {
+    // Persistent: one workgroup per CU (the kernel's LDS allows no more).
+    const int64_t g = blocks < num_cus ? blocks : num_cus;
+    dim3 pgrid((unsigned)g);
+    hipLaunchKernelGGL(gemm_dma_kernel<false>, pgrid, block, 0, stream, a);
+    VT_HIP_CHECK(hipGetLastError());
+    return VT_OK;
+  }
+  const bool edge = (r.M % BM) || (r.N % BN) || (r.K % 128);
   if (edge) {
     if (has_d) hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, true, true>), grid, block, 0, stream, a);
     else hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, true, false>), grid, block, 0, stream, a);
@@ -964,9 +1230,9 @@ int vt_gemm_i8(const int8_t *A, const int8_t *B, const int32_t *D, int32_t *C, i
   if (rc) return rc;
   hipStream_t s = (hipStream_t)stream;
   switch (chosen) {
-    case VT_VARIANT_MFMA_256x256: return launch_mfma<256, 256>(q, s);
-    case VT_VARIANT_MFMA_128x128: return launch_mfma<128, 128>(q, s);
-    case VT_VARIANT_MFMA_256x128: return launch_mfma<256, 128>(q, s);
+    case VT_VARIANT_MFMA_256x256: return launch_mfma<256, 256>(q, s, st->num_cus);
+    case VT_VARIANT_MFMA_128x128: return launch_mfma<128, 128>(q, s, st->num_cus);
+    case VT_VARIANT_MFMA_256x128: return launch_mfma<256, 128>(q, s, st->num_cus);
     case VT_VARIANT_SKINNY: return launch_skinny(q, ks, st, stream);
     case VT_VARIANT_GENERIC: return launch_generic(q, s);
     default: return fail(VT_EINVAL, "unknown variant %d", (int)chosen);

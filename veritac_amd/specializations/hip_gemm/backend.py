@@ -50,11 +50,11 @@ TILES = {
     "mfma_256x256": (256, 256, 64, 256, 2 * (256 * 64 + 64 * 256)),
     "mfma_256x128": (256, 128, 64, 256, 2 * (256 * 64 + 64 * 128)),
     "mfma_128x128": (128, 128, 64, 256, 2 * (128 * 64 + 64 * 128)),
-    "skinny": (16, 64, 256, 1024, 2 * 16 * 1024),
+    "skinny": (16, 256, 64, 1024, 2 * 16 * 1024),
     "generic": (4, 64, 1, 256, 0),
 }
 SKINNY_MAX_M = 16
-SKINNY_PIPE_ROWS = 256 * 4  # stage rows x stages in flight (kSkinny* in the HIP source)
+SKINNY_PIPE_ROWS = 64 * 2   # stage rows x stages in flight (kSkinny* in the HIP source)
 LDS_PER_CU = 160 * 1024
 
 # MI355X datasheet figures used by the analytic model and the rooflines.
@@ -97,7 +97,7 @@ def _auto_k_split(n, k, batch):
     tiles = -(-n // TILES["skinny"][1]) * batch
     if tiles >= 192:
         return 1
-    ks = -(-256 // tiles)
+    ks = -(-224 // tiles)
     ks = min(ks, -(-k // SKINNY_PIPE_ROWS))
     return max(1, min(ks, 64))
 
