@@ -318,3 +318,43 @@ def test_full_tile_repeated_launches_are_stable(dev):
         say("repeat", variant)
         for C in outs:
             assert np.array_equal(C.cpu().numpy(), want), variant
+
+
+# (m, n, k, batch, with_d): decode-sized skinny problems -- a single k slice
+# (K = 64), K not a multiple of the slice pipeline (4160), M of 1 / 3 / 7 / 15,
+# an initial partial sum and two batches.
+DECODE_SHAPES = [(16, 8192, 4096, 1, False), (1, 8192, 64, 1, True), (3, 8192, 128, 1, False),
+                 (15, 8192, 4160, 1, True), (16, 4096, 512, 2, True), (7, 14336, 1024, 1, False)]
+
+
+@pytest.mark.parametrize("shape", DECODE_SHAPES)
+def test_decode_kernel_shapes(dev, shape):
+    m, n, k, b, with_d = shape
+    say("decode shape", shape)
+    assert _lib.select_variant(m, n, k, b, k, n, True)[0] == "skinny"
+    rng = np.random.default_rng(m * 7 + k)
+    A = rng.integers(-128, 128, (b, m, k) if b > 1 else (m, k), dtype=np.int8)
+    B = rng.integers(-128, 128, (b, k, n) if b > 1 else (k, n), dtype=np.int8)
+    D = rng.integers(-2**20, 2**20, A.shape[:-1] + (n,), dtype=np.int32) if with_d else None
+    want = go.gemm_i8_f64(A, B, D)
+    assert np.array_equal(gpu_gemm(dev, A, B, D), want)
+    for ks in (1, 3):
+        assert np.array_equal(gpu_gemm(dev, A, B, D, variant="skinny", k_split=ks), want)
+
+
+def test_decode_kernel_padded_strides(dev):
+    m, n, k = 16, 8192, 2048
+    lda, ldb, ldc = k + 80, n + 128, n + 48
+    rng = np.random.default_rng(5)
+    Ap = rng.integers(-128, 128, (m, lda), dtype=np.int8)
+    Bp = rng.integers(-128, 128, (k, ldb), dtype=np.int8)
+    want = go.gemm_i8_f64(Ap[:, :k], Bp[:, :n])
+    At = torch.from_numpy(Ap).to(dev)
+    Bt = torch.from_numpy(Bp).to(dev)
+    Ct = torch.full((m, ldc), INT32_MIN, dtype=torch.int32, device=dev)
+    _lib.gemm_raw(At.data_ptr(), Bt.data_ptr(), None, Ct.data_ptr(), m, n, k, lda, ldb, n, ldc,
+                  variant="skinny", k_split=0)
+    _lib.sync(None)
+    got = Ct.cpu().numpy()
+    assert np.array_equal(got[:, :n], want)
+    assert (got[:, n:] == INT32_MIN).all()

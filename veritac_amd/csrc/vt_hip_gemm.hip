@@ -9,23 +9,29 @@
 // kernel here relies on.
 //
 // Kernels
-//   gemm_mfma_kernel<BM,BN>  compute-bound tiles. 256 threads = 4 waves in a
-//       2x2 grid, each wave owns a (BM/2)x(BN/2) block of 32x32 accumulators
-//       fed by v_mfma_i32_32x32x32_i8. A/B k-slices of 64 bytes are staged
-//       global -> VGPR -> LDS (double buffer, one LDS-only barrier per step,
-//       next slice's global loads in flight during the MFMAs). A is stored
-//       [m][k] and read with ds_read_b128; B stays row-major [k][n] in LDS and
-//       is read into the MFMA operand layout with ds_read_b64_tr_b8 (gfx950's
-//       transposing LDS read), so B is never transposed in memory. 16-byte
-//       chunks are XOR-swizzled so the LDS reads are bank-conflict free.
-//       Workgroup ids are remapped so consecutive tiles share an XCD (and its
-//       L2), then grouped along M.
+//   gemm_dma_kernel  full 256x256 tiles without D (the 8192^3 case).
+//       Persistent: one workgroup per CU walks its tiles in XCD-contiguous
+//       order; k slices go global -> LDS by direct-to-LDS DMA
+//       (global_load_lds_dwordx4) into four stages, three slices ahead, and
+//       the slice stream runs across tile boundaries. The MFMA, fragment-read
+//       and DMA instructions follow an explicit per-slot schedule.
+//   gemm_mfma_kernel<BM,BN>  every other compute-bound case. 256 threads = 4
+//       waves in a 2x2 grid, each wave owns a (BM/2)x(BN/2) block of 32x32
+//       accumulators fed by v_mfma_i32_32x32x32_i8. A/B k-slices of 64 bytes
+//       are staged global -> VGPR -> LDS (three LDS buffers, next slices'
+//       global loads in flight during the MFMAs). A is stored [m][k] and read
+//       with ds_read_b128; B stays row-major [k][n] in LDS and is read into
+//       the MFMA operand layout with ds_read_b64_tr_b8 (gfx950's transposing
+//       LDS read), so B is never transposed in memory. 16-byte chunks are
+//       XOR-swizzled so the LDS accesses are bank-conflict free. Workgroup ids
+//       are remapped so consecutive tiles share an XCD (and its L2), then
+//       grouped along M.
 //   skinny_kernel<NB>  M <= 16 (decode). Bandwidth-bound: each workgroup
-//       streams an NB-column slab of B exactly once over a K slice, U slices
-//       of 64 rows in flight in registers, LDS double buffer, the A slice
-//       resident in LDS, v_mfma_i32_16x16x64_i8 with M padded to 16 by zero
-//       rows. K slices are reduced by the last-arriving workgroup of each
-//       column slab (int32 partials in a workspace, device-scope counter).
+//       streams an NB-column slab of B exactly once over a K slice with
+//       non-temporal loads, U stages of 64 rows in flight in registers, LDS
+//       double buffer, the A slice resident in LDS, v_mfma_i32_16x16x64_i8
+//       with M padded to 16. K slices write int32 partials to a workspace and
+//       skinny_reduce_kernel, next on the same stream, adds them (and D).
 //   generic_kernel  any shape, stride or alignment; one thread per output,
 //       int32 VALU. Used where the vector kernels' alignment rules fail.
 //
@@ -86,12 +92,17 @@ __device__ __forceinline__ int32_t add_wrap(int32_t a, int32_t b) {
   return (int32_t)((uint32_t)a + (uint32_t)b);
 }
 
-// LDS swizzles. gfx950's LDS serves 256 bytes per cycle (64 banks of 4 bytes):
-// 16 lanes of a 16-byte access or 32 lanes of an 8-byte access. The swizzles
-// below keep every such group on distinct banks, and also every half group
-// (the 128-byte case), for the access patterns of the kernels:
-//   A slice [m][64 B], ds_read_b128 of one 16-byte chunk from 16 consecutive
-//     rows: chunk c of row r is stored at c ^ (((r >> 1) ^ (r >> 3)) & 3);
+// LDS swizzles. gfx950's LDS has 64 banks of 4 bytes (256 bytes per cycle).
+// Measured lane grouping (one bank cycle each, conflict-free only if the
+// group's addresses fall on distinct banks):
+//   ds_read_b128: four groups of 16 lanes, lane L in group
+//     parity((L >> 2) & 7) + 2 * (L >> 5), e.g. {0-3, 12-15, 20-27};
+//   ds_read_b64 / ds_read_b64_tr_b8: lanes 0-31 and lanes 32-63.
+// The swizzles below keep every group on distinct banks for the access
+// patterns of the kernels:
+//   A slice [m][64 B], ds_read_b128 of one 16-byte chunk from 32 consecutive
+//     rows: chunk c of row r is stored at c ^ ((r >> 2) & 3), which gives the
+//     four rows of equal r % 4 within each lane group four distinct chunks;
 //   B slice [k][n], ds_read_b64_tr_b8 of 8 consecutive rows by 16 lanes, two
 //     16-lane groups reading adjacent chunks (c, c ^ 1) of the same rows:
 //     chunk c of row r is stored at c ^ b_swz(r).
@@ -103,13 +114,18 @@ __device__ __forceinline__ int b_swz(int row) {
   return (row >> 1) & 3;
 }
 
+__device__ __forceinline__ int a_swz(int row) { return (row >> 2) & 3; }
+
 __device__ __forceinline__ int a_off(int row, int c) {
-  return row * 64 + ((c ^ (((row >> 1) ^ (row >> 3)) & 3)) << 4);
+  return row * 64 + ((c ^ a_swz(row)) << 4);
 }
 
 // Epilogue shared by the MFMA kernels. 32x32 accumulator layout: element e
 // of lane l is row 8*(e/4) + 4*(l/32) + e%4 and column l%32 of the block, so
-// one store instruction writes two full 128-byte row segments of C.
+// one store instruction writes two full 128-byte row segments of C. C is
+// written with non-temporal stores: every CU reaches a tile end at about the
+// same time, and streaming the whole C tile out keeps that burst from
+// displacing the A/B panels the L2 still serves.
 template <int MI, int NI, bool EDGE, bool HAS_D>
 __device__ __forceinline__ void store_tile(const v16i (&acc)[MI][NI], int32_t *Cb,
                                            const int32_t *Db, int64_t ldc, int64_t ldd,
@@ -125,7 +141,7 @@ __device__ __forceinline__ void store_tile(const v16i (&acc)[MI][NI], int32_t *C
         if (!EDGE || (row < M && col < N)) {
           int32_t v = acc[mi][ni][e];
           if (HAS_D) v = add_wrap(v, Db[(int64_t)row * ldd + col]);
-          Cb[(int64_t)row * ldc + col] = v;
+          __builtin_nontemporal_store(v, Cb + (int64_t)row * ldc + col);
         }
       }
     }
@@ -447,7 +463,7 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(GemmArgs p) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int arow = (wave * 4 + i) * 16 + (lane >> 2);
-    const int ac = (lane & 3) ^ (((arow >> 1) ^ (arow >> 3)) & 3);
+    const int ac = (lane & 3) ^ a_swz(arow);
     a_lane[i] = (uint32_t)((int64_t)arow * lda + ac * 16);
     const int brow = (wave * 4 + i) * 4 + (lane >> 4);
     const int bc = (lane & 15) ^ b_swz<BCH>(brow);
@@ -540,41 +556,34 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(GemmArgs p) {
 
   int gs = 0;   // global slice index
   for (int it = 0; it < ntiles; ++it) {
-    // Explicit schedule, one MFMA per scheduling region (in fragment read
-    // order, so each MFMA waits only for its own operands), each followed by
-    // two fragment reads or one DMA.
+    // Explicit schedule over the 32 MFMA slots of a slice, one MFMA per
+    // scheduling region: slots 0-15 multiply the k 0..31 fragments of slice
+    // gs while the k 32..63 fragments of slice gs are read (one per slot, in
+    // the order the next slots need them); slots 16-31 multiply those while
+    // the k 0..31 fragments of slice gs+1 (published by the previous barrier)
+    // are read. The eight DMAs of slice gs+3 go out one every four slots so
+    // the memory pipeline sees a steady stream instead of a burst.
     for (int kt = 0; kt < KT; ++kt, ++gs) {
       const int s0 = gs & 3, s1 = (gs + 1) & 3, s3 = (gs + 3) & 3;
       const int8_t *abase, *bbase;
       next_bases(abase, bbase);   // slice gs+3
       const uint32_t ma = lds0 + s3 * STAGE + wave * 4 * 1024;
       const uint32_t mb = ma + A_BYTES;
-      // First half step: MFMAs of k 0..31 (slice gs); the k 32..63 fragments
-      // of slice gs and the DMA of slice gs+3 go out between them.
+      constexpr int kNeed[NUNIT] = {0, 4, 5, 6, 7, 8, 9, 10, 11, 1, 2, 3};
 #pragma unroll
-      for (int i = 0; i < MI * NI; ++i) {
-        mfma(i / NI, i % NI, fa0, fl0, fh0);
-        if (i < NUNIT / 2) {
-          read_unit(s0, 1, 2 * i, fa1, fl1, fh1);
-          read_unit(s0, 1, 2 * i + 1, fa1, fl1, fh1);
-        } else if (i - NUNIT / 2 < 4) {
-          const int d = i - NUNIT / 2;
-          dma_b128(abase, a_lane[d], ma + d * 1024);
-        } else if (i - NUNIT / 2 < 8) {
-          const int d = i - NUNIT / 2 - 4;
-          dma_b128(bbase, b_lane[d], mb + d * 1024);
+      for (int slot = 0; slot < 2 * MI * NI; ++slot) {
+        const int i = slot % (MI * NI);
+        if (slot < MI * NI) {
+          mfma(i / NI, i % NI, fa0, fl0, fh0);
+          if (i < NUNIT) read_unit(s0, 1, kNeed[i], fa1, fl1, fh1);
+        } else {
+          mfma(i / NI, i % NI, fa1, fl1, fh1);
+          if (i < NUNIT) read_unit(s1, 0, kNeed[i], fa0, fl0, fh0);
         }
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      // Second half step: MFMAs of k 32..63; slice gs+1's first fragments
-      // (published by the previous barrier) go out between them. All reads
-      // of stage s0 were issued above, ahead of these reads of stage s1.
-#pragma unroll
-      for (int i = 0; i < MI * NI; ++i) {
-        mfma(i / NI, i % NI, fa1, fl1, fh1);
-        if (i < NUNIT / 2) {
-          read_unit(s1, 0, 2 * i, fa0, fl0, fh0);
-          read_unit(s1, 0, 2 * i + 1, fa0, fl0, fh0);
+        if ((slot & 3) == 2) {
+          const int d = slot >> 2;
+          if (d < 4) dma_b128(abase, a_lane[d], ma + d * 1024);
+          else dma_b128(bbase, b_lane[d - 4], mb + (d - 4) * 1024);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -601,6 +610,21 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(GemmArgs p) {
 // ---------------------------------------------------------------------------
 // Skinny (decode) kernels: M <= 16
 // ---------------------------------------------------------------------------
+
+// Row pitch of the LDS-resident A slice in the skinny kernel: a multiple of
+// 16 bytes that is 2 (mod 4) chunks, so the 16 rows x 4 chunks read by one
+// ds_read_b128 (lane l: row l % 16, chunk l / 16) land on distinct banks in
+// every lane group.
+__host__ __device__ __forceinline__ int skinny_a_stride(int k_chunk) {
+  return k_chunk + 16 * ((2 - (k_chunk >> 4)) & 3);
+}
+
+// B stage swizzle of the skinny kernel (rows of 16 chunks): lanes 0-31 of a
+// ds_read_b64_tr_b8 read rows r0 + 0..7 and r0 + 16..23 of one chunk, so the
+// swizzle gives those 16 rows 16 distinct chunk positions.
+__device__ __forceinline__ int skinny_b_swz(int row) {
+  return (row & 7) | (((row >> 4) & 1) << 3);
+}
 
 struct SkinnyArgs {
   const int8_t *A;
@@ -630,9 +654,10 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(SkinnyArgs p) {
   constexpr int KB = R / 64;                  // 64-row k-blocks per stage
   constexpr int STAGE_BYTES = R * NB;
   static_assert(KB * NBLK == WAVES && R % 64 == 0, "one MFMA per wave per stage");
+  static_assert(NBLK == 16, "skinny_b_swz assumes 256-byte stage rows");
 
   extern __shared__ __attribute__((aligned(16))) int8_t dsmem[];
-  const int a_stride = p.k_chunk + 16;        // +16 bytes: rows land in distinct banks
+  const int a_stride = skinny_a_stride(p.k_chunk);
   int8_t *const As = dsmem;
   int8_t *const Bs0 = dsmem + 16 * a_stride;  // stage buffer b at Bs0 + b*STAGE_BYTES
 
@@ -659,7 +684,7 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(SkinnyArgs p) {
 
   const int brow = tid / NBLK, bc = tid % NBLK;
   const int8_t *bsrc = Bb + min(n0 + bc * 16, N - 16);
-  const int b_lds = brow * NB + ((bc ^ b_swz<NBLK>(brow)) << 4);
+  const int b_lds = brow * NB + ((bc ^ skinny_b_swz(brow)) << 4);
   // Loads for stages >= T (issued by the last U stages) re-read the slice's
   // last row, which is resident in L2, and are discarded.
   const int krow_last = min(kbeg + p.k_chunk - 1, K - 1);
@@ -688,7 +713,7 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(SkinnyArgs p) {
   const int g = lane >> 4, j = lane & 15;
   const int nblk = wave % NBLK, kb = wave / NBLK;
   const int r0 = kb * 64 + g * 16 + (j >> 1);
-  const int b_frag = r0 * NB + ((nblk ^ b_swz<NBLK>(r0)) << 4) + (j & 1) * 8;
+  const int b_frag = r0 * NB + ((nblk ^ skinny_b_swz(r0)) << 4) + (j & 1) * 8;
   const int a_frag = (lane & 15) * a_stride + kb * 64 + g * 16;
 
   v4i acc = v4i{0, 0, 0, 0};
@@ -1034,10 +1059,10 @@ int launch_skinny_cfg(const Problem &q, int k_split, DeviceState *st, void *stre
   // count it implies; shrink slices whose A part would not fit in LDS.
   int64_t chunk = (q.K + k_split - 1) / k_split;
   chunk = (chunk + kAlign - 1) / kAlign * kAlign;
-  int64_t lds = 16 * (chunk + 16) + kStageLds;
+  int64_t lds = 16 * (int64_t)skinny_a_stride((int)chunk) + kStageLds;
   if (lds > kMaxSkinnyLds) {
-    chunk = ((kMaxSkinnyLds - kStageLds) / 16 - 16) / kAlign * kAlign;
-    lds = 16 * (chunk + 16) + kStageLds;
+    chunk = ((kMaxSkinnyLds - kStageLds) / 16 - 48) / kAlign * kAlign;
+    lds = 16 * (int64_t)skinny_a_stride((int)chunk) + kStageLds;
   }
   const int ks = (int)((q.K + chunk - 1) / chunk);
   SkinnyArgs a;

@@ -88,9 +88,15 @@ def skinny_split(plan):
     stage_lds = TILES["skinny"][4]
     chunk = -(-k // ks)
     chunk = -(-chunk // align) * align
-    if 16 * (chunk + 16) + stage_lds > LDS_PER_CU:
-        chunk = ((LDS_PER_CU - stage_lds) // 16 - 16) // align * align
+    if 16 * skinny_a_stride(chunk) + stage_lds > LDS_PER_CU:
+        chunk = ((LDS_PER_CU - stage_lds) // 16 - 48) // align * align
     return -(-k // chunk), chunk
+
+
+def skinny_a_stride(k_chunk):
+    """LDS row pitch of the skinny kernel's A slice (skinny_a_stride in the
+    HIP source): k_chunk padded to 2 (mod 4) 16-byte chunks."""
+    return k_chunk + 16 * ((2 - (k_chunk >> 4)) & 3)
 
 
 def _auto_k_split(n, k, batch):
@@ -118,7 +124,7 @@ def required_resources(plan):
         return lds, -(-m // tm) * -(-n // tn) * batch
     if variant == "skinny":
         ks, chunk = skinny_split(plan)
-        return lds + 16 * (chunk + 16), -(-n // tn) * ks * batch
+        return lds + 16 * skinny_a_stride(chunk), -(-n // tn) * ks * batch
     return 0, -(-n // tn) * min(-(-m // tm), 65535) * min(batch, 65535)
 
 
