@@ -410,19 +410,29 @@ __device__ __forceinline__ void dma_b128(const int8_t *base, uint32_t voff, uint
 // read in step g-1). The wait at the end of step g (vmcnt(8): only slice
 // g+3's eight DMAs per wave may still be in flight) plus the barrier publish
 // slice g+2 before step g+1 reads its fragments early.
-template <bool HAS_D>
-__global__ __launch_bounds__(256, 1) void gemm_dma_kernel(GemmArgs p) {
+//
+// WAVES = 4: one wave per SIMD, each owning a 128x128 block (2x2 layout).
+// WAVES = 8: two waves per SIMD, each owning a 128x64 block (2 rows x 4
+// columns of waves), so while one wave of a SIMD waits (a DMA the memory
+// pipeline cannot take yet, a C store burst) the other keeps its MFMA pipe
+// busy; fragment reads per MFMA rise by a third.
+template <int WAVES, bool HAS_D>
+__global__ __launch_bounds__(64 * WAVES, 1) void gemm_dma_kernel(GemmArgs p) {
+  static_assert(WAVES == 4 || WAVES == 8, "4 or 8 waves");
   constexpr int BM = 256, BN = 256, BK = 64;
-  constexpr int WTM = BM / 2, WTN = BN / 2, MI = WTM / 32, NI = WTN / 32;
+  constexpr int WTM = 128, WTN = WAVES == 4 ? 128 : 64, MI = WTM / 32, NI = WTN / 32;
   constexpr int BCH = BN / 16;
   constexpr int A_BYTES = BM * BK, B_BYTES = BK * BN, STAGE = A_BYTES + B_BYTES;
   constexpr int NSTAGE = 4;
+  constexpr int DPW = 16 / WAVES;        // 1 KB DMA blocks of A (and of B) per wave per slice
+  constexpr int DMAS = 2 * DPW;          // DMAs per wave per slice
   __shared__ __attribute__((aligned(1024))) int8_t smem[NSTAGE * STAGE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = WAVES == 4 ? wave >> 1 : wave & 1;
+  const int wn = WAVES == 4 ? wave & 1 : wave >> 1;
 
   // This workgroup computes logical tiles wl, wl + G, wl + 2G, ... where wl
   // is its XCD-contiguous rank (workgroup w runs on XCD w % 8), so the tiles
@@ -454,18 +464,19 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(GemmArgs p) {
   const int KT = p.K / BK;
   const int last_g = ntiles * KT - 1;
 
-  // DMA sources. Wave w fills A blocks 4w..4w+3 (16 rows of 64 bytes each)
-  // and B blocks 4w..4w+3 (4 rows of 256 bytes each); lane L lands at byte
-  // 16*L of its block, so it fetches the logical chunk that the swizzle maps
-  // to that position (XOR swizzles are their own inverse). Lane offsets are
-  // relative to the tile's origin, which goes into the wave-uniform base.
-  uint32_t a_lane[4], b_lane[4];
+  // DMA sources. Wave w fills A blocks DPW*w .. DPW*w+DPW-1 (16 rows of 64
+  // bytes each) and the same B blocks (4 rows of 256 bytes each); lane L lands
+  // at byte 16*L of its block, so it fetches the logical chunk that the
+  // swizzle maps to that position (XOR swizzles are their own inverse). Lane
+  // offsets are relative to the tile's origin, which goes into the
+  // wave-uniform base.
+  uint32_t a_lane[DPW], b_lane[DPW];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int arow = (wave * 4 + i) * 16 + (lane >> 2);
+  for (int i = 0; i < DPW; ++i) {
+    const int arow = (wave * DPW + i) * 16 + (lane >> 2);
     const int ac = (lane & 3) ^ a_swz(arow);
     a_lane[i] = (uint32_t)((int64_t)arow * lda + ac * 16);
-    const int brow = (wave * 4 + i) * 4 + (lane >> 4);
+    const int brow = (wave * DPW + i) * 4 + (lane >> 4);
     const int bc = (lane & 15) ^ b_swz<BCH>(brow);
     b_lane[i] = (uint32_t)((int64_t)brow * ldb + bc * 16);
   }
@@ -494,12 +505,12 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(GemmArgs p) {
   auto issue_slice = [&](int stage) {
     const int8_t *abase, *bbase;
     next_bases(abase, bbase);
-    const uint32_t ma = lds0 + stage * STAGE + wave * 4 * 1024;
+    const uint32_t ma = lds0 + stage * STAGE + wave * DPW * 1024;
     const uint32_t mb = ma + A_BYTES;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dma_b128(abase, a_lane[i], ma + i * 1024);
+    for (int i = 0; i < DPW; ++i) dma_b128(abase, a_lane[i], ma + i * 1024);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dma_b128(bbase, b_lane[i], mb + i * 1024);
+    for (int i = 0; i < DPW; ++i) dma_b128(bbase, b_lane[i], mb + i * 1024);
   };
 
   const int g = lane >> 4, j = lane & 15;
@@ -524,11 +535,11 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(GemmArgs p) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[mi][ni][e] = 0;
 
-  // Fragments of one 32-deep k step as 12 LDS reads ("units"): units 0..3
-  // are the A blocks (ds_read_b128), units 4..11 the lo/hi halves of the B
-  // blocks (ds_read_b64_tr_b8).
+  // Fragments of one 32-deep k step as MI + 2*NI LDS reads ("units"): units
+  // 0..MI-1 are the A blocks (ds_read_b128), the rest the lo/hi halves of the
+  // B blocks (ds_read_b64_tr_b8).
   constexpr int NUNIT = MI + 2 * NI;
-  static_assert(NUNIT == 12, "the barrier wait count assumes 12 fragment reads");
+  static_assert(NUNIT <= 15, "the barrier's lgkmcnt counts one k step of reads");
   v4i fa0[MI], fa1[MI];
   v2i fl0[NI], fh0[NI], fl1[NI], fh1[NI];
   auto read_unit = [&](int stage, int ks, int u, v4i *fa, v2i *fl, v2i *fh) {
@@ -550,7 +561,7 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(GemmArgs p) {
   issue_slice(0);
   issue_slice(1);
   issue_slice(2);
-  asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");   // slices 0, 1 landed
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" :: "n"(DMAS) : "memory");   // slices 0, 1 landed
 #pragma unroll
   for (int u = 0; u < NUNIT; ++u) read_unit(0, 0, u, fa0, fl0, fh0);
 
@@ -561,37 +572,37 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(GemmArgs p) {
     // gs while the k 32..63 fragments of slice gs are read (one per slot, in
     // the order the next slots need them); slots 16-31 multiply those while
     // the k 0..31 fragments of slice gs+1 (published by the previous barrier)
-    // are read. The eight DMAs of slice gs+3 go out one every four slots so
-    // the memory pipeline sees a steady stream instead of a burst.
+    // are read. The DMAs of slice gs+3 go out one every four slots so the
+    // memory pipeline sees a steady stream instead of a burst.
     for (int kt = 0; kt < KT; ++kt, ++gs) {
       const int s0 = gs & 3, s1 = (gs + 1) & 3, s3 = (gs + 3) & 3;
       const int8_t *abase, *bbase;
       next_bases(abase, bbase);   // slice gs+3
-      const uint32_t ma = lds0 + s3 * STAGE + wave * 4 * 1024;
+      const uint32_t ma = lds0 + s3 * STAGE + wave * DPW * 1024;
       const uint32_t mb = ma + A_BYTES;
-      constexpr int kNeed[NUNIT] = {0, 4, 5, 6, 7, 8, 9, 10, 11, 1, 2, 3};
+      // Read order = first use: A0 and the B blocks (MFMAs 0..NI-1), then A1..
 #pragma unroll
       for (int slot = 0; slot < 2 * MI * NI; ++slot) {
         const int i = slot % (MI * NI);
         if (slot < MI * NI) {
           mfma(i / NI, i % NI, fa0, fl0, fh0);
-          if (i < NUNIT) read_unit(s0, 1, kNeed[i], fa1, fl1, fh1);
+          if (i < NUNIT) read_unit(s0, 1, i == 0 ? 0 : i <= 2 * NI ? MI + i - 1 : i - 2 * NI, fa1, fl1, fh1);
         } else {
           mfma(i / NI, i % NI, fa1, fl1, fh1);
-          if (i < NUNIT) read_unit(s1, 0, kNeed[i], fa0, fl0, fh0);
+          if (i < NUNIT) read_unit(s1, 0, i == 0 ? 0 : i <= 2 * NI ? MI + i - 1 : i - 2 * NI, fa0, fl0, fh0);
         }
         if ((slot & 3) == 2) {
           const int d = slot >> 2;
-          if (d < 4) dma_b128(abase, a_lane[d], ma + d * 1024);
-          else dma_b128(bbase, b_lane[d - 4], mb + (d - 4) * 1024);
+          if (d < DPW) dma_b128(abase, a_lane[d], ma + d * 1024);
+          else dma_b128(bbase, b_lane[d - DPW], mb + (d - DPW) * 1024);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
-      // Slice gs+2 has landed (only slice gs+3's eight DMAs per wave remain
-      // in flight; older stores are waited for as well) and every read of
-      // stage s0 has completed (only the 12 reads of stage s1 remain), so
-      // after the barrier step gs+1 may refill stage s0.
-      asm volatile("s_waitcnt vmcnt(8) lgkmcnt(12)\n\ts_barrier" ::: "memory");
+      // Slice gs+2 has landed (only slice gs+3's DMAs remain in flight; older
+      // stores are waited for as well) and every read of stage s0 has
+      // completed (only the NUNIT reads of stage s1 remain), so after the
+      // barrier step gs+1 may refill stage s0.
+      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(%1)\n\ts_barrier" :: "n"(DMAS), "n"(NUNIT) : "memory");
     }
     int bidx, m0, n0;
     tile_coords(it, bidx, m0, n0);
@@ -1005,6 +1016,9 @@ bool offsets_fit_32(const Problem &q, int64_t m_rows) {
   return a_span < (1ll << 32) - 4096 && b_span < (1ll << 32) - 4096;
 }
 
+// Waves per workgroup of the persistent full-tile kernel.
+constexpr int kDmaWaves = 4;
+
 template <int BM, int BN>
 int launch_mfma(const Problem &q, hipStream_t stream, int num_cus) {
   // Fold contiguous shared-B batches into one stacked-M GEMM.
@@ -1032,7 +1046,7 @@ int launch_mfma(const Problem &q, hipStream_t stream, int num_cus) {
     // Persistent: one workgroup per CU (the kernel's LDS allows no more).
     const int64_t g = blocks < num_cus ? blocks : num_cus;
     dim3 pgrid((unsigned)g);
-    hipLaunchKernelGGL(gemm_dma_kernel<false>, pgrid, block, 0, stream, a);
+    hipLaunchKernelGGL((gemm_dma_kernel<kDmaWaves, false>), pgrid, dim3(64 * kDmaWaves), 0, stream, a);
     VT_HIP_CHECK(hipGetLastError());
     return VT_OK;
   }
