@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define VT_ABI_VERSION 1
+#define VT_ABI_VERSION 2
 
 /* Status codes. */
 #define VT_OK 0
@@ -120,6 +120,49 @@ int vt_device_count(void);
 
 /* VT_ABI_VERSION of the loaded library. */
 int vt_abi_version(void);
+
+/*
+ * Gemmini command-stream replay.
+ *
+ * vt_replay_i8 executes a weight-stationary Gemmini command stream (the
+ * `commands` of a veritac_program_request_v1, specializations/gemmini_gemm/
+ * backend.py:891-936) on the GPU with the semantics of the reference's
+ * interpreter `run_commands` (backend.py:433-562): a scratchpad of int8 rows,
+ * an accumulator of int32 rows, mvin / compute / mvout tile moves, overwrite
+ * or accumulate into the accumulator, and rejection of int32 overflow. It
+ * replaces that interpreter's execution step; the stream's static checks
+ * (configuration order, address spaces, initialised reads, fences, every
+ * output written) run on the host first (specializations/hip_gemm/replay.py),
+ * which lowers the stream to the tile program below.
+ *
+ * program: device pointer to n_ops operations of 8 int32 words each,
+ *   { VT_REPLAY_MVIN,    buf (0 = A, 1 = B), offset, row stride, scratchpad row, -, -, index }
+ *   { VT_REPLAY_LATCH_B, scratchpad row, -, -, -, -, -, index }
+ *   { VT_REPLAY_COMPUTE, A scratchpad row, accumulator row, accumulate (0/1), -, -, -, index }
+ *   { VT_REPLAY_MVOUT,   accumulator row, C offset, C row stride, -, -, -, index }
+ *   (offsets and strides in elements; every tile is 16 x 16; `index` is the
+ *   position of the originating command, reported on failure).
+ * A int8 [m*k], B int8 [k*n], C int32 [m*n]: device pointers, row-major.
+ * status: device pointer to 4 int32 words the kernel fills with
+ *   { VT_REPLAY_STATUS_*, index, row, column } of the first failure, or zeros.
+ * Every operand address is bounds-checked on the device as well; an
+ * operation outside m, n, k or the scratchpad / accumulator sizes stops the
+ * replay with VT_REPLAY_STATUS_RANGE instead of touching memory.
+ * The scratchpad (16 bytes per row) and accumulator (64 bytes per row) live
+ * in LDS: scratchpad_rows * 16 + accumulator_rows * 64 <= 152 KiB.
+ */
+#define VT_REPLAY_MVIN 1
+#define VT_REPLAY_LATCH_B 2
+#define VT_REPLAY_COMPUTE 3
+#define VT_REPLAY_MVOUT 4
+#define VT_REPLAY_STATUS_OK 0
+#define VT_REPLAY_STATUS_OVERFLOW 1   /* int32 accumulator overflow         */
+#define VT_REPLAY_STATUS_RANGE 2      /* operand outside the declared sizes */
+#define VT_REPLAY_STATUS_OPCODE 3     /* unknown operation                  */
+
+int vt_replay_i8(const int32_t *program, int64_t n_ops, const int8_t *A, const int8_t *B,
+                 int32_t *C, int64_t m, int64_t n, int64_t k, int64_t scratchpad_rows,
+                 int64_t accumulator_rows, int32_t *status, void *stream);
 
 #ifdef __cplusplus
 }

@@ -19,6 +19,24 @@ def golden():
         return json.load(fh)
 
 
+@pytest.fixture(scope="session")
+def commands():
+    import json
+    with open(os.path.join(ROOT, "tests", "golden", "gemmini_commands.json")) as fh:
+        return json.load(fh)["streams"]
+
+
+def witness_inputs(stream):
+    """The recorded counterexample input of a rejection witness: flat int8
+    lists, all zero except the listed A / B indices, which are one."""
+    p = stream["plan"]
+    A = [0] * (p["m"] * p["k"])
+    B = [0] * (p["k"] * p["n"])
+    for buf, idx in stream["witness"]["sparse_inputs"]["ones"]:
+        (A if buf == "a" else B)[idx] = 1
+    return A, B
+
+
 def decode_cout(hex_text):
     """8 hex digits per int32 (run_raw_spike.py:409-423 parse rule)."""
     vals = []

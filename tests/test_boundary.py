@@ -27,7 +27,9 @@ def test_library_exports_every_declared_symbol():
     assert declared == sorted(_lib.EXPORTS)
     for name in declared:
         assert hasattr(lib, name), name
-    assert lib.vt_abi_version() == 1
+    header = open(os.path.join(ROOT, "include", "vt_hip_gemm.h")).read()
+    assert "#define VT_ABI_VERSION %d" % _lib.ABI_VERSION in header
+    assert lib.vt_abi_version() == _lib.ABI_VERSION
 
 
 def test_variant_table_matches_backend():
@@ -103,3 +105,36 @@ def test_missing_library_fails_closed(tmp_path, monkeypatch):
     monkeypatch.delenv("VT_HIP_GEMM_LIB")
     monkeypatch.setattr(_lib, "_lib", None)
     assert _lib.load_library() is not None
+
+
+REPLAY_OK = dict(prog=1 << 20, n_ops=1, A=1 << 21, B=1 << 22, C=1 << 23, m=16, n=16, k=16,
+                 sp=32, acc=16, status=1 << 24)
+
+
+@pytest.mark.parametrize("kw", [dict(m=0), dict(k=-16), dict(n_ops=-1), dict(sp=8), dict(acc=15),
+                                dict(A=None), dict(status=None), dict(prog=None),
+                                dict(m=1 << 20, k=1 << 20)])
+def test_replay_invalid_arguments_rejected_before_device(kw):
+    a = dict(REPLAY_OK, **kw)
+    lib = veritac_amd.load_library()
+    rc = lib.vt_replay_i8(a["prog"], a["n_ops"], a["A"], a["B"], a["C"], a["m"], a["n"], a["k"],
+                          a["sp"], a["acc"], a["status"], None)
+    assert rc == _lib.VT_EINVAL, _lib.last_error()
+
+
+def test_replay_refuses_a_scratchpad_beyond_lds():
+    a = dict(REPLAY_OK, sp=16384, acc=1024)
+    lib = veritac_amd.load_library()
+    rc = lib.vt_replay_i8(a["prog"], a["n_ops"], a["A"], a["B"], a["C"], a["m"], a["n"], a["k"],
+                          a["sp"], a["acc"], a["status"], None)
+    assert rc == _lib.VT_EUNSUPPORTED and "LDS" in _lib.last_error()
+
+
+def test_replay_fails_closed_without_gpu():
+    if _lib.device_count() > 0:
+        pytest.skip("a gfx950 device is present")
+    a = REPLAY_OK
+    with pytest.raises(_lib.HipGemmError) as exc:
+        _lib.replay_raw(a["prog"], a["n_ops"], a["A"], a["B"], a["C"], a["m"], a["n"], a["k"],
+                        a["sp"], a["acc"], a["status"])
+    assert exc.value.code == _lib.VT_ENODEV

@@ -14,7 +14,7 @@ import threading
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 DEFAULT_LIB = os.path.join(PKG_DIR, "libvt_hip_gemm.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 VT_OK = 0
 VT_EINVAL = -1
@@ -37,7 +37,12 @@ VARIANTS = tuple(VARIANT_IDS)
 
 # Every function include/vt_hip_gemm.h declares.
 EXPORTS = ("vt_gemm_i8", "vt_gemm_select", "vt_variant_info", "vt_variant_name",
-           "vt_last_error", "vt_sync", "vt_device_count", "vt_abi_version")
+           "vt_last_error", "vt_sync", "vt_device_count", "vt_abi_version", "vt_replay_i8")
+
+# Replay operation codes and status codes (VT_REPLAY_* in include/vt_hip_gemm.h).
+REPLAY_MVIN, REPLAY_LATCH_B, REPLAY_COMPUTE, REPLAY_MVOUT = 1, 2, 3, 4
+REPLAY_STATUS = {0: "ok", 1: "int32 accumulator overflow", 2: "operand out of range",
+                 3: "unknown operation"}
 
 
 class HipGemmError(RuntimeError):
@@ -74,6 +79,8 @@ def _declare(lib):
     lib.vt_sync.restype = ctypes.c_int
     lib.vt_device_count.argtypes = []
     lib.vt_device_count.restype = ctypes.c_int
+    lib.vt_replay_i8.argtypes = [p, i64, p, p, p, i64, i64, i64, i64, i64, p, p]
+    lib.vt_replay_i8.restype = ctypes.c_int
     lib.vt_abi_version.argtypes = []
     lib.vt_abi_version.restype = ctypes.c_int
 
@@ -152,3 +159,15 @@ def gemm_raw(A_ptr, B_ptr, D_ptr, C_ptr, M, N, K, lda, ldb, ldd, ldc, batch=1,
 
 def sync(stream=None):
     return check(load_library().vt_sync(stream), "vt_sync")
+
+
+def replay_raw(prog_ptr, n_ops, A_ptr, B_ptr, C_ptr, m, n, k, scratchpad_rows,
+               accumulator_rows, status_ptr, stream=None):
+    """One vt_replay_i8 call on raw device pointers (integers); raises on failure.
+
+    The device-side outcome is written to the 4-word status buffer; read it
+    after synchronizing the stream.
+    """
+    lib = load_library()
+    check(lib.vt_replay_i8(prog_ptr, n_ops, A_ptr, B_ptr, C_ptr, m, n, k, scratchpad_rows,
+                           accumulator_rows, status_ptr, stream), "vt_replay_i8")

@@ -844,6 +844,85 @@ __global__ __launch_bounds__(256) void generic_kernel(GenericArgs p) {
 }
 
 // ---------------------------------------------------------------------------
+// Gemmini command-stream replay
+// ---------------------------------------------------------------------------
+
+// One workgroup of 256 threads executes the lowered stream in order, one
+// 16 x 16 tile operation at a time (thread t owns element (t / 16, t % 16)),
+// with the scratchpad, the accumulator and the latched B tile in LDS and a
+// barrier between operations. Every address is checked against the declared
+// sizes before use; the first failure is recorded and ends the replay.
+struct ReplayArgs {
+  const int32_t *prog;
+  int n_ops;
+  const int8_t *A;
+  const int8_t *B;
+  int32_t *C;
+  int64_t size_a, size_b, size_c;
+  int spad_rows, acc_rows;
+  int32_t *status;
+};
+
+__global__ __launch_bounds__(256) void replay_kernel(ReplayArgs p) {
+  extern __shared__ __attribute__((aligned(16))) int8_t lds[];
+  int8_t *const spad = lds;                                            // [spad_rows][16]
+  int32_t *const acc = (int32_t *)(lds + (int64_t)p.spad_rows * 16);   // [acc_rows][16]
+  int8_t *const latch = (int8_t *)(acc + (int64_t)p.acc_rows * 16);   // [16][16]
+  __shared__ int err[4];
+  const int t = threadIdx.x, r = t >> 4, c = t & 15;
+  if (t == 0) err[0] = err[1] = err[2] = err[3] = 0;
+  __syncthreads();
+  auto fail_at = [&](int code, int index) {
+    if (atomicCAS(&err[0], 0, code) == 0) {
+      err[1] = index;
+      err[2] = r;
+      err[3] = c;
+    }
+  };
+  for (int i = 0; i < p.n_ops; ++i) {
+    const int32_t *w = p.prog + 8 * (int64_t)i;
+    const int op = w[0], index = w[7];
+    if (op == VT_REPLAY_MVIN) {
+      const int64_t off = w[2], stride = w[3];
+      const int row = w[4];
+      const int64_t size = w[1] ? p.size_b : p.size_a;
+      if (row < 0 || row > p.spad_rows - 16 || off < 0 || stride < 0 || off + 15 * stride + 16 > size)
+        fail_at(VT_REPLAY_STATUS_RANGE, index);
+      else
+        spad[(row + r) * 16 + c] = (w[1] ? p.B : p.A)[off + r * stride + c];
+    } else if (op == VT_REPLAY_LATCH_B) {
+      const int row = w[1];
+      if (row < 0 || row > p.spad_rows - 16) fail_at(VT_REPLAY_STATUS_RANGE, index);
+      else latch[t] = spad[row * 16 + t];
+    } else if (op == VT_REPLAY_COMPUTE) {
+      const int arow = w[1], orow = w[2];
+      if (arow < 0 || arow > p.spad_rows - 16 || orow < 0 || orow > p.acc_rows - 16) {
+        fail_at(VT_REPLAY_STATUS_RANGE, index);
+      } else {
+        int32_t s = 0;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) s += (int32_t)spad[(arow + r) * 16 + q] * (int32_t)latch[q * 16 + c];
+        const int64_t v = (int64_t)s + (w[3] ? acc[(orow + r) * 16 + c] : 0);
+        if (v < INT32_MIN || v > INT32_MAX) fail_at(VT_REPLAY_STATUS_OVERFLOW, index);
+        else acc[(orow + r) * 16 + c] = (int32_t)v;
+      }
+    } else if (op == VT_REPLAY_MVOUT) {
+      const int orow = w[1];
+      const int64_t off = w[2], ldc = w[3];
+      if (orow < 0 || orow > p.acc_rows - 16 || off < 0 || ldc < 16 || off + 15 * ldc + 16 > p.size_c)
+        fail_at(VT_REPLAY_STATUS_RANGE, index);
+      else
+        p.C[off + r * ldc + c] = acc[(orow + r) * 16 + c];
+    } else {
+      fail_at(VT_REPLAY_STATUS_OPCODE, index);
+    }
+    __syncthreads();
+    if (err[0]) break;
+  }
+  if (t < 4) p.status[t] = err[t];
+}
+
+// ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
 
@@ -885,6 +964,8 @@ const VariantInfo kVariants[VT_VARIANT_COUNT] = {
 // Default skinny configuration: 256-column slabs (full 128-byte lines of B
 // per row), 16 waves, 2 stages in flight per thread.
 constexpr int kSkinnyNB = 256, kSkinnyWaves = 16, kSkinnyU = 2;
+// LDS for the replay's scratchpad and accumulator (plus the latched B tile).
+constexpr int kMaxReplayLds = 152 * 1024;
 constexpr int kMaxSkinnyLds = 160 * 1024;
 
 struct Workspace {
@@ -1161,6 +1242,53 @@ int launch_generic(const Problem &q, hipStream_t stream) {
 extern "C" {
 
 int vt_abi_version(void) { return VT_ABI_VERSION; }
+
+int vt_replay_i8(const int32_t *program, int64_t n_ops, const int8_t *A, const int8_t *B,
+                 int32_t *C, int64_t m, int64_t n, int64_t k, int64_t scratchpad_rows,
+                 int64_t accumulator_rows, int32_t *status, void *stream) {
+  g_err.clear();
+  if (m <= 0 || n <= 0 || k <= 0 || n_ops < 0)
+    return fail(VT_EINVAL, "replay sizes must be positive (m=%lld n=%lld k=%lld ops=%lld)",
+                (long long)m, (long long)n, (long long)k, (long long)n_ops);
+  if (m * k > INT32_MAX || k * n > INT32_MAX || m * n > INT32_MAX || n_ops > (1 << 28))
+    return fail(VT_EINVAL, "replay extents beyond the int32 indexing range");
+  if (scratchpad_rows < 16 || accumulator_rows < 16)
+    return fail(VT_EINVAL, "scratchpad and accumulator need at least 16 rows");
+  if (scratchpad_rows * 16 + accumulator_rows * 64 > kMaxReplayLds)
+    return fail(VT_EUNSUPPORTED,
+                "scratchpad (%lld rows) and accumulator (%lld rows) exceed the %d-byte LDS budget",
+                (long long)scratchpad_rows, (long long)accumulator_rows, kMaxReplayLds);
+  if (!A || !B || !C || !status || (n_ops > 0 && !program))
+    return fail(VT_EINVAL, "replay pointer is null");
+  int dev = 0;
+  DeviceState *st = nullptr;
+  int rc = current_device(&dev, &st);
+  if (rc) return rc;
+  static std::once_flag lds_attr_once;
+  static hipError_t attr_err = hipSuccess;
+  std::call_once(lds_attr_once, [&] {
+    attr_err = hipFuncSetAttribute((const void *)replay_kernel,
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, kMaxReplayLds + 256);
+  });
+  if (attr_err != hipSuccess)
+    return fail(VT_EHIP, "hipFuncSetAttribute(replay LDS) failed: %s", hipGetErrorString(attr_err));
+  ReplayArgs a;
+  a.prog = program;
+  a.n_ops = (int)n_ops;
+  a.A = A;
+  a.B = B;
+  a.C = C;
+  a.size_a = m * k;
+  a.size_b = k * n;
+  a.size_c = m * n;
+  a.spad_rows = (int)scratchpad_rows;
+  a.acc_rows = (int)accumulator_rows;
+  a.status = status;
+  const size_t lds = (size_t)(scratchpad_rows * 16 + accumulator_rows * 64 + 256);
+  hipLaunchKernelGGL(replay_kernel, dim3(1), dim3(256), lds, (hipStream_t)stream, a);
+  VT_HIP_CHECK(hipGetLastError());
+  return VT_OK;
+}
 
 const char *vt_last_error(void) { return g_err.c_str(); }
 
