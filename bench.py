@@ -79,23 +79,6 @@ def time_steps(plan, sets, steps, warmup, stream):
     return wall, durs
 
 
-def freivalds_check(A, B, C, trials=2, seed=0):
-    """Exact float64 check C.x == A.(B.x) on the GPU (all values are integers
-    below 2^53, so the products are exact); plus row/column checksums."""
-    import torch
-    g = torch.Generator(device=A.device)
-    g.manual_seed(seed)
-    Af, Bf, Cf = A.double(), B.double(), C.double()
-    ok = True
-    for _ in range(trials):
-        x = torch.randint(-3, 4, (B.shape[1],), device=A.device, generator=g).double()
-        ok &= bool(torch.equal(Cf @ x, Af @ (Bf @ x)))
-    ok &= bool(torch.equal(Cf.sum(0), Af.sum(0) @ Bf))
-    ok &= bool(torch.equal(Cf.sum(1), Af @ Bf.sum(1)))
-    del Af, Bf, Cf
-    return ok
-
-
 def cpu_baseline(A_np, B_np, budget_s=8.0):
     """Oracle C restatement (i-t-j order, OpenMP over rows) on a row sample."""
     from oracle import cref
@@ -219,6 +202,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode-shape figure")
     ap.add_argument("--variant", default="auto", help="kernel variant for the headline GEMM")
+    ap.add_argument("--provenance", default=None, metavar="PATH",
+                    help="write a hash-bound report of the last timed step's result to PATH")
     ap.add_argument("--workload", choices=("all", "gemm", "decode", "copy"), default="all",
                     help="all: the JSON line below; gemm / decode: only that kernel (for "
                          "profiler runs); copy: a plain 1 GiB device copy (counter calibration)")
@@ -232,6 +217,7 @@ def main():
     import torch
     from veritac_amd.specializations.hip_gemm import backend as hg
     from veritac_amd.specializations.hip_gemm import inputs
+    from veritac_amd.specializations.hip_gemm import verify
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
@@ -256,9 +242,20 @@ def main():
     avg_ms = statistics.mean(durs)
     achieved = ops / (avg_ms / 1e3) / 1e12
     log("parity check")
-    parity_ok = freivalds_check(sets[(args.warmup + args.steps - 1) % N_SETS][0],
-                                sets[(args.warmup + args.steps - 1) % N_SETS][1],
-                                sets[(args.warmup + args.steps - 1) % N_SETS][3])
+    last = sets[(args.warmup + args.steps - 1) % N_SETS]
+    check = verify.exact_check(last[0], last[1], last[3])
+    parity_ok = check["passed"]
+    if args.provenance:
+        from veritac_amd.specializations.hip_gemm import provenance
+        report = provenance.report_from_result(
+            plan, last[0], last[1], None, last[3],
+            inputs_description={"kind": "config_inputs", "config": 5, "seed": 0},
+            timing={"kernel_avg_ms": avg_ms, "kernel_min_ms": min(durs),
+                    "ms_per_step": ms_per_step, "steps": args.steps, "warmup": args.warmup})
+        with open(args.provenance, "w") as fh:
+            json.dump(report, fh, indent=2)
+            fh.write("\n")
+        log("provenance report %s (success=%s)" % (args.provenance, report["success"]))
     result = {
         "metric": METRIC,
         "value": ops / (ms_per_step / 1e3) / 1e12,
@@ -282,7 +279,8 @@ def main():
                      "traffic_split": TRAFFIC_GEMM_8192,
                      "kernel": "gemm_dma_kernel (256x256, persistent)", "kernel_avg_ms": avg_ms,
                      "kernel_min_ms": min(durs), "ops_per_launch": ops},
-        "parity": {"freivalds_and_checksums_exact": parity_ok},
+        "parity": {"exact_check_mod_2^32": parity_ok, "vectors": check["vectors"],
+                   "method": check["method"]},
     }
     del sets
     torch.cuda.empty_cache()

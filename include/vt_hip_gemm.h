@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define VT_ABI_VERSION 2
+#define VT_ABI_VERSION 3
 
 /* Status codes. */
 #define VT_OK 0
@@ -163,6 +163,49 @@ int vt_abi_version(void);
 int vt_replay_i8(const int32_t *program, int64_t n_ops, const int8_t *A, const int8_t *B,
                  int32_t *C, int64_t m, int64_t n, int64_t k, int64_t scratchpad_rows,
                  int64_t accumulator_rows, int32_t *status, void *stream);
+
+/*
+ * Device query for hardware profiles.
+ *
+ * vt_device_query fills `info` with what the HIP runtime reports for one
+ * device. It replaces the driver probe of the reference's hardware profile
+ * (Hardware/profile.py:180-265, `_probe_cuda`: cuDeviceGetName,
+ * cuDeviceGetAttribute, cuDeviceTotalMem_v2), which has no ROCm backend; the
+ * Python side (specializations/hip_gemm/provenance.py) normalises it into the
+ * same schema_version 1 profile. `supported` is 1 when the device's ISA is
+ * the one this library's code objects are built for (code_object_arch), the
+ * condition under which every other entry point runs on it.
+ *
+ * device: device ordinal, or -1 for the calling thread's current device.
+ * info_size: sizeof(vt_device_info) as the caller sees it; a mismatch
+ *   returns VT_EINVAL, so a binding built against another layout fails
+ *   instead of reading past the structure.
+ * Returns VT_ENODEV on a host without HIP devices, VT_EINVAL for a bad
+ * ordinal or pointer, VT_EHIP if the runtime refuses the query.
+ */
+typedef struct vt_device_info {
+  char name[256];                  /* marketing name ("AMD Instinct MI355X")   */
+  char arch[256];                  /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+  char code_object_arch[32];       /* ISA the library was compiled for        */
+  int64_t total_memory_bytes;      /* HBM capacity                             */
+  int64_t l2_cache_bytes;          /* L2 as the runtime reports it (per XCD)  */
+  int64_t lds_per_workgroup_bytes; /* largest LDS allocation of one workgroup */
+  int64_t lds_per_cu_bytes;        /* LDS of one compute unit                  */
+  int32_t compute_units;
+  int32_t wavefront_size;
+  int32_t max_threads_per_workgroup;
+  int32_t max_clock_khz;           /* peak engine clock                        */
+  int32_t memory_clock_khz;
+  int32_t memory_bus_width_bits;
+  int32_t pci_domain;
+  int32_t pci_bus;
+  int32_t pci_device;
+  int32_t hip_runtime_version;     /* hipRuntimeGetVersion                     */
+  int32_t hip_driver_version;      /* hipDriverGetVersion                      */
+  int32_t supported;               /* 1: arch matches code_object_arch         */
+} vt_device_info;
+
+int vt_device_query(int32_t device, vt_device_info *info, int64_t info_size);
 
 #ifdef __cplusplus
 }

@@ -26,6 +26,19 @@ def commands():
         return json.load(fh)["streams"]
 
 
+@pytest.fixture(scope="session")
+def output_digests():
+    import json
+    with open(os.path.join(ROOT, "tests", "golden", "output_digests.json")) as fh:
+        return json.load(fh)["runs"]
+
+
+def winner_stream(streams, run_name):
+    """The certified command stream of a recorded blind-search run."""
+    name = "blind_search/%s/certification/winner" % run_name
+    return next(s for s in streams if s["name"] == name)
+
+
 def witness_inputs(stream):
     """The recorded counterexample input of a rejection witness: flat int8
     lists, all zero except the listed A / B indices, which are one."""

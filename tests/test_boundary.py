@@ -138,3 +138,40 @@ def test_replay_fails_closed_without_gpu():
         _lib.replay_raw(a["prog"], a["n_ops"], a["A"], a["B"], a["C"], a["m"], a["n"], a["k"],
                         a["sp"], a["acc"], a["status"])
     assert exc.value.code == _lib.VT_ENODEV
+
+
+def test_device_info_layout_matches_the_header(tmp_path):
+    """The ctypes structure has the C compiler's size and field offsets."""
+    fields = [name for name, _ in _lib.DeviceInfo._fields_]
+    src = tmp_path / "layout.c"
+    src.write_text("#include <stddef.h>\n#include <stdio.h>\n#include \"vt_hip_gemm.h\"\n"
+                   "int main(void) {\n  printf(\"%zu\\n\", sizeof(vt_device_info));\n" +
+                   "".join('  printf("%%zu\\n", offsetof(vt_device_info, %s));\n' % f
+                           for f in fields) + "  return 0;\n}\n")
+    exe = tmp_path / "layout"
+    import subprocess
+    subprocess.run(["gcc", "-std=c99", "-I", os.path.join(ROOT, "include"), str(src), "-o",
+                    str(exe)], check=True)
+    out = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True,
+                                          check=True).stdout.split()]
+    assert out[0] == ctypes.sizeof(_lib.DeviceInfo)
+    assert out[1:] == [getattr(_lib.DeviceInfo, f).offset for f in fields]
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    body = re.search(r"typedef struct vt_device_info \{(.*?)\}", text, flags=re.S).group(1)
+    assert re.findall(r"(\w+)(?:\[\d+\])?;", body) == fields
+
+
+def test_device_query_validates_before_the_runtime():
+    lib = veritac_amd.load_library()
+    info = _lib.DeviceInfo()
+    assert lib.vt_device_query(-1, None, ctypes.sizeof(info)) == _lib.VT_EINVAL
+    assert lib.vt_device_query(-1, ctypes.byref(info), ctypes.sizeof(info) - 8) == _lib.VT_EINVAL
+    assert "info_size" in _lib.last_error()
+
+
+def test_device_query_fails_closed_without_gpu():
+    if _lib.device_count() > 0:
+        pytest.skip("a gfx950 device is present")
+    with pytest.raises(_lib.HipGemmError) as exc:
+        _lib.device_query()
+    assert exc.value.code == _lib.VT_ENODEV

@@ -14,7 +14,7 @@ import threading
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 DEFAULT_LIB = os.path.join(PKG_DIR, "libvt_hip_gemm.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 VT_OK = 0
 VT_EINVAL = -1
@@ -37,12 +37,38 @@ VARIANTS = tuple(VARIANT_IDS)
 
 # Every function include/vt_hip_gemm.h declares.
 EXPORTS = ("vt_gemm_i8", "vt_gemm_select", "vt_variant_info", "vt_variant_name",
-           "vt_last_error", "vt_sync", "vt_device_count", "vt_abi_version", "vt_replay_i8")
+           "vt_last_error", "vt_sync", "vt_device_count", "vt_abi_version", "vt_replay_i8",
+           "vt_device_query")
 
 # Replay operation codes and status codes (VT_REPLAY_* in include/vt_hip_gemm.h).
 REPLAY_MVIN, REPLAY_LATCH_B, REPLAY_COMPUTE, REPLAY_MVOUT = 1, 2, 3, 4
 REPLAY_STATUS = {0: "ok", 1: "int32 accumulator overflow", 2: "operand out of range",
                  3: "unknown operation"}
+
+
+class DeviceInfo(ctypes.Structure):
+    """vt_device_info of include/vt_hip_gemm.h (field for field)."""
+    _fields_ = [
+        ("name", ctypes.c_char * 256),
+        ("arch", ctypes.c_char * 256),
+        ("code_object_arch", ctypes.c_char * 32),
+        ("total_memory_bytes", ctypes.c_int64),
+        ("l2_cache_bytes", ctypes.c_int64),
+        ("lds_per_workgroup_bytes", ctypes.c_int64),
+        ("lds_per_cu_bytes", ctypes.c_int64),
+        ("compute_units", ctypes.c_int32),
+        ("wavefront_size", ctypes.c_int32),
+        ("max_threads_per_workgroup", ctypes.c_int32),
+        ("max_clock_khz", ctypes.c_int32),
+        ("memory_clock_khz", ctypes.c_int32),
+        ("memory_bus_width_bits", ctypes.c_int32),
+        ("pci_domain", ctypes.c_int32),
+        ("pci_bus", ctypes.c_int32),
+        ("pci_device", ctypes.c_int32),
+        ("hip_runtime_version", ctypes.c_int32),
+        ("hip_driver_version", ctypes.c_int32),
+        ("supported", ctypes.c_int32),
+    ]
 
 
 class HipGemmError(RuntimeError):
@@ -81,6 +107,8 @@ def _declare(lib):
     lib.vt_device_count.restype = ctypes.c_int
     lib.vt_replay_i8.argtypes = [p, i64, p, p, p, i64, i64, i64, i64, i64, p, p]
     lib.vt_replay_i8.restype = ctypes.c_int
+    lib.vt_device_query.argtypes = [i32, ctypes.POINTER(DeviceInfo), i64]
+    lib.vt_device_query.restype = ctypes.c_int
     lib.vt_abi_version.argtypes = []
     lib.vt_abi_version.restype = ctypes.c_int
 
@@ -171,3 +199,17 @@ def replay_raw(prog_ptr, n_ops, A_ptr, B_ptr, C_ptr, m, n, k, scratchpad_rows,
     lib = load_library()
     check(lib.vt_replay_i8(prog_ptr, n_ops, A_ptr, B_ptr, C_ptr, m, n, k, scratchpad_rows,
                            accumulator_rows, status_ptr, stream), "vt_replay_i8")
+
+
+def device_query(device=-1):
+    """vt_device_query as a dict of plain values; raises HipGemmError on refusal
+    (VT_ENODEV on a host without HIP devices)."""
+    lib = load_library()
+    info = DeviceInfo()
+    check(lib.vt_device_query(device, ctypes.byref(info), ctypes.sizeof(info)),
+          "vt_device_query")
+    out = {}
+    for name, _ in DeviceInfo._fields_:
+        v = getattr(info, name)
+        out[name] = v.decode("utf-8", "replace") if isinstance(v, bytes) else int(v)
+    return out

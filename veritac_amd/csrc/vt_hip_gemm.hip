@@ -1335,6 +1335,49 @@ int vt_device_count(void) {
   return n;
 }
 
+static_assert(sizeof(vt_device_info) == 624, "vt_device_info layout is part of the ABI");
+
+int vt_device_query(int32_t device, vt_device_info *info, int64_t info_size) {
+  if (info == nullptr) return fail(VT_EINVAL, "vt_device_query: info is NULL");
+  if (info_size != (int64_t)sizeof(vt_device_info))
+    return fail(VT_EINVAL, "vt_device_query: info_size %lld != sizeof(vt_device_info) %zu",
+                (long long)info_size, sizeof(vt_device_info));
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess || count <= 0)
+    return fail(VT_ENODEV, "no HIP device available");
+  int dev = device;
+  if (dev < 0) VT_HIP_CHECK(hipGetDevice(&dev));
+  if (dev >= count)
+    return fail(VT_EINVAL, "vt_device_query: device %d of %d", dev, count);
+  hipDeviceProp_t prop;
+  VT_HIP_CHECK(hipGetDeviceProperties(&prop, dev));
+  memset(info, 0, sizeof *info);
+  snprintf(info->name, sizeof info->name, "%s", prop.name);
+  snprintf(info->arch, sizeof info->arch, "%s", prop.gcnArchName);
+  snprintf(info->code_object_arch, sizeof info->code_object_arch, "%s", "gfx950");
+  info->total_memory_bytes = (int64_t)prop.totalGlobalMem;
+  info->l2_cache_bytes = prop.l2CacheSize;
+  info->lds_per_workgroup_bytes = (int64_t)(prop.sharedMemPerBlockOptin > prop.sharedMemPerBlock
+                                                ? prop.sharedMemPerBlockOptin
+                                                : prop.sharedMemPerBlock);
+  info->lds_per_cu_bytes = (int64_t)prop.maxSharedMemoryPerMultiProcessor;
+  info->compute_units = prop.multiProcessorCount;
+  info->wavefront_size = prop.warpSize;
+  info->max_threads_per_workgroup = prop.maxThreadsPerBlock;
+  info->max_clock_khz = prop.clockRate;
+  info->memory_clock_khz = prop.memoryClockRate;
+  info->memory_bus_width_bits = prop.memoryBusWidth;
+  info->pci_domain = prop.pciDomainID;
+  info->pci_bus = prop.pciBusID;
+  info->pci_device = prop.pciDeviceID;
+  VT_HIP_CHECK(hipRuntimeGetVersion(&info->hip_runtime_version));
+  VT_HIP_CHECK(hipDriverGetVersion(&info->hip_driver_version));
+  // gcnArchName carries target features after the ISA name ("gfx950:sramecc+:xnack-").
+  const size_t isa = strcspn(prop.gcnArchName, ":");
+  info->supported = isa == 6 && strncmp(prop.gcnArchName, "gfx950", 6) == 0;
+  return VT_OK;
+}
+
 int vt_sync(void *stream) {
   int count = 0;
   if (hipGetDeviceCount(&count) != hipSuccess || count <= 0)
