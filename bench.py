@@ -7,8 +7,10 @@ M = N = K = 8192, int8 inputs with half the entries fixed at -128 or 127 and
 the rest uniform, int32 output. One step = one GEMM launch over one batch of
 synthetic input already resident in HBM. The timed steps cycle through
 5 distinct input/output sets (1.9 GB) so no launch finds its operands in the
-256 MB Infinity Cache. Secondary figure: the M=16 x K=4096 x N=14336 decode
-GEMM (configuration 4) in GB/s of algorithmic traffic.
+256 MB Infinity Cache. Secondary figures: the M=16 x K=4096 x N=14336 decode
+GEMM (configuration 4) in GB/s of algorithmic traffic, once with row-major B
+and once with B prepacked by vt_pack_b_i8 (the pack is timed on its own and
+is not part of the steps).
 
 Prints ONE JSON line with the metric, the roofline of the dominant kernel
 (average launch duration from HIP events recorded on the launch stream), a
@@ -38,6 +40,7 @@ N_SETS = 5
 # 1 GiB copy gives). Update them with the kernels.
 TRAFFIC_GEMM_8192 = {"read": 805.6e6, "written": 269.9e6}
 TRAFFIC_DECODE_M16 = {"read": 58.9e6 + 3.7e6, "written": 3.7e6 + 0.92e6}
+TRAFFIC_DECODE_PACKED_M16 = {"read": 59.3e6, "written": 0.92e6}
 
 
 def log(*a):
@@ -115,10 +118,14 @@ def cpu_baseline(A_np, B_np, budget_s=8.0):
     }
 
 
-def bench_decode(dev, steps, warmup):
+def bench_decode(dev, steps, warmup, packed=False):
     """Decode-shaped GEMM (config 4, M=16): `steps` launches captured in one
-    HIP graph (launch overhead would otherwise dominate a ~15 us kernel) and
-    replayed; the launches cycle through 6 buffer sets (> 256 MB)."""
+    HIP graph (launch overhead would otherwise dominate a ~10-15 us kernel)
+    and replayed; the launches cycle through 6 buffer sets (> 256 MB).
+
+    packed=False: row-major B (vt_gemm_i8, skinny variant). packed=True: the
+    same B packed once per set by pack_b (vt_pack_b_i8, timed separately and
+    outside the graph) and multiplied by vt_gemm_i8_packed."""
     import numpy as np
     import torch
     from veritac_amd.specializations.hip_gemm import backend as hg
@@ -126,9 +133,27 @@ def bench_decode(dev, steps, warmup):
     c = inputs.config_inputs(4, seed=0, m=16)
     A = torch.from_numpy(c["A"]).to(dev)
     B = torch.from_numpy(c["B"]).to(dev)
-    plan = hg.make_plan(16, 14336, 4096)
     sets = make_sets(dev, A, B, None, (16, 14336), N_SETS + 1)
     stream = torch.cuda.Stream(dev)
+    pack_ms = None
+    if packed:
+        plan = hg.make_plan(16, 14336, 4096, variant=hg.PACKED_VARIANT)
+        packs = [hg.pack_b(s[1], stream=stream.cuda_stream) for s in sets]
+        stream.synchronize()
+        # the one-time pack, timed on its own: repack every set in place
+        times = []
+        for s, pb in zip(sets, packs):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            hg.pack_b(s[1], out=pb, stream=stream.cuda_stream)
+            e1.record(stream)
+            stream.synchronize()
+            times.append(e0.elapsed_time(e1))
+        pack_ms = statistics.median(times)
+        sets = [(s[0], pb, s[2], s[3]) for s, pb in zip(sets, packs)]
+    else:
+        plan = hg.make_plan(16, 14336, 4096)
     with torch.cuda.stream(stream):
         for i in range(max(warmup, len(sets))):
             s = sets[i % len(sets)]
@@ -154,11 +179,14 @@ def bench_decode(dev, steps, warmup):
         reps.append(e0.elapsed_time(e1) / steps)
     ms = statistics.median(reps)
     from oracle import gemm_oracle as go
-    exact = bool(np.array_equal(sets[0][3].cpu().numpy(), go.gemm_i8_f64(c["A"], c["B"])))
+    want = go.gemm_i8_f64(c["A"], c["B"])
+    exact = all(bool(np.array_equal(s[3].cpu().numpy(), want)) for s in sets)
     alg = hg.algorithmic_bytes(plan)
     gbps = alg / (ms / 1e3) / 1e9
-    return {
-        "metric": "HBM GB/s @M=16 decode shape (M=16, K=4096, N=14336)",
+    traffic = TRAFFIC_DECODE_PACKED_M16 if packed else TRAFFIC_DECODE_M16
+    out = {
+        "metric": ("HBM GB/s @M=16 decode shape (M=16, K=4096, N=14336)"
+                   + (", B prepacked" if packed else "")),
         "value": gbps,
         "unit": "GB/s",
         "ms_per_step": ms,
@@ -167,12 +195,19 @@ def bench_decode(dev, steps, warmup):
         "variant": plan["variant"], "k_split": plan["k_split"],
         "roofline": {"bound": "hbm", "achieved": gbps, "peak": PEAK_GBPS, "unit": "GB/s",
                      "frac": gbps / PEAK_GBPS,
-                     "traffic": TRAFFIC_DECODE_M16["read"] + TRAFFIC_DECODE_M16["written"],
-                     "traffic_split": TRAFFIC_DECODE_M16, "algorithmic_bytes": alg,
-                     "kernels": "skinny_kernel<256,16,2> + skinny_reduce_kernel per step"},
-        "parity": "bit-exact vs oracle (full output)" if exact else "MISMATCH",
+                     "traffic": (traffic["read"] + traffic["written"]) if traffic else None,
+                     "traffic_split": traffic, "algorithmic_bytes": alg,
+                     "kernels": ("packed_skinny_kernel<4,8,2> per step" if packed else
+                                 "skinny_kernel<256,16,2> + skinny_reduce_kernel per step")},
+        "parity": "bit-exact vs oracle (full output, every set)" if exact else "MISMATCH",
         "rotated_sets": len(sets),
     }
+    if packed:
+        out["b_layout"] = ("packed once per weight matrix by vt_pack_b_i8 (not in the timed "
+                           "steps): %.1f us for the 58.7 MB B (median of %d, HIP events)"
+                           % (pack_ms * 1e3, len(sets)))
+        out["pack_ms"] = pack_ms
+    return out
 
 
 def bench_copy(dev, steps, warmup):
@@ -204,9 +239,11 @@ def main():
     ap.add_argument("--variant", default="auto", help="kernel variant for the headline GEMM")
     ap.add_argument("--provenance", default=None, metavar="PATH",
                     help="write a hash-bound report of the last timed step's result to PATH")
-    ap.add_argument("--workload", choices=("all", "gemm", "decode", "copy"), default="all",
-                    help="all: the JSON line below; gemm / decode: only that kernel (for "
-                         "profiler runs); copy: a plain 1 GiB device copy (counter calibration)")
+    ap.add_argument("--workload", choices=("all", "gemm", "decode", "decode_packed", "copy"),
+                    default="all",
+                    help="all: the JSON line below; gemm / decode / decode_packed: only that "
+                         "kernel (for profiler runs); copy: a plain 1 GiB device copy "
+                         "(counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -224,9 +261,20 @@ def main():
     if args.workload == "copy":
         print(json.dumps(bench_copy(dev, args.steps, args.warmup)), flush=True)
         return
-    if args.workload == "decode":
-        print(json.dumps(bench_decode(dev, max(args.steps, 6), args.warmup)), flush=True)
-        return
+    if args.workload in ("decode", "decode_packed"):
+        res = bench_decode(dev, max(args.steps, 6), args.warmup,
+                           packed=args.workload == "decode_packed")
+        print(json.dumps(res), flush=True)
+        sys.exit(0 if res["parity"].startswith("bit-exact") else 1)
+    decode = None
+    if args.workload == "all" and not args.no_decode:
+        # The decode figures come first: right after the 8192^3 GEMM the board
+        # is still power-throttled and a ~10 us streaming kernel reads ~7% slower.
+        log("decode shape")
+        row_major = bench_decode(dev, 120, args.warmup)
+        log("decode shape, packed B")
+        decode = (row_major, bench_decode(dev, 120, args.warmup, packed=True))
+        torch.cuda.empty_cache()
     log("generating config 5 inputs")
     c = inputs.config_inputs(5, seed=0)
     M = N = K = 8192
@@ -287,9 +335,10 @@ def main():
     if args.workload == "gemm":
         print(json.dumps(result), flush=True)
         sys.exit(0 if parity_ok else 1)
-    if not args.no_decode:
-        log("decode shape")
-        result["secondary"] = bench_decode(dev, 120, args.warmup)
+    if decode:
+        result["secondary"], result["secondary_packed_b"] = decode
+        if not all(r["parity"].startswith("bit-exact") for r in decode):
+            parity_ok = False
     if not args.no_cpu:
         log("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(c["A"], c["B"])

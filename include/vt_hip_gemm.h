@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define VT_ABI_VERSION 3
+#define VT_ABI_VERSION 4
 
 /* Status codes. */
 #define VT_OK 0
@@ -206,6 +206,63 @@ typedef struct vt_device_info {
 } vt_device_info;
 
 int vt_device_query(int32_t device, vt_device_info *info, int64_t info_size);
+
+/*
+ * Packed-B decode path.
+ *
+ * A decode-shaped GEMM (M <= 16 rows of activations against K x N int8
+ * weights) is bound by streaming B from HBM once. Row-major B makes the
+ * kernel transpose it through LDS and split K across workgroups to reach
+ * enough memory parallelism, which costs a second reduction launch. When the
+ * same weights serve many calls, pack them once into the layout below and
+ * call vt_gemm_i8_packed: every wave then loads its MFMA operand straight
+ * from HBM in 1 KiB coalesced pieces, K is not split, and the result is the
+ * same C = D + A.B as vt_gemm_i8, bit for bit.
+ *
+ * The reference keeps weights row-major and has no packed format; this is an
+ * MI355X layout for the skinny shape of the reference's GEMM contract
+ * (VeriTac/Gemmini/Semantics.lean:76-77), with the same arithmetic.
+ *
+ * Layout: Kp = K rounded up to a multiple of 64, kbt = Kp / 64. For each
+ * 16-column block nb (0 <= nb < N/16) and 64-row block kb (0 <= kb < kbt) a
+ * 1024-byte tile at byte offset (nb * kbt + kb) * 1024 holds, at tile byte
+ * l * 16 + i (l = 0..63, i = 0..15),
+ *     B[kb*64 + 16*(l/16) + i][nb*16 + l%16]     (0 for rows >= K).
+ * That is the B operand of v_mfma_i32_16x16x64_i8 for lane l. One packed B
+ * takes N * Kp bytes; every 16-column block is contiguous over K.
+ */
+
+/* Bytes of one packed B (N * Kp), or a negative VT_E* code (N % 16 != 0,
+ * negative or >= 2^30 sizes). No device call. */
+int64_t vt_packed_b_size(int64_t K, int64_t N);
+
+/*
+ * vt_pack_b_i8 -- row-major B int8 [batch][K][ldb] -> packed B
+ * [batch][vt_packed_b_size(K, N)] (stride_b / stride_bp bytes between
+ * batches). Needs N % 16 == 0, ldb and strides multiples of 16, 16-byte
+ * aligned B and Bp. Asynchronous on `stream`, like vt_gemm_i8.
+ */
+int vt_pack_b_i8(const int8_t *B, int8_t *Bp, int64_t K, int64_t N, int64_t ldb,
+                 int64_t batch, int64_t stride_b, int64_t stride_bp, void *stream);
+
+/*
+ * vt_gemm_i8_packed -- C = D + A.B with B packed by vt_pack_b_i8.
+ *
+ * Same contract, argument meaning and error behaviour as vt_gemm_i8
+ * (which replaces specializations/gemmini_gemm/backend.py:433-562 /
+ * :712-720 execution), with B given packed: Bp [batch][packed size],
+ * stride_bp 0 = one packed B shared by every batch. Needs N % 16 == 0,
+ * K % 16 == 0, lda and strides multiples of 16, 16-byte aligned A and Bp.
+ * Any M: rows run in groups of 16, each group streaming B once (the kernel
+ * is built for M <= 16). k_split: workgroups along K (0 = automatic: 1 when
+ * N gives enough column groups, else a split whose partial sums a second
+ * kernel adds).
+ */
+int vt_gemm_i8_packed(const int8_t *A, const int8_t *Bp, const int32_t *D, int32_t *C,
+                      int64_t M, int64_t N, int64_t K,
+                      int64_t lda, int64_t ldd, int64_t ldc, int64_t batch,
+                      int64_t stride_a, int64_t stride_bp, int64_t stride_d,
+                      int64_t stride_c, int32_t k_split, void *stream);
 
 #ifdef __cplusplus
 }

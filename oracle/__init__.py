@@ -15,8 +15,12 @@ Contents
                  and OpenMP over output rows; built by ``oracle/Makefile``
                  into ``oracle/_build/libvt_oracle.so``.
 ``cref``         ctypes loader for that library.
+``packed_b``     numpy restatement of the packed-B weight layout of the decode
+                 path (include/vt_hip_gemm.h): pack, unpack, and the product
+                 read under the MFMA operand convention.
 
-Pinning (how each function is checked, see tests/test_oracle.py):
+Pinning (how each function is checked, see tests/test_oracle.py and
+tests/test_packed_host.py):
   scalar_matmul / reference_matmul / gemm_i8 / ref_gemm.c
       - the 24 full-output Spike COUT vectors recorded by the reference
         (tests/golden/spike_cout.json, independent of the reference's Python);
@@ -33,4 +37,8 @@ Pinning (how each function is checked, see tests/test_oracle.py):
         (value = byte - 128 for the same state sequence). No recorded
         reference vector uses this stream, so beyond that relation it is
         "parity unpinned" (no fixture fixes its absolute values).
+  packed_b.pack_b / unpack_b / gemm_from_packed
+      - round trip on ragged shapes; the product read under the
+        v_mfma_i32_16x16x64_i8 operand convention equals the closed-form A.B;
+        three planted layout mistakes fail both checks.
 """

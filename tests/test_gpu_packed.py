@@ -1,0 +1,208 @@
+"""Packed-B decode path on the GPU, through the C ABI (needs a gfx950 GPU).
+
+vt_pack_b_i8 must produce the oracle's packed bytes exactly, and
+vt_gemm_i8_packed must give C = D + A.B bit for bit: the same result as the
+oracle and as vt_gemm_i8 on the row-major B. Outputs are poisoned with
+INT32_MIN before each launch so unwritten cells show.
+"""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from oracle import gemm_oracle as go
+from oracle import packed_b as pk
+from veritac_amd import HipGemmError, _lib
+from veritac_amd.specializations.hip_gemm import backend as hg
+from veritac_amd.specializations.hip_gemm import inputs
+
+pytestmark = pytest.mark.gpu
+
+INT32_MIN = -2**31
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    assert _lib.load_library().vt_device_count() >= 1, "GPU visible but not gfx950"
+    return torch.device("cuda", 0)
+
+
+def say(*args):
+    print(*args, flush=True)
+
+
+def to_dev(dev, x):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+
+
+def gpu_pack(dev, B, ldb=None):
+    """vt_pack_b_i8 of a row-major B (optionally with a padded row pitch)."""
+    k, n = B.shape
+    ldb = n if ldb is None else ldb
+    host = np.zeros((k, ldb), np.int8)
+    host[:, :n] = B
+    Bt = to_dev(dev, host)
+    size = _lib.packed_b_size(k, n)
+    Bp = torch.full((max(size, 16),), 0x5A, dtype=torch.int8, device=dev)
+    _lib.pack_b_raw(Bt.data_ptr(), Bp.data_ptr(), k, n, ldb)
+    _lib.sync(None)
+    return Bp[:size].cpu().numpy()
+
+
+def gpu_gemm_packed(dev, A, B, D=None, k_split=0, in_place=False):
+    """Pack B on the GPU, then C = D + A.B through vt_gemm_i8_packed."""
+    M, K = A.shape
+    N = B.shape[1]
+    Bt = to_dev(dev, B)
+    size = _lib.packed_b_size(K, N)
+    Bp = torch.empty(size, dtype=torch.int8, device=dev)
+    _lib.pack_b_raw(Bt.data_ptr(), Bp.data_ptr(), K, N, N)
+    At = to_dev(dev, A)
+    if in_place:
+        C = to_dev(dev, D)
+        Dt = C
+    else:
+        C = torch.full((M, N), INT32_MIN, dtype=torch.int32, device=dev)
+        Dt = to_dev(dev, D) if D is not None else None
+    _lib.gemm_packed_raw(At.data_ptr(), Bp.data_ptr(), Dt.data_ptr() if Dt is not None else None,
+                         C.data_ptr(), M, N, K, K, N, N, k_split=k_split)
+    _lib.sync(None)
+    return C.cpu().numpy()
+
+
+@pytest.mark.parametrize("k,n", [(1, 16), (64, 16), (100, 48), (130, 272), (4096, 256),
+                                 (1000, 14336)])
+def test_pack_matches_oracle_bytes(dev, k, n):
+    say("pack", k, n)
+    B = np.random.default_rng(k + n).integers(-128, 128, (k, n), dtype=np.int8)
+    assert np.array_equal(gpu_pack(dev, B), pk.pack_b(B))
+
+
+def test_pack_with_row_pitch_and_batches(dev):
+    k, n, batch, ldb = 200, 80, 3, 112
+    rng = np.random.default_rng(9)
+    B = rng.integers(-128, 128, (batch, k, ldb), dtype=np.int8)
+    Bt = to_dev(dev, B)
+    size = _lib.packed_b_size(k, n)
+    stride_bp = size + 1024
+    Bp = torch.full((batch * stride_bp,), 0x33, dtype=torch.int8, device=dev)
+    _lib.pack_b_raw(Bt.data_ptr(), Bp.data_ptr(), k, n, ldb, batch, k * ldb, stride_bp)
+    _lib.sync(None)
+    got = Bp.cpu().numpy()
+    for b in range(batch):
+        part = got[b * stride_bp:(b + 1) * stride_bp]
+        assert np.array_equal(part[:size], pk.pack_b(B[b, :, :n])), b
+        assert np.all(part[size:] == 0x33), b   # nothing written past the packed size
+
+
+def test_full_packed_config4_full_output(dev):
+    """Config 4 (M = 1 and 16, K = 4096, N = 14336) through pack_b / run."""
+    for m in (16, 1):
+        c = inputs.config_inputs(4, seed=0, m=m)
+        say("config 4 packed m=%d" % m)
+        A, B = to_dev(dev, c["A"]), to_dev(dev, c["B"])
+        Bp = hg.pack_b(B)
+        plan = hg.make_plan(m, 14336, 4096, variant=hg.PACKED_VARIANT)
+        C = hg.run(plan, A, Bp).cpu().numpy()
+        assert np.array_equal(C, go.gemm_i8_f64(c["A"], c["B"])), m
+        C_row = hg.run(hg.make_plan(m, 14336, 4096), A, B).cpu().numpy()
+        assert np.array_equal(C, C_row), m
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 16, 16), (3, 48, 80), (16, 64, 64), (16, 80, 48),
+                                   (7, 4160, 272), (16, 1024, 2048), (17, 256, 128),
+                                   (40, 512, 96), (5, 8192, 32)])
+@pytest.mark.parametrize("k_split", [0, 1, 3])
+def test_edge_shapes_and_splits(dev, m, k, n, k_split):
+    say("packed", m, k, n, "k_split", k_split)
+    rng = np.random.default_rng(m * 1000 + k + n + k_split)
+    A = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    B = rng.integers(-128, 128, (k, n), dtype=np.int8)
+    assert np.array_equal(gpu_gemm_packed(dev, A, B, k_split=k_split), go.gemm_i8(A, B))
+
+
+@pytest.mark.parametrize("k_split", [0, 1, 4])
+def test_initial_partial_sum_and_in_place(dev, k_split):
+    rng = np.random.default_rng(5 + k_split)
+    m, k, n = 16, 2048, 1024
+    A = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    B = rng.integers(-128, 128, (k, n), dtype=np.int8)
+    D = rng.integers(-2**20, 2**20, (m, n), dtype=np.int32)
+    want = go.gemm_i8(A, B, D)
+    assert np.array_equal(gpu_gemm_packed(dev, A, B, D, k_split=k_split), want)
+    assert np.array_equal(gpu_gemm_packed(dev, A, B, D, k_split=k_split, in_place=True), want)
+
+
+def test_extremes_at_k8192(dev):
+    m, k, n = 16, 8192, 64
+    A = np.full((m, k), -128, np.int8)
+    B = np.full((k, n), -128, np.int8)
+    C = gpu_gemm_packed(dev, A, B)
+    assert np.all(C == 134217728)
+    A = np.tile(np.array([-128, 127], np.int8), (m, k // 2))
+    B = np.tile(np.array([[127], [-128]], np.int8), (k // 2, n))
+    assert np.array_equal(gpu_gemm_packed(dev, A, B), go.gemm_i8(A, B))
+
+
+@pytest.mark.parametrize("shared", [True, False])
+def test_batches(dev, shared):
+    rng = np.random.default_rng(11 + shared)
+    batch, m, k, n = 3, 16, 512, 192
+    A = rng.integers(-128, 128, (batch, m, k), dtype=np.int8)
+    B = rng.integers(-128, 128, (k, n) if shared else (batch, k, n), dtype=np.int8)
+    D = rng.integers(-1000, 1000, (batch, m, n), dtype=np.int32)
+    At, Bt, Dt = to_dev(dev, A), to_dev(dev, B), to_dev(dev, D)
+    Bp = hg.pack_b(Bt)
+    plan = hg.make_plan(m, n, k, batch=batch, b_shared=shared, has_d=True, d_max_abs=1000,
+                        variant=hg.PACKED_VARIANT)
+    C = hg.run(plan, At, Bp, Dt).cpu().numpy()
+    for b in range(batch):
+        Bb = B if shared else B[b]
+        assert np.array_equal(C[b], go.gemm_i8(A[b], Bb, D[b])), b
+
+
+def test_repeated_launches_stay_exact(dev):
+    c = inputs.config_inputs(4, seed=3, m=16)
+    A, B = to_dev(dev, c["A"]), to_dev(dev, c["B"])
+    Bp = hg.pack_b(B)
+    plan = hg.make_plan(16, 14336, 4096, variant=hg.PACKED_VARIANT)
+    want = go.gemm_i8_f64(c["A"], c["B"])
+    outs = [torch.full((16, 14336), INT32_MIN, dtype=torch.int32, device=dev) for _ in range(4)]
+    for i in range(20):
+        hg.run(plan, A, Bp, out=outs[i % 4])
+    torch.cuda.synchronize()
+    for C in outs:
+        assert np.array_equal(C.cpu().numpy(), want)
+
+
+def test_refusals_never_launch(dev):
+    A = torch.zeros((16, 64), dtype=torch.int8, device=dev)
+    Bp = torch.zeros(64 * 64, dtype=torch.int8, device=dev)
+    C = torch.zeros((16, 64), dtype=torch.int32, device=dev)
+    with pytest.raises(HipGemmError):   # N not a multiple of 16
+        _lib.gemm_packed_raw(A.data_ptr(), Bp.data_ptr(), None, C.data_ptr(), 16, 40, 64, 64, 40, 64)
+    with pytest.raises(HipGemmError):   # K not a multiple of 16
+        _lib.gemm_packed_raw(A.data_ptr(), Bp.data_ptr(), None, C.data_ptr(), 16, 64, 40, 64, 64, 64)
+    with pytest.raises(HipGemmError):   # misaligned A
+        _lib.gemm_packed_raw(A.data_ptr() + 1, Bp.data_ptr(), None, C.data_ptr(), 16, 64, 64, 64,
+                             64, 64)
+    with pytest.raises(HipGemmError):   # ldc < N
+        _lib.gemm_packed_raw(A.data_ptr(), Bp.data_ptr(), None, C.data_ptr(), 16, 64, 64, 64, 64, 32)
+    with pytest.raises(HipGemmError):   # pack: ldb < N
+        _lib.pack_b_raw(A.data_ptr(), Bp.data_ptr(), 16, 64, 48)
+    _lib.sync(None)
+
+
+def test_repack_in_place(dev):
+    rng = np.random.default_rng(21)
+    k, n = 320, 96
+    B1 = rng.integers(-128, 128, (k, n), dtype=np.int8)
+    B2 = rng.integers(-128, 128, (k, n), dtype=np.int8)
+    Bp = hg.pack_b(to_dev(dev, B1))
+    same = hg.pack_b(to_dev(dev, B2), out=Bp)
+    assert same is Bp
+    assert np.array_equal(Bp.data.cpu().numpy(), pk.pack_b(B2))
+    with pytest.raises(HipGemmError, match="out must be"):
+        hg.pack_b(to_dev(dev, B2[:, :80]), out=Bp)

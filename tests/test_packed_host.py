@@ -1,0 +1,123 @@
+"""Packed-B layout on the CPU: the oracle restatement is pinned by the GEMM it
+must preserve (round trip, and the product read under the MFMA operand
+convention equals A @ B), planted layout mistakes fail those checks, the
+library's size query agrees, and the backend refuses mismatched operands
+before any device call."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import gemm_oracle as go
+from oracle import packed_b as pk
+from veritac_amd import HipGemmError, _lib
+from veritac_amd.specializations.hip_gemm import backend as hg
+
+SHAPES = [(1, 16), (16, 16), (64, 16), (100, 48), (130, 272), (256, 64), (1000, 32)]
+
+
+def rand_b(k, n, seed):
+    rng = np.random.default_rng(seed)
+    B = rng.integers(-128, 128, (k, n), dtype=np.int8)
+    B[0, :] = -128
+    B[-1, ::2] = 127
+    return B
+
+
+@pytest.mark.parametrize("k,n", SHAPES)
+def test_round_trip_and_size(k, n):
+    B = rand_b(k, n, k * 131 + n)
+    Bp = pk.pack_b(B)
+    assert Bp.dtype == np.int8 and Bp.size == pk.packed_size(k, n) == n * (-(-k // 64) * 64)
+    assert np.array_equal(pk.unpack_b(Bp, k, n), B)
+    # padding rows contribute nothing: same multiset of nonzero bytes
+    assert np.count_nonzero(Bp) == np.count_nonzero(B)
+    assert int(np.abs(Bp.astype(np.int64)).sum()) == int(np.abs(B.astype(np.int64)).sum())
+
+
+@pytest.mark.parametrize("k,n", SHAPES)
+def test_packed_product_under_mfma_operand_convention(k, n):
+    B = rand_b(k, n, 7 + k + n)
+    A = np.random.default_rng(k).integers(-128, 128, (5, k), dtype=np.int8)
+    assert np.array_equal(pk.gemm_from_packed(A, pk.pack_b(B), k, n), go.gemm_i8(A, B))
+
+
+def _wrong_packs(B):
+    """Plausible layout mistakes, each a full permutation of the right bytes."""
+    k, n = B.shape
+    kbt = -(-k // 64)
+    pad = np.zeros((kbt * 64, n), np.int8)
+    pad[:k] = B
+    t = pad.reshape(kbt, 4, 16, n // 16, 16)
+    yield "lane = column*4 + k group", t.transpose(3, 0, 4, 1, 2).reshape(-1)
+    yield "tiles ordered [kb][nb]", t.transpose(0, 3, 1, 4, 2).reshape(-1)
+    yield "tile bytes transposed", t.transpose(3, 0, 1, 2, 4).reshape(-1)
+
+
+def test_planted_layout_mistakes_fail():
+    k, n = 128, 48
+    B = rand_b(k, n, 3)
+    A = np.random.default_rng(4).integers(-128, 128, (4, k), dtype=np.int8)
+    want = go.gemm_i8(A, B)
+    for name, wrong in _wrong_packs(B):
+        wrong = np.ascontiguousarray(wrong)
+        assert not np.array_equal(pk.gemm_from_packed(A, wrong, k, n), want), name
+        assert not np.array_equal(pk.unpack_b(wrong, k, n), B), name
+
+
+def test_library_size_query_matches_layout():
+    for k, n in SHAPES + [(0, 16), (4096, 14336), (4160, 14336)]:
+        assert _lib.packed_b_size(k, n) == pk.packed_size(k, n)
+    for k, n in [(64, 8), (64, 17), (-1, 16), (64, -16), (1 << 30, 16)]:
+        with pytest.raises(HipGemmError):
+            _lib.packed_b_size(k, n)
+
+
+def test_packed_plans_validate():
+    p = hg.make_plan(16, 14336, 4096, variant=hg.PACKED_VARIANT)
+    assert hg.validate_plan(p) == (True, "ok")
+    assert hg.required_resources(p) == (32768, 224)
+    assert hg.packed_split(p) == (1, 64)
+    # few column groups: split K; rows beyond 16 run as row groups
+    p = hg.make_plan(40, 2048, 1024, variant=hg.PACKED_VARIANT)
+    assert hg.validate_plan(p)[0]
+    assert hg.packed_split(p) == (2, 8)
+    assert hg.required_resources(p)[1] == 32 * 2 * 3
+    for bad in (dict(n=24), dict(k=40), dict(batch=70000), dict(k_split=-1)):
+        assert not hg.validate_plan(dict(p, **bad))[0], bad
+    # packed is never an automatic candidate for a row-major B
+    assert hg.PACKED_VARIANT not in hg.VARIANTS
+    assert all(c["plan"]["variant"] != hg.PACKED_VARIANT
+               for c in hg.optimize(16, 14336, 4096)["candidates"])
+
+
+def test_run_refuses_mismatched_packed_operands():
+    calls = []
+
+    def fake(plan, A, B, D, C, stream):
+        calls.append(plan["variant"])
+
+    k, n = 128, 64
+    A = torch.zeros((16, k), dtype=torch.int8)
+    B = torch.zeros((k, n), dtype=torch.int8)
+    Bp = hg.PackedB(torch.zeros(pk.packed_size(k, n), dtype=torch.int8), k, n)
+    plan = hg.make_plan(16, n, k, variant=hg.PACKED_VARIANT)
+    hg.run(plan, A, Bp, runner=fake)
+    assert calls == [hg.PACKED_VARIANT]
+    with pytest.raises(HipGemmError, match="packed by pack_b"):
+        hg.run(plan, A, B, runner=fake)
+    with pytest.raises(HipGemmError, match="needs variant"):
+        hg.run(hg.make_plan(16, n, k, variant="skinny"), A, Bp, runner=fake)
+    with pytest.raises(HipGemmError, match="plan needs"):
+        hg.run(hg.make_plan(16, n + 16, k, variant=hg.PACKED_VARIANT), A[:, :k],
+               Bp, runner=fake)
+    short = hg.PackedB(torch.zeros(100, dtype=torch.int8), k, n)
+    with pytest.raises(HipGemmError, match="contiguous int8"):
+        hg.run(plan, A, short, runner=fake)
+    assert calls == [hg.PACKED_VARIANT]
+
+
+def test_pack_b_refuses_host_tensors():
+    with pytest.raises(HipGemmError, match="no CPU path"):
+        hg.pack_b(torch.zeros((64, 16), dtype=torch.int8))
+    with pytest.raises(HipGemmError):
+        hg.pack_b(torch.zeros((64, 16), dtype=torch.int32))

@@ -14,7 +14,7 @@ import threading
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 DEFAULT_LIB = os.path.join(PKG_DIR, "libvt_hip_gemm.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 VT_OK = 0
 VT_EINVAL = -1
@@ -38,7 +38,7 @@ VARIANTS = tuple(VARIANT_IDS)
 # Every function include/vt_hip_gemm.h declares.
 EXPORTS = ("vt_gemm_i8", "vt_gemm_select", "vt_variant_info", "vt_variant_name",
            "vt_last_error", "vt_sync", "vt_device_count", "vt_abi_version", "vt_replay_i8",
-           "vt_device_query")
+           "vt_device_query", "vt_packed_b_size", "vt_pack_b_i8", "vt_gemm_i8_packed")
 
 # Replay operation codes and status codes (VT_REPLAY_* in include/vt_hip_gemm.h).
 REPLAY_MVIN, REPLAY_LATCH_B, REPLAY_COMPUTE, REPLAY_MVOUT = 1, 2, 3, 4
@@ -111,6 +111,13 @@ def _declare(lib):
     lib.vt_device_query.restype = ctypes.c_int
     lib.vt_abi_version.argtypes = []
     lib.vt_abi_version.restype = ctypes.c_int
+    lib.vt_packed_b_size.argtypes = [i64, i64]
+    lib.vt_packed_b_size.restype = ctypes.c_int64
+    lib.vt_pack_b_i8.argtypes = [p, p, i64, i64, i64, i64, i64, i64, p]
+    lib.vt_pack_b_i8.restype = ctypes.c_int
+    lib.vt_gemm_i8_packed.argtypes = [p, p, p, p, i64, i64, i64, i64, i64, i64, i64,
+                                      i64, i64, i64, i64, i32, p]
+    lib.vt_gemm_i8_packed.restype = ctypes.c_int
 
 
 def load_library():
@@ -213,3 +220,27 @@ def device_query(device=-1):
         v = getattr(info, name)
         out[name] = v.decode("utf-8", "replace") if isinstance(v, bytes) else int(v)
     return out
+
+
+def packed_b_size(k, n):
+    """Bytes of one packed B (vt_packed_b_size); raises for shapes the format refuses."""
+    size = load_library().vt_packed_b_size(k, n)
+    if size < 0:
+        check(int(size), "vt_packed_b_size")
+    return size
+
+
+def pack_b_raw(B_ptr, Bp_ptr, K, N, ldb, batch=1, stride_b=0, stride_bp=0, stream=None):
+    """One vt_pack_b_i8 call on raw device pointers (integers); raises on failure."""
+    lib = load_library()
+    return check(lib.vt_pack_b_i8(B_ptr, Bp_ptr, K, N, ldb, batch, stride_b, stride_bp, stream),
+                 "vt_pack_b_i8")
+
+
+def gemm_packed_raw(A_ptr, Bp_ptr, D_ptr, C_ptr, M, N, K, lda, ldd, ldc, batch=1,
+                    stride_a=0, stride_bp=0, stride_d=0, stride_c=0, k_split=0, stream=None):
+    """One vt_gemm_i8_packed call on raw device pointers (integers); raises on failure."""
+    lib = load_library()
+    st = lib.vt_gemm_i8_packed(A_ptr, Bp_ptr, D_ptr, C_ptr, M, N, K, lda, ldd, ldc, batch,
+                               stride_a, stride_bp, stride_d, stride_c, k_split, stream)
+    return check(st, "vt_gemm_i8_packed")

@@ -813,6 +813,165 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(ReduceArgs p) {
 }
 
 // ---------------------------------------------------------------------------
+// Packed-B decode path
+// ---------------------------------------------------------------------------
+//
+// Packed B: for every 16-column block nb (N/16 of them) and 64-row block kb
+// (kbt = ceil(K/64) of them) one 1 KiB tile at byte (nb*kbt + kb)*1024 holds,
+// at l*16 + i (lane l = 0..63, i = 0..15), B[kb*64 + 16*(l/16) + i][nb*16 + l%16]
+// (zero for rows >= K). That is lane l's operand of v_mfma_i32_16x16x64_i8
+// (column l%16, k 16*(l/16)..+15), so a wave feeds the MFMA from one
+// coalesced 1 KiB load with no LDS transpose, and each 16-column block is
+// contiguous over K.
+
+// Row-major B -> packed B. One workgroup turns a 64-row x 256-column block
+// into 16 tiles through LDS: coalesced 16-byte loads in, 16-byte tile chunks out.
+struct PackArgs {
+  const int8_t *B;
+  int8_t *Bp;
+  int64_t ldb, sb, sbp;
+  int K, N, kbt;
+};
+
+__global__ __launch_bounds__(256) void pack_b_kernel(PackArgs p) {
+  constexpr int PITCH = 272;   // 256 columns + 16 bytes
+  __shared__ __attribute__((aligned(16))) int8_t tile[64 * PITCH];
+  const int kb = blockIdx.x, ng = blockIdx.y, bidx = blockIdx.z, tid = threadIdx.x;
+  const int8_t *Bb = p.B + bidx * p.sb;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = (tid >> 4) + 16 * i, c = tid & 15;
+    const int k = kb * 64 + row, col = ng * 256 + c * 16;
+    v4i v = v4i{0, 0, 0, 0};
+    if (k < p.K && col < p.N) v = *(const v4i *)(Bb + (int64_t)k * p.ldb + col);
+    st_lds_b128(tile, row * PITCH + c * 16, v);
+  }
+  __syncthreads();
+  const int nbt = p.N / 16;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int ch = tid + 256 * i, nbl = ch >> 6, l = ch & 63, nb = ng * 16 + nbl;
+    if (nb >= nbt) continue;
+    v4i v;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      uint32_t w = 0;
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+        w |= (uint32_t)(uint8_t)tile[(16 * (l >> 4) + 4 * q + b) * PITCH + nbl * 16 + (l & 15)]
+             << (8 * b);
+      v[q] = (int)w;
+    }
+    *(v4i *)(p.Bp + bidx * p.sbp + ((int64_t)nb * p.kbt + kb) * 1024 + l * 16) = v;
+  }
+}
+
+struct PackedArgs {
+  const int8_t *A;
+  const int8_t *Bp;
+  const int32_t *D;
+  int32_t *C;
+  int64_t lda, ldd, ldc;
+  int64_t sa, sbp, sd, sc;
+  int M, N, K;
+  int kbt;           // 64-row blocks of the packed layout
+  int groups;        // column groups of NBW 16-column blocks
+  int k_split;       // workgroups along K per column group
+  int kb_per_split;  // 64-row blocks per K slice
+  int32_t *ws;       // [batch][k_split][M][N] partials when k_split > 1
+};
+
+// M <= 16. One workgroup = WAVES waves over NBW 16-column blocks and one K
+// slice. Wave w takes the 64-row blocks kb_beg + w, kb_beg + w + WAVES, ...;
+// per block it loads its A fragment (16 bytes per lane, rows past M and k past
+// K zero) and the NBW packed B tiles, S blocks ahead of the MFMAs
+// (non-temporal loads: B is streamed once). The WAVES partial sums of each
+// column block are added through LDS and written once (plus D), or go to the
+// workspace when K is split across workgroups.
+template <int NBW, int WAVES, int S, bool HAS_D>
+__global__ __launch_bounds__(64 * WAVES) void packed_skinny_kernel(PackedArgs p) {
+  __shared__ v4i red[WAVES * NBW * 64];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // XCD-contiguous logical ids: neighbouring column groups share an L2.
+  const int G = gridDim.x, w = blockIdx.x;
+  const int q = G >> 3, r = G & 7, x = w & 7;
+  const int wl = x * q + (x < r ? x : r) + (w >> 3);
+  const int group = wl % p.groups, split = wl / p.groups;
+  const int bidx = blockIdx.y;
+  const int nb0 = group * NBW, nbt = p.N / 16;
+  const int kb_beg = split * p.kb_per_split;
+  const int kb_end = min(kb_beg + p.kb_per_split, p.kbt);
+  const int arow = lane & 15, acol = (lane >> 4) * 16;
+  const bool arow_ok = arow < p.M;
+  const int8_t *a_src = p.A + bidx * p.sa + (int64_t)(arow_ok ? arow : 0) * p.lda + acol;
+  const int8_t *Bb = p.Bp + bidx * p.sbp;
+  // Column blocks past the last one (a partial group) re-read the last block
+  // and are never stored.
+  int64_t b_off[NBW];
+#pragma unroll
+  for (int n = 0; n < NBW; ++n) b_off[n] = (int64_t)min(nb0 + n, nbt - 1) * p.kbt * 1024 + lane * 16;
+  v4i acc[NBW];
+#pragma unroll
+  for (int n = 0; n < NBW; ++n) acc[n] = v4i{0, 0, 0, 0};
+
+  const int first = kb_beg + wave;
+  const int steps = first < kb_end ? (kb_end - first + WAVES - 1) / WAVES : 0;
+  v4i a[S], b[S][NBW];
+  auto load = [&](int s, v4i &av, v4i (&bv)[NBW]) {
+    if (s < steps) {
+      const int kb = first + s * WAVES;
+#pragma unroll
+      for (int n = 0; n < NBW; ++n)
+        bv[n] = __builtin_nontemporal_load((const v4i *)(Bb + b_off[n] + (int64_t)kb * 1024));
+      av = (arow_ok && kb * 64 + acol < p.K) ? *(const v4i *)(a_src + kb * 64) : v4i{0, 0, 0, 0};
+    } else {
+#pragma unroll
+      for (int n = 0; n < NBW; ++n) bv[n] = v4i{0, 0, 0, 0};
+      av = v4i{0, 0, 0, 0};
+    }
+  };
+#pragma unroll
+  for (int s = 0; s < S; ++s) load(s, a[s], b[s]);
+  for (int s0 = 0; s0 < steps; s0 += S) {
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+#pragma unroll
+      for (int n = 0; n < NBW; ++n)
+        acc[n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[s], b[s][n], acc[n], 0, 0, 0);
+      load(s0 + s + S, a[s], b[s]);
+    }
+  }
+
+  // 16x16 accumulator layout: element e of lane l is row 4*(l/16) + e,
+  // column l%16. Thread t sums output (block t/256, row (t/16)%16, column t%16)
+  // over the waves, so 16 consecutive threads write 64 contiguous bytes.
+#pragma unroll
+  for (int n = 0; n < NBW; ++n) red[(wave * NBW + n) * 64 + lane] = acc[n];
+  __syncthreads();
+  const int32_t *Db = HAS_D ? p.D + bidx * p.sd : nullptr;
+  int32_t *Cb = p.C + bidx * p.sc;
+  int32_t *wsb = p.ws ? p.ws + ((int64_t)bidx * p.k_split + split) * p.M * p.N : nullptr;
+  for (int t = tid; t < NBW * 256; t += 64 * WAVES) {
+    const int n = t >> 8, row = (t >> 4) & 15, c = t & 15;
+    const int src = (row >> 2) * 16 + c, e = row & 3;
+    int32_t s = 0;
+#pragma unroll
+    for (int wv = 0; wv < WAVES; ++wv)
+      s = add_wrap(s, ((const int32_t *)&red[(wv * NBW + n) * 64 + src])[e]);
+    const int nb = nb0 + n;
+    if (nb >= nbt || row >= p.M) continue;
+    const int col = nb * 16 + c;
+    if (p.k_split == 1) {
+      if (HAS_D) s = add_wrap(s, Db[(int64_t)row * p.ldd + col]);
+      Cb[(int64_t)row * p.ldc + col] = s;
+    } else {
+      wsb[(int64_t)row * p.N + col] = s;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Generic kernel: any shape, stride and alignment
 // ---------------------------------------------------------------------------
 
@@ -1216,6 +1375,71 @@ int launch_skinny(const Problem &q, int k_split, DeviceState *st, void *stream) 
   return launch_skinny_cfg<kSkinnyNB, kSkinnyWaves, kSkinnyU>(q, k_split, st, stream);
 }
 
+// Packed-B decode configuration: 4 column blocks (64 columns) per workgroup,
+// 8 waves, 2 row blocks of loads ahead. For N = 14336 that is 224 workgroups
+// streaming 256 KiB each.
+constexpr int kPackedNBW = 4, kPackedWaves = 8, kPackedS = 2;
+
+int64_t packed_kbt(int64_t K) { return (K + 63) / 64; }
+
+// Workgroups along K for the packed kernel: 1 when the column groups alone
+// give most CUs a workgroup, else enough K slices for ~224 workgroups, each
+// slice at least one row block per wave.
+int packed_k_split(int64_t N, int64_t K, int64_t batch) {
+  const int64_t groups = (N / 16 + kPackedNBW - 1) / kPackedNBW * batch;
+  if (groups >= 192) return 1;
+  int64_t ks = (224 + groups - 1) / groups;
+  const int64_t max_by_k = (packed_kbt(K) + kPackedWaves - 1) / kPackedWaves;
+  if (ks > max_by_k) ks = max_by_k;
+  if (ks < 1) ks = 1;
+  if (ks > 64) ks = 64;
+  return (int)ks;
+}
+
+// One launch (plus the partial-sum reduction when K is split) over at most
+// 16 rows of A / C / D.
+int launch_packed_rows(const Problem &q, int k_split, DeviceState *st, void *stream) {
+  PackedArgs a;
+  a.A = q.A; a.Bp = q.B; a.D = q.D; a.C = q.C;
+  a.lda = q.lda; a.ldd = q.ldd; a.ldc = q.ldc;
+  a.sa = q.sa; a.sbp = q.sb; a.sd = q.sd; a.sc = q.sc;
+  a.M = (int)q.M; a.N = (int)q.N; a.K = (int)q.K;
+  a.kbt = (int)packed_kbt(q.K);
+  a.groups = (int)((q.N / 16 + kPackedNBW - 1) / kPackedNBW);
+  const int ks0 = k_split > 0 ? k_split : packed_k_split(q.N, q.K, q.batch);
+  a.kb_per_split = (a.kbt + ks0 - 1) / ks0;
+  a.k_split = (a.kbt + a.kb_per_split - 1) / a.kb_per_split;
+  a.ws = nullptr;
+  if ((int64_t)a.groups * a.k_split > 0x7fffffff || q.batch > 65535)
+    return fail(VT_EUNSUPPORTED, "packed grid too large");
+  if (a.k_split > 1) {
+    Workspace *w = nullptr;
+    const size_t pbytes = (size_t)q.batch * a.k_split * q.M * q.N * sizeof(int32_t);
+    int rc = get_workspace(st, stream, pbytes, &w);
+    if (rc) return rc;
+    a.ws = w->partials;
+  }
+  hipStream_t s = (hipStream_t)stream;
+  dim3 grid((unsigned)(a.groups * a.k_split), (unsigned)q.batch), block(64 * kPackedWaves);
+  if (q.D && a.k_split == 1)
+    hipLaunchKernelGGL((packed_skinny_kernel<kPackedNBW, kPackedWaves, kPackedS, true>), grid, block, 0, s, a);
+  else
+    hipLaunchKernelGGL((packed_skinny_kernel<kPackedNBW, kPackedWaves, kPackedS, false>), grid, block, 0, s, a);
+  VT_HIP_CHECK(hipGetLastError());
+  if (a.k_split > 1) {
+    ReduceArgs r;
+    r.ws = a.ws; r.D = q.D; r.C = q.C;
+    r.ldd = q.ldd; r.ldc = q.ldc; r.sd = q.sd; r.sc = q.sc;
+    r.M = (int)q.M; r.N = (int)q.N; r.k_split = a.k_split;
+    const int64_t per = q.M * q.N / 4;
+    dim3 rgrid((unsigned)((per + 255) / 256), (unsigned)q.batch);
+    if (q.D) hipLaunchKernelGGL(skinny_reduce_kernel<true>, rgrid, dim3(256), 0, s, r);
+    else hipLaunchKernelGGL(skinny_reduce_kernel<false>, rgrid, dim3(256), 0, s, r);
+    VT_HIP_CHECK(hipGetLastError());
+  }
+  return VT_OK;
+}
+
 int launch_generic(const Problem &q, hipStream_t stream) {
   GenericArgs a;
   a.A = q.A; a.B = q.B; a.D = q.D; a.C = q.C;
@@ -1447,6 +1671,93 @@ int vt_gemm_i8(const int8_t *A, const int8_t *B, const int32_t *D, int32_t *C, i
     case VT_VARIANT_GENERIC: return launch_generic(q, s);
     default: return fail(VT_EINVAL, "unknown variant %d", (int)chosen);
   }
+}
+
+int64_t vt_packed_b_size(int64_t K, int64_t N) {
+  if (K < 0 || N < 0 || N % 16 != 0 || K >= (1ll << 30) || N >= (1ll << 30))
+    return fail(VT_EINVAL, "packed B needs 0 <= K < 2^30 and 0 <= N < 2^30 with N %% 16 == 0 "
+                "(K=%lld N=%lld)", (long long)K, (long long)N);
+  return N * packed_kbt(K) * 64;
+}
+
+int vt_pack_b_i8(const int8_t *B, int8_t *Bp, int64_t K, int64_t N, int64_t ldb, int64_t batch,
+                 int64_t stride_b, int64_t stride_bp, void *stream) {
+  g_err.clear();
+  if (K < 0 || N < 0 || batch < 0) return fail(VT_EINVAL, "negative size");
+  const int64_t size = vt_packed_b_size(K, N);
+  if (size < 0) return (int)size;
+  if (K == 0 || N == 0 || batch == 0) return VT_OK;
+  if (!B || !Bp) return fail(VT_EINVAL, "B or Bp is null");
+  if (ldb < N) return fail(VT_EINVAL, "ldb=%lld < N=%lld", (long long)ldb, (long long)N);
+  if (ldb % 16 || stride_b % 16 || stride_bp % 16 || !aligned16(B) || !aligned16(Bp))
+    return fail(VT_EUNSUPPORTED, "pack needs ldb and strides multiples of 16 and 16-byte aligned B, Bp");
+  if (stride_b < 0 || stride_bp < 0) return fail(VT_EINVAL, "negative batch stride");
+  if (batch > 1 && stride_bp < size)
+    return fail(VT_EINVAL, "stride_bp=%lld overlaps packed batches (size %lld)",
+                (long long)stride_bp, (long long)size);
+  if (batch > 65535 || (N + 255) / 256 > 65535)
+    return fail(VT_EUNSUPPORTED, "pack grid too large (batch=%lld N=%lld)", (long long)batch,
+                (long long)N);
+  if ((K - 1) * ldb + N >= (1ll << 40)) return fail(VT_EINVAL, "B extent beyond 2^40");
+  int dev = 0;
+  DeviceState *st = nullptr;
+  int rc = current_device(&dev, &st);
+  if (rc) return rc;
+  PackArgs a;
+  a.B = B; a.Bp = Bp; a.ldb = ldb; a.sb = stride_b; a.sbp = stride_bp;
+  a.K = (int)K; a.N = (int)N; a.kbt = (int)packed_kbt(K);
+  hipLaunchKernelGGL(pack_b_kernel, dim3((unsigned)a.kbt, (unsigned)((N + 255) / 256), (unsigned)batch),
+                     dim3(256), 0, (hipStream_t)stream, a);
+  VT_HIP_CHECK(hipGetLastError());
+  return VT_OK;
+}
+
+int vt_gemm_i8_packed(const int8_t *A, const int8_t *Bp, const int32_t *D, int32_t *C, int64_t M,
+                      int64_t N, int64_t K, int64_t lda, int64_t ldd, int64_t ldc, int64_t batch,
+                      int64_t stride_a, int64_t stride_bp, int64_t stride_d, int64_t stride_c,
+                      int32_t k_split, void *stream) {
+  g_err.clear();
+  if (M < 0 || N < 0 || K < 0 || batch < 0)
+    return fail(VT_EINVAL, "negative size (M=%lld N=%lld K=%lld batch=%lld)", (long long)M,
+                (long long)N, (long long)K, (long long)batch);
+  if (k_split < 0 || k_split > 4096) return fail(VT_EINVAL, "k_split %d out of range", (int)k_split);
+  if (stride_a < 0 || stride_bp < 0 || stride_d < 0 || stride_c < 0)
+    return fail(VT_EINVAL, "negative batch stride");
+  if (M == 0 || N == 0 || batch == 0) return VT_OK;
+  if (!C) return fail(VT_EINVAL, "C is null");
+  if (K > 0 && (!A || !Bp)) return fail(VT_EINVAL, "A or Bp is null");
+  if (ldc < N) return fail(VT_EINVAL, "ldc=%lld < N=%lld", (long long)ldc, (long long)N);
+  if (K > 0 && lda < K) return fail(VT_EINVAL, "lda=%lld < K=%lld", (long long)lda, (long long)K);
+  if (D && ldd < N) return fail(VT_EINVAL, "ldd=%lld < N=%lld", (long long)ldd, (long long)N);
+  if (batch > 1 && stride_c < M * ldc)
+    return fail(VT_EINVAL, "stride_c=%lld overlaps batches (M*ldc=%lld)", (long long)stride_c,
+                (long long)(M * ldc));
+  if (M >= (1ll << 30) || N >= (1ll << 30) || K >= (1ll << 30))
+    return fail(VT_EINVAL, "size beyond 2^30");
+  if (N % 16 || K % 16)
+    return fail(VT_EUNSUPPORTED, "packed B needs N %% 16 == 0 and K %% 16 == 0 (N=%lld K=%lld)",
+                (long long)N, (long long)K);
+  if (K > 0 && (lda % 16 || stride_a % 16 || stride_bp % 16 || !aligned16(A) || !aligned16(Bp)))
+    return fail(VT_EUNSUPPORTED,
+                "packed GEMM needs lda and strides multiples of 16 and 16-byte aligned A, Bp");
+  if (batch > 65535) return fail(VT_EUNSUPPORTED, "packed GEMM supports batch <= 65535");
+  int dev = 0;
+  DeviceState *st = nullptr;
+  int rc = current_device(&dev, &st);
+  if (rc) return rc;
+  Problem q = {A, Bp, D, C, M, N, K, lda, 0, ldd, ldc, batch, stride_a, stride_bp, stride_d, stride_c};
+  if (K == 0) return launch_generic(q, (hipStream_t)stream);   // C = D (or 0)
+  // Rows in groups of 16: each group streams B once more.
+  for (int64_t r0 = 0; r0 < M; r0 += 16) {
+    Problem g = q;
+    g.A = A + r0 * lda;
+    g.C = C + r0 * ldc;
+    g.D = D ? D + r0 * ldd : nullptr;
+    g.M = M - r0 < 16 ? M - r0 : 16;
+    rc = launch_packed_rows(g, k_split, st, stream);
+    if (rc) return rc;
+  }
+  return VT_OK;
 }
 
 }  // extern "C"

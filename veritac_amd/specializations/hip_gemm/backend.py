@@ -42,7 +42,11 @@ INT8_DOMAIN_CONSTRAINT = "inputs are int8 in [-128,127] and k*16384 + |D| <= 214
 MAX_EXTENT = 2**40
 
 VARIANTS = ("mfma_256x256", "mfma_256x128", "mfma_128x128", "skinny", "generic")
-SUPPORTED_VARIANTS = ("auto",) + VARIANTS
+# The packed-B decode variant takes B prepacked by pack_b (vt_pack_b_i8), not
+# row-major, so it is never an automatic candidate for a row-major B.
+PACKED_VARIANT = "skinny_packed"
+ALL_VARIANTS = VARIANTS + (PACKED_VARIANT,)
+SUPPORTED_VARIANTS = ("auto",) + ALL_VARIANTS
 
 # variant -> (tile_m, tile_n, tile_k, threads, lds_bytes); mirrors the native
 # table returned by vt_variant_info (checked by the tests).
@@ -52,7 +56,11 @@ TILES = {
     "mfma_128x128": (128, 128, 64, 256, 2 * (128 * 64 + 64 * 128)),
     "skinny": (16, 256, 64, 1024, 2 * 16 * 1024),
     "generic": (4, 64, 1, 256, 0),
+    # 16 rows (groups of 16 for larger m), 4 column blocks, 64-row blocks,
+    # 8 waves, LDS for the cross-wave sums (kPacked* in the HIP source)
+    "skinny_packed": (16, 64, 64, 512, 8 * 4 * 1024),
 }
+PACKED_WAVES = 8
 SKINNY_MAX_M = 16
 SKINNY_PIPE_ROWS = 64 * 2   # stage rows x stages in flight (kSkinny* in the HIP source)
 LDS_PER_CU = 160 * 1024
@@ -108,6 +116,23 @@ def _auto_k_split(n, k, batch):
     return max(1, min(ks, 64))
 
 
+def packed_split(plan):
+    """(k_split, 64-row blocks per slice) the packed kernel launches.
+
+    Mirrors packed_k_split / launch_packed_rows in csrc/vt_hip_gemm.hip.
+    """
+    n, k, batch, ks = plan["n"], plan["k"], plan["batch"], plan["k_split"]
+    kbt = -(-k // 64)
+    if ks <= 0:
+        groups = -(-(n // 16) // 4) * batch
+        if groups >= 192:
+            ks = 1
+        else:
+            ks = max(1, min(-(-224 // groups), -(-kbt // PACKED_WAVES), 64))
+    per = -(-kbt // ks)
+    return -(-kbt // per), per
+
+
 def required_resources(plan):
     """(lds_bytes per workgroup, workgroups) the plan's variant launches.
 
@@ -125,6 +150,9 @@ def required_resources(plan):
     if variant == "skinny":
         ks, chunk = skinny_split(plan)
         return lds + 16 * skinny_a_stride(chunk), -(-n // tn) * ks * batch
+    if variant == PACKED_VARIANT:
+        ks, _ = packed_split(plan)
+        return lds, -(-n // tn) * ks * batch * -(-m // tm)
     return 0, -(-n // tn) * min(-(-m // tm), 65535) * min(batch, 65535)
 
 
@@ -166,8 +194,8 @@ def validate_plan(plan):
         if key not in plan or not isinstance(plan[key], bool):
             return False, "plan field %r must be a boolean" % key
     variant = plan.get("variant")
-    if variant not in VARIANTS:
-        return False, ("unsupported variant %r (supported: %s)" % (variant, list(VARIANTS)))
+    if variant not in ALL_VARIANTS:
+        return False, ("unsupported variant %r (supported: %s)" % (variant, list(ALL_VARIANTS)))
     m, n, k, batch, dim = plan["m"], plan["n"], plan["k"], plan["batch"], plan["dim"]
     if dim != DIM:
         return False, "dim must equal DIM=%d (got %d)" % (DIM, dim)
@@ -196,8 +224,13 @@ def validate_plan(plan):
             return False, "variant 'skinny' needs m <= %d (got %d)" % (SKINNY_MAX_M, m)
         if batch > 65535:
             return False, "variant 'skinny' supports batch <= 65535"
+    elif variant == PACKED_VARIANT:
+        if batch > 65535:
+            return False, "variant %r supports batch <= 65535" % PACKED_VARIANT
+        if max(m, n, k) >= 2**30:
+            return False, "variant %r needs m, n, k < 2^30" % PACKED_VARIANT
     elif variant != "generic" and plan["k_split"] != 0:
-        return False, "k_split applies to variant 'skinny' only"
+        return False, "k_split applies to variants 'skinny' and %r only" % PACKED_VARIANT
     lds, workgroups = required_resources(plan)
     if lds > LDS_PER_CU:
         return False, "LDS %d bytes > %d per CU" % (lds, LDS_PER_CU)
@@ -212,7 +245,7 @@ def validate_plan(plan):
 
 # Fraction of the dense INT8 peak each variant is modeled at when compute-bound.
 _MODEL_MFMA_EFF = {"mfma_256x256": 0.70, "mfma_256x128": 0.60, "mfma_128x128": 0.45,
-                   "skinny": 0.25, "generic": 0.002}
+                   "skinny": 0.25, "skinny_packed": 0.25, "generic": 0.002}
 
 
 def algorithmic_bytes(plan):
@@ -243,6 +276,13 @@ def modeled_counts(plan):
         ks, _ = skinny_split(plan)
         partial = 2 * 4 * b * m * n * ks if ks > 1 else 0
         l2_bytes = alg + partial + b * -(-n // tn) * 16 * k
+    elif variant == PACKED_VARIANT:
+        ks, _ = packed_split(plan)
+        groups = -(-m // 16)
+        partial = 2 * 4 * b * m * n * ks if ks > 1 else 0
+        # B once per 16-row group; each workgroup reads its A rows once
+        l2_bytes = (groups * (b * -(-k // 64) * 64 * n) + b * m * k * -(-n // tn)
+                    + 4 * b * m * n * (2 if plan["has_d"] else 1) + partial)
     else:
         l2_bytes = b * (m * n * k + -(-m // 4) * n * k) + 4 * b * m * n
     return {"ops": ops, "macs": ops // 2, "bytes_algorithmic": alg, "bytes_l2_modeled": l2_bytes,
@@ -344,9 +384,104 @@ def _check_tensor(name, t, shape, dtype, device):
         raise HipGemmError("%s must have unit stride in its last dimension" % name)
 
 
+class PackedB:
+    """Weights B packed for the decode kernel (vt_pack_b_i8's layout).
+
+    `data` is a flat int8 device tensor of `batch` packed matrices of
+    `size_bytes` each: for every 16-column block and 64-row block of the K x N
+    matrix, one 1 KiB tile holding the v_mfma_i32_16x16x64_i8 B operand
+    (include/vt_hip_gemm.h gives the byte formula). Build it with pack_b.
+    """
+
+    __slots__ = ("data", "k", "n", "batch")
+
+    def __init__(self, data, k, n, batch=1):
+        self.data, self.k, self.n, self.batch = data, k, n, batch
+
+    @property
+    def size_bytes(self):
+        """Bytes of one packed matrix: n * (k rounded up to 64)."""
+        return self.n * (-(-self.k // 64) * 64)
+
+    @property
+    def device(self):
+        return self.data.device
+
+    def __repr__(self):
+        return "PackedB(k=%d, n=%d, batch=%d, device=%s)" % (self.k, self.n, self.batch,
+                                                            self.data.device)
+
+
+def pack_b(B, *, out=None, stream=None):
+    """Pack row-major int8 B [k, n] (or [batch, k, n]) for the skinny_packed variant.
+
+    Runs vt_pack_b_i8 on B's GPU; raises HipGemmError for host tensors or
+    shapes the format refuses (n must be a multiple of 16). The packed copy
+    is computed once and reused by every call with these weights. `out`, a
+    PackedB of the same shape, is repacked in place instead of allocating.
+    """
+    torch = _torch()
+    if not isinstance(B, torch.Tensor) or B.dtype != torch.int8 or B.dim() not in (2, 3):
+        raise HipGemmError("B must be an int8 torch tensor [k, n] or [batch, k, n]")
+    if B.device.type != "cuda":
+        raise HipGemmError("B must be on a gfx950 GPU (got %s); hip_gemm has no CPU path"
+                           % B.device)
+    if B.stride(-1) != 1:
+        raise HipGemmError("B must have unit stride in its last dimension")
+    batch = B.shape[0] if B.dim() == 3 else 1
+    k, n = B.shape[-2], B.shape[-1]
+    size = _lib.packed_b_size(k, n)
+    if out is None:
+        data = torch.empty(batch * size, dtype=torch.int8, device=B.device)
+    else:
+        if not isinstance(out, PackedB) or (out.k, out.n, out.batch) != (k, n, batch):
+            raise HipGemmError("out must be a PackedB with k=%d n=%d batch=%d" % (k, n, batch))
+        data = out.data
+        if (not isinstance(data, torch.Tensor) or data.dtype != torch.int8 or data.dim() != 1
+                or data.numel() != batch * size or not data.is_contiguous()
+                or data.device != B.device):
+            raise HipGemmError("out.data must be a contiguous int8 tensor of %d bytes on %s"
+                               % (batch * size, B.device))
+    if stream is None:
+        with torch.cuda.device(B.device):
+            stream = torch.cuda.current_stream(B.device).cuda_stream
+    _lib.pack_b_raw(B.data_ptr(), data.data_ptr(), k, n, B.stride(-2), batch,
+                    B.stride(0) if B.dim() == 3 else 0, size, stream)
+    return out if out is not None else PackedB(data, k, n, batch)
+
+
+def _check_packed(B, plan, device):
+    torch = _torch()
+    if not isinstance(B, PackedB):
+        raise HipGemmError("variant %r needs B packed by pack_b (got %s)"
+                           % (PACKED_VARIANT, type(B).__name__))
+    want_batch = 1 if (plan["batch"] == 1 or plan["b_shared"]) else plan["batch"]
+    if (B.k, B.n, B.batch) != (plan["k"], plan["n"], want_batch):
+        raise HipGemmError("packed B is k=%d n=%d batch=%d, plan needs k=%d n=%d batch=%d"
+                           % (B.k, B.n, B.batch, plan["k"], plan["n"], want_batch))
+    data = B.data
+    if (not isinstance(data, torch.Tensor) or data.dtype != torch.int8 or data.dim() != 1
+            or data.numel() != B.batch * B.size_bytes or not data.is_contiguous()):
+        raise HipGemmError("packed B data must be a contiguous int8 tensor of %d bytes"
+                           % (B.batch * B.size_bytes))
+    if data.device != device:
+        raise HipGemmError("packed B is on %s, expected %s" % (data.device, device))
+
+
 def native_runner(plan, A, B, D, C, stream):
-    """Default device runner: one vt_gemm_i8 call through the C ABI."""
+    """Default device runner: one vt_gemm_i8 (or vt_gemm_i8_packed) call
+    through the C ABI."""
     m, n, k, b = plan["m"], plan["n"], plan["k"], plan["batch"]
+    if plan["variant"] == PACKED_VARIANT:
+        ldd = D.stride(-2) if D is not None else n
+        sbp = B.size_bytes if B.batch > 1 else 0
+        _lib.gemm_packed_raw(A.data_ptr(), B.data.data_ptr(),
+                             D.data_ptr() if D is not None else None, C.data_ptr(),
+                             m, n, k, A.stride(-2), ldd, C.stride(-2), b,
+                             A.stride(0) if b > 1 else 0, sbp,
+                             D.stride(0) if (D is not None and b > 1) else 0,
+                             C.stride(0) if b > 1 else 0, plan["k_split"], stream)
+        return
     lda = A.stride(-2)
     ldb = B.stride(-2)
     ldc = C.stride(-2)
@@ -378,7 +513,13 @@ def run(plan, A, B, D=None, *, out=None, stream=None, runner=None):
     device = A.device
     a_shape, b_shape, c_shape = _operand_shapes(plan)
     _check_tensor("A", A, a_shape, torch.int8, device)
-    _check_tensor("B", B, b_shape, torch.int8, device)
+    if plan["variant"] == PACKED_VARIANT:
+        _check_packed(B, plan, device)
+    else:
+        if isinstance(B, PackedB):
+            raise HipGemmError("a packed B needs variant %r (plan has %r)"
+                               % (PACKED_VARIANT, plan["variant"]))
+        _check_tensor("B", B, b_shape, torch.int8, device)
     if plan["has_d"]:
         if D is None:
             raise HipGemmError("plan has_d=True but D is None")
