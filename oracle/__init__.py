@@ -30,13 +30,14 @@ tests/test_packed_host.py):
         K-tiling invariance, a planted-mistake check (dropped partial sum).
   lcg8_stream / fill_inputs
       - the reference's own LCG known-answer test and the lcg COUT vectors.
-  deterministic_inputs ("lcg" mode, byte-128 mapping)
-      - closed-form restatement of backend.py:583-593, cross-checked against
-        an independent C-style uint32 implementation in ref_gemm.c
-        (vt_ref_lcg_fill) and against its relation to lcg8_stream
-        (value = byte - 128 for the same state sequence). No recorded
-        reference vector uses this stream, so beyond that relation it is
-        "parity unpinned" (no fixture fixes its absolute values).
+  deterministic_inputs (every mode) / scalar_matmul
+      - input/output vectors produced by the reference's own functions
+        (tests/golden/lcg_inputs.json, written by
+        tests/golden/make_lcg_vectors.py in the build container), which also
+        tell the byte - 128 mapping from the two's-complement one;
+      - the relation value = lcg8 byte - 128 for the same state sequence, and
+        the C twin in ref_gemm.c (vt_ref_lcg_fill), which computes the value
+        by a different formula (top bit flipped, read as int8).
   packed_b.pack_b / unpack_b / gemm_from_packed
       - round trip on ragged shapes; the product read under the
         v_mfma_i32_16x16x64_i8 operand convention equals the closed-form A.B;

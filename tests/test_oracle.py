@@ -169,3 +169,41 @@ def test_batched_broadcast_equals_per_batch():
     C = go.gemm_i8(A, B)
     for b in range(4):
         assert np.array_equal(C[b], cref.gemm_i8(A[b], B))
+
+
+def test_deterministic_inputs_match_reference_vectors():
+    """deterministic_inputs and scalar_matmul against vectors the reference's
+    own functions produced (tests/golden/make_lcg_vectors.py), in every mode:
+    the oracle's restatement, its C twin and the product's generator."""
+    import json
+    import os
+    from veritac_amd.specializations.hip_gemm import inputs
+    path = os.path.join(os.path.dirname(__file__), "golden", "lcg_inputs.json")
+    with open(path) as fh:
+        cases = json.load(fh)["cases"]
+    assert len(cases) == 10
+    assert {c["mode"] for c in cases} == {"lcg", "max", "minmax", "min", "zero"}
+    for c in cases:
+        m, n, k, seed, mode = c["m"], c["n"], c["k"], c["seed"], c["mode"]
+        A, B = go.deterministic_inputs(m, n, k, seed, mode)
+        assert (A, B) == (c["A"], c["B"]), (m, n, k, seed, mode)
+        An, Bn = inputs.deterministic_inputs(m, n, k, seed, mode)
+        assert An.reshape(-1).tolist() == c["A"] and Bn.reshape(-1).tolist() == c["B"]
+        assert go.scalar_matmul(c["A"], c["B"], m, n, k) == c["C"]
+        assert go.gemm_i8(An, Bn).reshape(-1).tolist() == c["C"]
+        if mode == "lcg":
+            ca, cb = cref.lcg_fill(seed, m * k, k * n)
+            assert ca.tolist() == c["A"] and cb.tolist() == c["B"]
+
+
+def test_reference_vectors_pin_the_byte_mapping():
+    """The fixture tells byte - 128 from the two's-complement reading of the
+    same bytes (the Spike harness's mapping): a planted swap must fail it."""
+    import json
+    import os
+    path = os.path.join(os.path.dirname(__file__), "golden", "lcg_inputs.json")
+    with open(path) as fh:
+        c = json.load(fh)["cases"][2]
+    stream = go.lcg8_stream(c["m"] * c["k"] + c["k"] * c["n"], c["seed"])
+    assert [b - 128 for b in stream[:c["m"] * c["k"]]] == c["A"]
+    assert [go.to_int8(b) for b in stream[:c["m"] * c["k"]]] != c["A"]

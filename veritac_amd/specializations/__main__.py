@@ -1,27 +1,32 @@
-"""Inspect available specializations; this command never launches a backend.
+"""Print specialization descriptors as JSON; never launches a backend.
 
     python -m veritac_amd.specializations list
     python -m veritac_amd.specializations show hip_gemm
 """
-import argparse
 import json
+import sys
 
-from .catalog import describe, list_specializations
+from . import catalog
+
+USAGE = "usage: python -m veritac_amd.specializations {list | show <id>}"
 
 
 def main(argv=None):
-    parser = argparse.ArgumentParser(description=__doc__)
-    commands = parser.add_subparsers(dest="command", required=True)
-    commands.add_parser("list", help="List scopes without loading hardware dependencies")
-    show = commands.add_parser("show", help="Show one specialization description")
-    show.add_argument("specialization")
-    args = parser.parse_args(argv)
-    try:
-        result = list_specializations() if args.command == "list" else describe(args.specialization)
-    except ValueError as error:
-        parser.error(str(error))
-    print(json.dumps(result, indent=2))
+    args = sys.argv[1:] if argv is None else list(argv)
+    if args == ["list"]:
+        payload = catalog.list_specializations()
+    elif len(args) == 2 and args[0] == "show":
+        try:
+            payload = catalog.describe(args[1])
+        except ValueError as exc:
+            print("%s\nerror: %s" % (USAGE, exc), file=sys.stderr)
+            return 2
+    else:
+        print(USAGE, file=sys.stderr)
+        return 2
+    print(json.dumps(payload, indent=2))
+    return 0
 
 
 if __name__ == "__main__":
-    main()
+    sys.exit(main())
