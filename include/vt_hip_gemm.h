@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define VT_ABI_VERSION 4
+#define VT_ABI_VERSION 5
 
 /* Status codes. */
 #define VT_OK 0
@@ -263,6 +263,37 @@ int vt_gemm_i8_packed(const int8_t *A, const int8_t *Bp, const int32_t *D, int32
                       int64_t lda, int64_t ldd, int64_t ldc, int64_t batch,
                       int64_t stride_a, int64_t stride_bp, int64_t stride_d,
                       int64_t stride_c, int32_t k_split, void *stream);
+
+/*
+ * Run-time compiled loop-nest kernels.
+ *
+ * The reference turns a loop nest (its `Stmt` JSON, README.md:456-503) into
+ * C with emit_c.py (specializations/cpu_gemm/emit_c.py:83-155) and runs it
+ * through gcc as a subprocess (specializations/cpu_gemm/runner.py:65-108).
+ * Here the Python emitter (specializations/hip_gemm/loopnest.py) writes a
+ * HIP kernel instead, and these entry points replace the gcc + subprocess
+ * step: hipRTC compiles the source for gfx950 in process, and the kernel is
+ * launched on the caller's stream.
+ *
+ * vt_rtc_compile: compile `source`, which must define
+ *   extern "C" __global__ void <kernel_name>(...); no device is needed.
+ *   On a compiler error it returns VT_EINVAL and vt_last_error() holds the
+ *   start of the compiler log. *out is a library-owned handle, freed by
+ *   vt_rtc_release.
+ * vt_rtc_code_size: bytes of the compiled code object (negative: VT_E*).
+ * vt_rtc_launch: load the code object on the current device (once) and
+ *   launch grid x block threads; args[i] points at the value of the kernel's
+ *   i-th parameter (hipModuleLaunchKernel's convention) and must match the
+ *   kernel's parameter list.
+ */
+typedef struct vt_rtc_program vt_rtc_program;
+
+int vt_rtc_compile(const char *source, const char *kernel_name, vt_rtc_program **out);
+int64_t vt_rtc_code_size(const vt_rtc_program *program);
+int vt_rtc_launch(vt_rtc_program *program, uint32_t grid_x, uint32_t grid_y, uint32_t grid_z,
+                  uint32_t block_x, uint32_t block_y, uint32_t block_z, void **args,
+                  void *stream);
+void vt_rtc_release(vt_rtc_program *program);
 
 #ifdef __cplusplus
 }

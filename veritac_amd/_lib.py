@@ -14,7 +14,7 @@ import threading
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 DEFAULT_LIB = os.path.join(PKG_DIR, "libvt_hip_gemm.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 VT_OK = 0
 VT_EINVAL = -1
@@ -38,7 +38,8 @@ VARIANTS = tuple(VARIANT_IDS)
 # Every function include/vt_hip_gemm.h declares.
 EXPORTS = ("vt_gemm_i8", "vt_gemm_select", "vt_variant_info", "vt_variant_name",
            "vt_last_error", "vt_sync", "vt_device_count", "vt_abi_version", "vt_replay_i8",
-           "vt_device_query", "vt_packed_b_size", "vt_pack_b_i8", "vt_gemm_i8_packed")
+           "vt_device_query", "vt_packed_b_size", "vt_pack_b_i8", "vt_gemm_i8_packed",
+           "vt_rtc_compile", "vt_rtc_code_size", "vt_rtc_launch", "vt_rtc_release")
 
 # Replay operation codes and status codes (VT_REPLAY_* in include/vt_hip_gemm.h).
 REPLAY_MVIN, REPLAY_LATCH_B, REPLAY_COMPUTE, REPLAY_MVOUT = 1, 2, 3, 4
@@ -118,6 +119,15 @@ def _declare(lib):
     lib.vt_gemm_i8_packed.argtypes = [p, p, p, p, i64, i64, i64, i64, i64, i64, i64,
                                       i64, i64, i64, i64, i32, p]
     lib.vt_gemm_i8_packed.restype = ctypes.c_int
+    lib.vt_rtc_compile.argtypes = [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(p)]
+    lib.vt_rtc_compile.restype = ctypes.c_int
+    lib.vt_rtc_code_size.argtypes = [p]
+    lib.vt_rtc_code_size.restype = ctypes.c_int64
+    u32 = ctypes.c_uint32
+    lib.vt_rtc_launch.argtypes = [p, u32, u32, u32, u32, u32, u32, ctypes.POINTER(p), p]
+    lib.vt_rtc_launch.restype = ctypes.c_int
+    lib.vt_rtc_release.argtypes = [p]
+    lib.vt_rtc_release.restype = None
 
 
 def load_library():
@@ -244,3 +254,38 @@ def gemm_packed_raw(A_ptr, Bp_ptr, D_ptr, C_ptr, M, N, K, lda, ldd, ldc, batch=1
     st = lib.vt_gemm_i8_packed(A_ptr, Bp_ptr, D_ptr, C_ptr, M, N, K, lda, ldd, ldc, batch,
                                stride_a, stride_bp, stride_d, stride_c, k_split, stream)
     return check(st, "vt_gemm_i8_packed")
+
+
+class RtcProgram:
+    """A kernel compiled at run time by vt_rtc_compile (freed with the object)."""
+
+    def __init__(self, source, kernel_name):
+        lib = load_library()
+        handle = ctypes.c_void_p()
+        check(lib.vt_rtc_compile(source.encode(), kernel_name.encode(), ctypes.byref(handle)),
+              "vt_rtc_compile")
+        self._lib, self._handle, self.kernel_name = lib, handle, kernel_name
+
+    @property
+    def code_size(self):
+        return self._lib.vt_rtc_code_size(self._handle)
+
+    def launch(self, grid, block, arg_values, stream=None):
+        """Launch with `arg_values`: ctypes scalars or pointers, one per kernel
+        parameter in order (kept alive for the call)."""
+        ptrs = (ctypes.c_void_p * max(1, len(arg_values)))(
+            *[ctypes.cast(ctypes.byref(v), ctypes.c_void_p) for v in arg_values])
+        g = tuple(grid) + (1,) * (3 - len(grid))
+        b = tuple(block) + (1,) * (3 - len(block))
+        check(self._lib.vt_rtc_launch(self._handle, *g, *b, ptrs, stream), "vt_rtc_launch")
+
+    def close(self):
+        if self._handle:
+            self._lib.vt_rtc_release(self._handle)
+            self._handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

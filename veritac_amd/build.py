@@ -26,6 +26,8 @@ HIPCC_FLAGS = [
     "-Wall", "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
+# hipRTC compiles the emitted loop-nest kernels at run time.
+LINK_FLAGS = ["-L/opt/rocm/lib", "-lhiprtc", "-Wl,-rpath,/opt/rocm/lib"]
 
 
 def hipcc():
@@ -37,7 +39,7 @@ def hipcc():
 
 def build(verbose=False):
     tmp = LIB_PATH + ".tmp"
-    cmd = [hipcc()] + HIPCC_FLAGS + ["-I", INCLUDE] + SOURCES + ["-o", tmp]
+    cmd = [hipcc()] + HIPCC_FLAGS + ["-I", INCLUDE] + SOURCES + LINK_FLAGS + ["-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)

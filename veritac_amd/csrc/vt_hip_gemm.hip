@@ -40,6 +40,7 @@
 // the clamped B rows there contribute nothing.
 
 #include <hip/hip_runtime.h>
+#include <hip/hiprtc.h>
 
 #include <stdarg.h>
 #include <stdint.h>
@@ -50,6 +51,7 @@
 #include <mutex>
 #include <string>
 #include <utility>
+#include <vector>
 
 #include "vt_hip_gemm.h"
 
@@ -1758,6 +1760,114 @@ int vt_gemm_i8_packed(const int8_t *A, const int8_t *Bp, const int32_t *D, int32
     if (rc) return rc;
   }
   return VT_OK;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Run-time compiled loop-nest kernels (hipRTC)
+// ---------------------------------------------------------------------------
+
+// A gfx950 code object compiled from source, and its module / function on
+// every device it has been launched on.
+struct vt_rtc_program {
+  std::string kernel;
+  std::vector<char> code;
+  std::mutex mu;
+  std::map<int, std::pair<hipModule_t, hipFunction_t>> loaded;
+};
+
+extern "C" {
+
+int vt_rtc_compile(const char *source, const char *kernel_name, vt_rtc_program **out) {
+  g_err.clear();
+  if (!source || !kernel_name || !out) return fail(VT_EINVAL, "vt_rtc_compile: null argument");
+  *out = nullptr;
+  if (!kernel_name[0] || strlen(kernel_name) > 255)
+    return fail(VT_EINVAL, "vt_rtc_compile: bad kernel name");
+  hiprtcProgram prog;
+  hiprtcResult r = hiprtcCreateProgram(&prog, source, "loopnest.hip", 0, nullptr, nullptr);
+  if (r != HIPRTC_SUCCESS) return fail(VT_EHIP, "hiprtcCreateProgram: %s", hiprtcGetErrorString(r));
+  // Same code-generation rules as the library's own kernels: gfx950, no
+  // packed FP32 instructions; no FMA contraction, so floating-point loop
+  // nests round like the C they are emitted from.
+  const char *opts[] = {"--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off",
+                        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"};
+  r = hiprtcCompileProgram(prog, (int)(sizeof opts / sizeof opts[0]), opts);
+  if (r != HIPRTC_SUCCESS) {
+    size_t n = 0;
+    std::string log;
+    if (hiprtcGetProgramLogSize(prog, &n) == HIPRTC_SUCCESS && n > 0) {
+      log.resize(n);
+      hiprtcGetProgramLog(prog, &log[0]);
+    }
+    hiprtcDestroyProgram(&prog);
+    if (log.size() > 400) log = log.substr(0, 400) + "...";
+    return fail(VT_EINVAL, "hiprtcCompileProgram: %s: %s", hiprtcGetErrorString(r), log.c_str());
+  }
+  size_t size = 0;
+  r = hiprtcGetCodeSize(prog, &size);
+  std::vector<char> code(size);
+  if (r == HIPRTC_SUCCESS && size > 0) r = hiprtcGetCode(prog, code.data());
+  hiprtcDestroyProgram(&prog);
+  if (r != HIPRTC_SUCCESS || size == 0)
+    return fail(VT_EHIP, "hiprtcGetCode: %s", hiprtcGetErrorString(r));
+  vt_rtc_program *p = new vt_rtc_program;
+  p->kernel = kernel_name;
+  p->code = std::move(code);
+  *out = p;
+  return VT_OK;
+}
+
+int64_t vt_rtc_code_size(const vt_rtc_program *p) {
+  if (!p) return fail(VT_EINVAL, "vt_rtc_code_size: null program");
+  return (int64_t)p->code.size();
+}
+
+int vt_rtc_launch(vt_rtc_program *p, uint32_t grid_x, uint32_t grid_y, uint32_t grid_z,
+                  uint32_t block_x, uint32_t block_y, uint32_t block_z, void **args,
+                  void *stream) {
+  g_err.clear();
+  if (!p) return fail(VT_EINVAL, "vt_rtc_launch: null program");
+  if (!grid_x || !grid_y || !grid_z || !block_x || !block_y || !block_z ||
+      (uint64_t)block_x * block_y * block_z > 1024 || grid_y > 65535 || grid_z > 65535)
+    return fail(VT_EINVAL, "vt_rtc_launch: bad launch shape");
+  int dev = 0;
+  DeviceState *st = nullptr;
+  int rc = current_device(&dev, &st);
+  if (rc) return rc;
+  hipFunction_t fn = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(p->mu);
+    auto it = p->loaded.find(dev);
+    if (it == p->loaded.end()) {
+      hipModule_t mod = nullptr;
+      VT_HIP_CHECK(hipModuleLoadData(&mod, p->code.data()));
+      hipError_t e = hipModuleGetFunction(&fn, mod, p->kernel.c_str());
+      if (e != hipSuccess) {
+        (void)hipModuleUnload(mod);
+        return fail(VT_EINVAL, "kernel %s not in the compiled module: %s", p->kernel.c_str(),
+                    hipGetErrorString(e));
+      }
+      p->loaded[dev] = std::make_pair(mod, fn);
+    } else {
+      fn = it->second.second;
+    }
+  }
+  VT_HIP_CHECK(hipModuleLaunchKernel(fn, grid_x, grid_y, grid_z, block_x, block_y, block_z, 0,
+                                     (hipStream_t)stream, args, nullptr));
+  return VT_OK;
+}
+
+void vt_rtc_release(vt_rtc_program *p) {
+  if (!p) return;
+  int cur = -1;
+  const bool have_cur = hipGetDevice(&cur) == hipSuccess;
+  for (auto &kv : p->loaded) {
+    if (hipSetDevice(kv.first) == hipSuccess) (void)hipModuleUnload(kv.second.first);
+  }
+  if (have_cur && !p->loaded.empty()) (void)hipSetDevice(cur);
+  delete p;
 }
 
 }  // extern "C"
