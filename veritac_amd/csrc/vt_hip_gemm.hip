@@ -569,6 +569,13 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_dma_kernel(GemmArgs p) {
 
   int gs = 0;   // global slice index
   for (int it = 0; it < ntiles; ++it) {
+    // Once per tile: wait for every LDS read and scalar load. The compiler
+    // hoists epilogue kernel-argument loads (s_load) above the tile loop, and
+    // scalar loads retire out of order with LDS reads; left pending into the
+    // k loop they make every step open with lgkmcnt(0), a full LDS round trip
+    // on the first MFMA of each 64-deep slice. Cleared here, the steps keep
+    // their early fragment reads in flight across the barrier.
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0); vmcnt, expcnt untouched
     // Explicit schedule over the 32 MFMA slots of a slice, one MFMA per
     // scheduling region: slots 0-15 multiply the k 0..31 fragments of slice
     // gs while the k 32..63 fragments of slice gs are read (one per slot, in
