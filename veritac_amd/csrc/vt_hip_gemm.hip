@@ -785,7 +785,10 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(SkinnyArgs p) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int row = g * 4 + e;
-      if (row < M) wsb[(int64_t)row * N + col] = acc[e];
+      // Non-temporal: the partials are read once, by the next kernel, and
+      // kept out of L2 they need no writeback at the kernel boundary
+      // (measured 15.4 -> 15.1 us per decode step at K = 4096, N = 14336).
+      if (row < M) __builtin_nontemporal_store(acc[e], wsb + (int64_t)row * N + col);
     }
   }
 }
@@ -809,9 +812,9 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(ReduceArgs p) {
   const int64_t e = i * 4;
   const int row = (int)(e / p.N), col = (int)(e - (int64_t)row * p.N);
   const int32_t *w = p.ws + (int64_t)bidx * p.k_split * p.M * p.N + e;
-  v4i s = *(const v4i *)w;
+  v4i s = __builtin_nontemporal_load((const v4i *)w);
   for (int q = 1; q < p.k_split; ++q) {
-    const v4i o = *(const v4i *)(w + (int64_t)q * p.M * p.N);
+    const v4i o = __builtin_nontemporal_load((const v4i *)(w + (int64_t)q * p.M * p.N));
 #pragma unroll
     for (int t = 0; t < 4; ++t) s[t] = add_wrap(s[t], o[t]);
   }
@@ -975,7 +978,7 @@ __global__ __launch_bounds__(64 * WAVES) void packed_skinny_kernel(PackedArgs p)
       if (HAS_D) s = add_wrap(s, Db[(int64_t)row * p.ldd + col]);
       Cb[(int64_t)row * p.ldc + col] = s;
     } else {
-      wsb[(int64_t)row * p.N + col] = s;
+      __builtin_nontemporal_store(s, wsb + (int64_t)row * p.N + col);
     }
   }
 }
