@@ -300,6 +300,28 @@ def test_full_tile_dma_path(dev, shape):
     assert np.array_equal(gpu_gemm(dev, A3, B3, D3, variant="mfma_256x256"), go.gemm_i8(A3, B3, D3))
 
 
+# Persistent-kernel shapes where workgroups walk several tiles, some one more
+# than others (529 and 600 tiles over 256 workgroups), k loops of 2 and of an
+# odd 3 slices (the slice stream crosses tile boundaries every few steps),
+# batches walked by one grid, repeated into poisoned outputs.
+MULTI_TILE_SHAPES = [(5120, 7680, 512, 1), (5888, 5888, 128, 1), (4096, 8192, 192, 1),
+                     (2048, 2048, 320, 8)]
+
+
+@pytest.mark.parametrize("shape", MULTI_TILE_SHAPES)
+def test_staggered_tile_schedule(dev, shape):
+    m, n, k, batch = shape
+    rng = np.random.default_rng(m + n + k + batch)
+    A = rng.integers(-128, 128, (batch, m, k) if batch > 1 else (m, k), dtype=np.int8)
+    B = rng.integers(-128, 128, (batch, k, n) if batch > 1 else (k, n), dtype=np.int8)
+    tiles = batch * (m // 256) * (n // 256)
+    assert tiles >= 512, "shape must give every workgroup at least two tiles"
+    say("multi-tile", shape, "tiles", tiles)
+    want = go.gemm_i8(A, B)
+    for _ in range(3):
+        assert np.array_equal(gpu_gemm(dev, A, B, variant="mfma_256x256"), want), shape
+
+
 def test_full_tile_repeated_launches_are_stable(dev):
     """Many back-to-back launches of the pipelined kernels give identical,
     exact results (a stage published too early would show as a mismatch)."""
