@@ -153,6 +153,25 @@ __device__ __forceinline__ void store_tile(const v16i (&acc)[MI][NI], int32_t *C
   }
 }
 
+// Initial partial sums D of one wave's tile, in the accumulator layout of
+// store_tile, loaded into registers (rows or columns past M, N read 0).
+template <int MI, int NI, bool EDGE>
+__device__ __forceinline__ void load_d_tile(int32_t (&d)[MI][NI][16], const int32_t *Db,
+                                            int64_t ldd, int row0, int col0, int M, int N,
+                                            int lane) {
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni) {
+      const int col = col0 + ni * 32 + (lane & 31);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int row = row0 + mi * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+        d[mi][ni][e] = (!EDGE || (row < M && col < N)) ? Db[(int64_t)row * ldd + col] : 0;
+      }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Compute-bound MFMA kernel
 // ---------------------------------------------------------------------------
@@ -329,6 +348,16 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma_kernel(GemmArgs p) {
   // wait on LDS latency across steps. The single barrier per step also
   // guarantees every wave has finished reading buffer kt%3 before step kt+1
   // overwrites it with slice kt+3.
+  // Small wave tiles (at most 4 accumulator blocks, 64 registers) load their
+  // initial partial sums D here, so that memory round trip overlaps the k
+  // loop instead of following it: the epilogue's block-by-block D loads
+  // otherwise add ~6 us to a 128^3..512^3 GEMM.
+  constexpr bool D_EARLY = HAS_D && MI * NI <= 4;
+  int32_t d_pre[D_EARLY ? MI : 1][D_EARLY ? NI : 1][16];
+  if constexpr (D_EARLY)
+    load_d_tile<MI, NI, EDGE>(d_pre, p.D + bidx * p.sd, p.ldd, m0 + wm * WTM, n0 + wn * WTN, M, N,
+                              lane);
+
   v4i ra0[CA], rb0[CB], ra1[CA], rb1[CB];
   load_slice(0, ra0, rb0);
   store_slice(0, ra0, rb0);
@@ -381,8 +410,19 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma_kernel(GemmArgs p) {
     step(kt + 1, ra1, rb1);
   }
 
-  store_tile<MI, NI, EDGE, HAS_D>(acc, p.C + bidx * p.sc, HAS_D ? p.D + bidx * p.sd : nullptr,
-                                  p.ldc, p.ldd, m0 + wm * WTM, n0 + wn * WTN, M, N, lane);
+  if constexpr (D_EARLY) {
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[mi][ni][e] = add_wrap(acc[mi][ni][e], d_pre[mi][ni][e]);
+    store_tile<MI, NI, EDGE, false>(acc, p.C + bidx * p.sc, nullptr, p.ldc, p.ldd,
+                                    m0 + wm * WTM, n0 + wn * WTN, M, N, lane);
+  } else {
+    store_tile<MI, NI, EDGE, HAS_D>(acc, p.C + bidx * p.sc, HAS_D ? p.D + bidx * p.sd : nullptr,
+                                    p.ldc, p.ldd, m0 + wm * WTM, n0 + wn * WTN, M, N, lane);
+  }
 }
 
 // ---------------------------------------------------------------------------
