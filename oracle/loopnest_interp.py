@@ -2,12 +2,16 @@
 
 Executes a loop nest exactly as the C that the reference's emitter writes
 would run it (specializations/cpu_gemm/emit_c.py:83-155): loops in program
-order, `for (v = lo; v < hi; v++)`, integer division and modulo truncating
-toward zero as in C, flat buffers indexed either with the reference's
-stride-1000 rule (emit_c.py:29-44) or row-major with declared shapes. Values
-are Python ints (exact, then wrapped to the buffer's width on store) or
-floats (float64 buffers). It walks the JSON itself and shares no code with
-the HIP emitter it checks.
+order, `for (v = lo; v < hi; v++)` with `hi` evaluated before every
+iteration, integer division and modulo truncating toward zero as in C, flat
+buffers indexed either with the reference's stride-1000 rule
+(emit_c.py:29-44) or row-major with declared shapes. A store's value is
+computed in floating point when the stored-to buffer or a buffer read in the
+value (outside its indices) is floating point, else in exact Python ints
+wrapped to the buffer's width on store; indices and loop bounds are ints,
+and a floating value read there truncates toward zero. Buffers allocated by
+the nest are float64 when any given buffer is floating point, else int64.
+It walks the JSON itself and shares no code with the HIP emitter it checks.
 
 Pinned by closed forms in tests/test_loopnest_host.py: the naive matmul nest
 and its tiled / reordered forms give A @ B (and D + A @ B when C starts at
@@ -41,7 +45,8 @@ def _eval(e, env, ctx, floating):
     if tag == "var":
         return float(env[e["name"]]) if floating else env[e["name"]]
     if tag == "bufRead":
-        return ctx.bufs[e["buf"]][_flat(e, env, ctx)].item()
+        v = ctx.bufs[e["buf"]][_flat(e, env, ctx)].item()
+        return float(v) if floating else int(v)        # int() truncates toward zero
     a = _eval(e["left"], env, ctx, floating)
     b = _eval(e["right"], env, ctx, floating)
     if tag == "add":
@@ -64,6 +69,16 @@ def _flat(node, env, ctx):
     return flat
 
 
+def _value_bufs(e, out):
+    """Buffers read in expression e, not counting reads inside indices."""
+    if e["tag"] == "bufRead":
+        out.add(e["buf"])
+    elif e["tag"] in ("add", "mul", "div", "mod"):
+        _value_bufs(e["left"], out)
+        _value_bufs(e["right"], out)
+    return out
+
+
 def _store(arr, flat, value):
     if arr.dtype.kind == "f":
         arr[flat] = value
@@ -78,11 +93,11 @@ def _run(s, env, ctx):
     if tag == "skip":
         return
     if tag == "bufWrite":
-        _store(ctx.bufs[s["buf"]], _flat(s, env, ctx), _eval(s["val"], env, ctx, ctx.floating))
+        floating = any(ctx.bufs[b].dtype.kind == "f" for b in _value_bufs(s["val"], {s["buf"]}))
+        _store(ctx.bufs[s["buf"]], _flat(s, env, ctx), _eval(s["val"], env, ctx, floating))
     elif tag == "loop":
         v = _eval(s["lo"], env, ctx, False)
-        hi = _eval(s["hi"], env, ctx, False)
-        while v < hi:
+        while v < _eval(s["hi"], env, ctx, False):
             env[s["var"]] = v
             _run(s["body"], env, ctx)
             v += 1
@@ -110,8 +125,9 @@ def run(stmt, buffers, shapes=None, layout="dense"):
     """Execute `stmt` over flat numpy buffers {name: 1-D array}, in place.
 
     shapes: {name: dims} for layout "dense" (row-major); layout "reference"
-    uses the stride-1000 flat index. Floating-point arithmetic is used when
-    any buffer is floating point, exact integers otherwise.
+    uses the stride-1000 flat index. Each store computes in floating point
+    when its own buffer or a buffer its value reads is floating point, in
+    exact integers otherwise.
     """
     floating = any(b.dtype.kind == "f" for b in buffers.values())
     _run(stmt, {}, _Ctx(dict(buffers), dict(shapes or {}), layout, floating))

@@ -13,6 +13,7 @@ import pytest
 torch = pytest.importorskip("torch")
 
 from loopnest_tactics import reorder, tile
+from test_loopnest_host import DISJOINT_CASES
 from oracle import gemm_oracle as go
 from oracle import loopnest_interp as li
 from veritac_amd import _lib
@@ -181,3 +182,115 @@ def test_kernel_reuse_across_calls(dev):
         torch.cuda.synchronize()
         assert int(st.item()) == 0
         assert np.array_equal(C.cpu().numpy().reshape(M, N), go.gemm_i8(A, B))
+
+
+# ---------------------------------------------------------------------------
+# Mapping only where threads own disjoint cells; other edge cases
+# ---------------------------------------------------------------------------
+
+def _run_vs_interp(dev, stmt, decl, inputs, stream=None):
+    """Launch the nest, then compare every buffer with the sequential oracle."""
+    k = ln.LoopNestKernel(stmt, decl)
+    t = {b: torch.from_numpy(inputs[b].copy()).to(dev) for b in decl}
+    status = k(t, stream=stream)
+    torch.cuda.synchronize()
+    bufs = {b: inputs[b].copy() for b in decl}
+    li.run(stmt, bufs, {b: decl[b]["shape"] for b in decl})
+    for b in decl:
+        assert np.array_equal(t[b].cpu().numpy(), bufs[b]), b
+    return k, int(status.item())
+
+
+def _inputs(decl, seed):
+    rng = np.random.default_rng(seed)
+    out = {}
+    for b, d in decl.items():
+        n = int(np.prod(d["shape"]))
+        if d["dtype"] in ("float32", "float64"):
+            out[b] = rng.uniform(-4, 4, n).astype(d["dtype"])
+        else:
+            out[b] = rng.integers(-100, 100, n).astype(d["dtype"])
+    return out
+
+
+GPU_DISJOINT = [c for c in DISJOINT_CASES if c[0] not in ("row_spill", "data_bound")]
+
+
+@pytest.mark.parametrize("name,stmt,decl,want", GPU_DISJOINT, ids=[c[0] for c in GPU_DISJOINT])
+def test_order_dependent_nests_match_the_sequential_oracle(dev, name, stmt, decl, want):
+    say("disjoint", name, want)
+    k, st = _run_vs_interp(dev, stmt, decl, _inputs(decl, len(name)))
+    assert st == 0 and k.info["mapped"] == want
+
+
+def test_loop_bound_is_reevaluated_every_iteration(dev):
+    stmt = {"tag": "loop", "var": "i", "lo": lit(0), "hi": rd("Y", lit(0)), "ann": "none",
+            "body": wr("Y", [lit(0)], {"tag": "add", "left": rd("Y", lit(0)), "right": lit(-1)})}
+    k, st = _run_vs_interp(dev, stmt, {"Y": {"dtype": "int32", "shape": (1,)}},
+                           {"Y": np.array([5], np.int32)})
+    assert st == 0 and k.info["mapped"] == []
+
+
+def test_each_store_typed_by_its_own_buffers_and_int64_wraps(dev):
+    mul = lambda a, b: {"tag": "mul", "left": a, "right": b}      # noqa: E731
+    stmt = {"tag": "seq",
+            "s1": wr("Z", [lit(0)], mul(rd("W", lit(0)), rd("W", lit(0)))),
+            "s2": {"tag": "seq", "s1": wr("F", [lit(0)], mul(rd("W", lit(1)), lit(3))),
+                   "s2": wr("Z", [lit(1)], mul(rd("W", lit(1)), rd("W", lit(1))))}}
+    decl = {"W": {"dtype": "int64", "shape": (2,)}, "Z": {"dtype": "int64", "shape": (2,)},
+            "F": {"dtype": "float64", "shape": (1,)}}
+    w = np.array([2**40 + 3, 2**31 + 1], np.int64)
+    k, st = _run_vs_interp(dev, stmt, decl, {"W": w, "Z": np.zeros(2, np.int64),
+                                             "F": np.zeros(1)})
+    assert st == 0
+
+
+def test_floating_index_truncates_toward_zero(dev):
+    stmt = loop("i", 2, wr("Y", [var("i")], rd("S", rd("X", var("i")))))
+    decl = {"X": {"dtype": "float64", "shape": (2,)}, "S": {"dtype": "int64", "shape": (3,)},
+            "Y": {"dtype": "int64", "shape": (2,)}}
+    _, st = _run_vs_interp(dev, stmt, decl, {"X": np.array([2.7, -0.5]),
+                                             "S": np.array([10, 20, 30], np.int64),
+                                             "Y": np.zeros(2, np.int64)})
+    assert st == 0
+
+
+def test_caller_stream_is_ordered_after_the_current_one(dev):
+    M, K, N = 64, 96, 80
+    decl = {"A": {"dtype": "int8", "shape": (M, K)}, "B": {"dtype": "int8", "shape": (K, N)},
+            "C": {"dtype": "int32", "shape": (M, N)}}
+    k = ln.LoopNestKernel(ln.matmul_stmt(M, K, N), decl)
+    rng = np.random.default_rng(5)
+    A = rng.integers(-128, 128, (M, K), dtype=np.int8)
+    B = rng.integers(-128, 128, (K, N), dtype=np.int8)
+    side = torch.cuda.Stream(device=dev)
+    for rep in range(3):
+        t = {"A": torch.from_numpy(A.reshape(-1)).to(dev), "B": torch.from_numpy(B.reshape(-1)).to(dev),
+             "C": torch.full((M * N,), 7, dtype=torch.int32, device=dev)}
+        side.wait_stream(torch.cuda.current_stream(dev))      # inputs are filled on the current stream
+        status = k(t, stream=side.cuda_stream)
+        side.synchronize()
+        assert int(status.item()) == 0
+        assert np.array_equal(t["C"].cpu().numpy().reshape(M, N),
+                              go.gemm_i8(A, B, np.full((M, N), 7, np.int32)))
+    res = ln.benchmark_matmul(ln.matmul_stmt(24, 40, 56), 24, 40, 56, num_runs=3,
+                              stream=side.cuda_stream)
+    assert res["correct"] and res["status"] == 0 and res["gpu_time_ms"] > 0
+
+
+def test_empty_loop_launches_nothing(dev):
+    k = ln.LoopNestKernel(loop("i", 0, wr("Y", [var("i")], lit(1))),
+                          {"Y": {"dtype": "int32", "shape": (4,)}})
+    y = torch.full((4,), -3, dtype=torch.int32, device=dev)
+    assert int(k({"Y": y}).item()) == 0
+    assert y.cpu().tolist() == [-3] * 4
+
+
+def test_nest_without_buffers_reports_division_by_zero(dev):
+    stmt = {"tag": "loop", "var": "i", "lo": lit(0),
+            "hi": {"tag": "div", "left": lit(1), "right": lit(0)}, "ann": "none", "body": {"tag": "skip"}}
+    k = ln.LoopNestKernel(stmt, {})
+    assert k.info["params"] == [] and k.info["threads"] == 1
+    status = k({})
+    torch.cuda.synchronize()
+    assert int(status.item()) == ln.STATUS_DIV0

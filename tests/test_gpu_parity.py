@@ -265,7 +265,19 @@ def test_backend_run_on_side_stream(dev):
     with torch.cuda.stream(s):
         C = hg.run(plan, A, B)
     s.synchronize()
-    assert np.array_equal(C.cpu().numpy(), go.gemm_i8(A.cpu().numpy(), B.cpu().numpy()))
+    want = go.gemm_i8(A.cpu().numpy(), B.cpu().numpy())
+    assert np.array_equal(C.cpu().numpy(), want)
+    # a raw stream handle while torch's current stream stays the default one:
+    # outputs allocated here are recorded as used on it
+    s.wait_stream(torch.cuda.current_stream(dev))
+    C2 = hg.run(plan, A, B, stream=s.cuda_stream)
+    W = B[:, :256].contiguous()
+    Bp = hg.pack_b(W, stream=s.cuda_stream)
+    x = A[:16].contiguous()
+    C3 = hg.run(hg.make_plan(16, 256, 256, variant="skinny_packed"), x, Bp, stream=s.cuda_stream)
+    s.synchronize()
+    assert np.array_equal(C2.cpu().numpy(), want)
+    assert np.array_equal(C3.cpu().numpy(), want[:16, :256])
     flat = hg.run_flat(hg.make_plan(16, 16, 16), [1] * 256, [-2] * 256)
     assert flat == [-32] * 256
 

@@ -215,3 +215,243 @@ def test_kernel_call_refuses_bad_tensors_before_launch():
         k(dict(ok, C=torch.zeros(15, dtype=torch.int32)))
     with pytest.raises(ln.LoopNestError, match="missing tensor"):
         k({"A": ok["A"], "B": ok["B"]})
+
+
+# ---------------------------------------------------------------------------
+# Disjointness: threads of the mapped loops never share a cell
+# ---------------------------------------------------------------------------
+
+def add(a, b):
+    return {"tag": "add", "left": a, "right": b}
+
+
+def mul(a, b):
+    return {"tag": "mul", "left": a, "right": b}
+
+
+def bump(buf, *idx):
+    """buf[idx] = buf[idx] * 2 + 1: one index list, order-dependent value."""
+    return wr(buf, list(idx), add(mul(rd(buf, *idx), lit(2)), lit(1)))
+
+
+def y_decl(n, extra=None):
+    decl = {"Y": {"dtype": "int32", "shape": (n,)}}
+    decl.update(extra or {})
+    return decl
+
+
+def _copy_and_reduce(row):
+    """Y[row*i + k] = X[i, k]; W[i] = W[i] + X[i, k]."""
+    return {"tag": "seq",
+            "s1": wr("Y", [add(mul(var("i"), lit(row)), var("k"))], rd("X", var("i"), var("k"))),
+            "s2": wr("W", [var("i")], add(rd("W", var("i")), rd("X", var("i"), var("k"))))}
+
+
+X34 = {"X": {"dtype": "int32", "shape": (3, 4)}}
+X48 = {"X": {"dtype": "int32", "shape": (4, 8)}}
+
+DISJOINT_CASES = [
+    # Y[i + j]: both loops mention the cell, and (0,1), (1,0) collide
+    ("sum_of_mapped", loop("i", 4, loop("j", 4, bump("Y", add(var("i"), var("j")))), "parallel"),
+     y_decl(8), []),
+    # Y[j % 2]: not affine
+    ("modulo", loop("j", 4, bump("Y", {"tag": "mod", "left": var("j"), "right": lit(2)})),
+     y_decl(2), []),
+    # Y[2i + j]: j < 2 separates, j < 3 does not
+    ("radix_ok", loop("i", 4, loop("j", 2, bump("Y", add(mul(var("i"), lit(2)), var("j"))))),
+     y_decl(8), ["i", "j"]),
+    ("radix_overlap", loop("i", 4, loop("j", 3, bump("Y", add(mul(lit(2), var("i")), var("j"))))),
+     y_decl(9), []),
+    # C[i, j] with j running past the row aliases the next row
+    ("row_spill", loop("i", 4, loop("j", 8, bump("Y", var("i"), var("j")))),
+     {"Y": {"dtype": "int32", "shape": (4, 4)}}, []),
+    ("row_exact", loop("i", 4, loop("j", 4, bump("Y", var("i"), var("j")))),
+     {"Y": {"dtype": "int32", "shape": (4, 4)}}, ["i", "j"]),
+    # a time loop outside: t stays sequential, j is mapped
+    ("time_loop", loop("t", 3, loop("j", 4, wr("Y", [var("j")], add(rd("Y", var("j")),
+                                                                   rd("X", var("t"), var("j")))))),
+     y_decl(4, X34), ["j"]),
+    # a sequential inner loop (it also reduces into W[i]) in the index:
+    # 8i + k separates k < 8, 4i + k does not
+    ("inner_digit", loop("i", 4, loop("k", 8, _copy_and_reduce(8), "unrolled")),
+     y_decl(32, dict(X48, W={"dtype": "int32", "shape": (4,)})), ["i"]),
+    ("inner_overlap", loop("i", 4, loop("k", 8, _copy_and_reduce(4))),
+     y_decl(32, dict(X48, W={"dtype": "int32", "shape": (4,)})), []),
+    # triangular inner loop: k < i + 1 <= 4, so 4i + k separates
+    ("triangular", loop("i", 4, {"tag": "loop", "var": "k", "lo": lit(0), "hi": add(var("i"), lit(1)),
+                                 "ann": "none", "body": bump("Y", add(mul(var("i"), lit(4)), var("k")))}),
+     y_decl(16), ["i"]),
+    # a bound read from memory leaves k's range unknown
+    ("data_bound", loop("i", 4, {"tag": "loop", "var": "k", "lo": lit(0), "hi": rd("X", var("i"), lit(0)),
+                                 "ann": "none", "body": bump("Y", add(mul(var("i"), lit(4)), var("k")))}),
+     y_decl(16, X48), []),
+    # negative coefficient: Y[7 - i]
+    ("reversed", loop("i", 8, bump("Y", add(lit(7), mul(lit(-1), var("i")))), "parallel"),
+     y_decl(8), ["i"]),
+]
+
+
+@pytest.mark.parametrize("name,stmt,decl,want", DISJOINT_CASES, ids=[c[0] for c in DISJOINT_CASES])
+def test_mapping_only_where_threads_own_disjoint_cells(name, stmt, decl, want):
+    info = ln.emit_kernel(stmt, decl)
+    assert info["mapped"] == want
+    if want:        # nothing mapped: nothing to enumerate (and bounds may read memory)
+        _assert_disjoint_by_enumeration(ln.parse_stmt(stmt), set(want), decl, "dense")
+
+
+def test_suppression_note_names_the_collision():
+    stmt = loop("i", 4, loop("j", 4, bump("Y", add(var("i"), var("j"))), "vectorize"), "parallel")
+    notes = ln.emit_kernel(stmt, y_decl(8))["notes"]
+    assert "parallel suppressed on i: iterations may write the same cell" in notes
+    assert "vectorize suppressed on j: iterations may write the same cell" in notes
+
+
+def _points(stmt, env, out):
+    """Every (env, buffer, flat cell) a nest's writes touch, by running its
+    loops (bounds over variables and literals only)."""
+    kind = stmt[0]
+    if kind == "loop":
+        lo = _value(stmt[2], env)
+        v = lo
+        while v < _value(stmt[3], env):
+            _points(stmt[5], dict(env, **{stmt[1]: v}), out)
+            v += 1
+    elif kind == "seq":
+        for s in stmt[1]:
+            _points(s, env, out)
+    elif kind == "write":
+        out.append((env, stmt[1], tuple(_value(i, env) for i in stmt[2])))
+    return out
+
+
+def _value(e, env):
+    if e[0] == "lit":
+        return e[1]
+    if e[0] == "var":
+        return env[e[1]]
+    a, b = _value(e[1], env), _value(e[2], env)
+    if e[0] == "add":
+        return a + b
+    if e[0] == "mul":
+        return a * b
+    assert b != 0
+    q = abs(a) // abs(b) * (1 if (a >= 0) == (b >= 0) else -1)
+    return q if e[0] == "div" else a - b * q
+
+
+def _assert_disjoint_by_enumeration(stmt, mapped, decl, layout):
+    """Brute force: no cell is written by two different mapped tuples."""
+    owner = {}
+    for env, buf, idx in _points(stmt, {}, []):
+        shape = decl[buf]["shape"]
+        flat = 0
+        for d, i in enumerate(idx):
+            flat = flat * (ln.REFERENCE_STRIDE if layout == "reference" else shape[d]) + i
+        key = tuple(sorted((v, env[v]) for v in mapped))
+        assert owner.setdefault((buf, flat), key) == key, (buf, flat, owner[(buf, flat)], key)
+
+
+def test_disjointness_is_sound_on_random_affine_nests():
+    """threads_disjoint never accepts a mapped set whose threads share a
+    cell: random 3-deep nests with affine (sometimes triangular) bounds and
+    affine 1-D or 2-D indices, every subset of the loops checked against
+    enumeration of every iteration point."""
+    import itertools
+    rng = np.random.default_rng(12345)
+    names = ("a", "b", "c")
+    accepted = rejected = 0
+    for trial in range(400):
+        ext = [int(x) for x in rng.integers(1, 5, 3)]
+        coef = [[int(x) for x in rng.integers(-4, 5, 3)] for _ in range(2)]
+        dims = int(rng.integers(1, 3))
+        triangular = bool(rng.integers(0, 3) == 0)
+        idx = []
+        for d in range(dims):
+            e = lit(0)
+            for n, c in zip(names, coef[d]):
+                if c:
+                    e = add(e, mul(lit(c), var(n)))
+            idx.append(e)
+        body = bump("Y", *idx)
+        inner_hi = add(var("b"), lit(1)) if triangular else lit(ext[2])
+        stmt_json = loop("a", ext[0], loop("b", ext[1], {"tag": "loop", "var": "c", "lo": lit(0),
+                                                         "hi": inner_hi, "ann": "none",
+                                                         "body": body}))
+        stmt = ln.parse_stmt(stmt_json)
+        # shift indices to be non-negative and size Y to hold every cell
+        pts = _points(stmt, {}, [])
+        lows = [min(p[2][d] for p in pts) for d in range(dims)]
+        highs = [max(p[2][d] for p in pts) for d in range(dims)]
+        idx = [add(i, lit(-lo)) for i, lo in zip(idx, lows)]
+        stmt_json = loop("a", ext[0], loop("b", ext[1], {"tag": "loop", "var": "c", "lo": lit(0),
+                                                         "hi": inner_hi, "ann": "none",
+                                                         "body": bump("Y", *idx)}))
+        stmt = ln.parse_stmt(stmt_json)
+        decl = {"Y": {"dtype": "int32", "shape": tuple(h - lo + 1 for h, lo in zip(highs, lows))}}
+        for r in range(1, 4):
+            for subset in itertools.combinations(range(3), r):
+                if triangular and 2 in subset:
+                    continue                       # mapped loops need constant bounds
+                mapped = {names[s]: ext[s] for s in subset}
+                if ln.threads_disjoint(stmt, mapped, decl):
+                    accepted += 1
+                    _assert_disjoint_by_enumeration(stmt, set(mapped), decl, "dense")
+                else:
+                    rejected += 1
+        got = ln.emit_kernel(stmt_json, decl)["mapped"]
+        _assert_disjoint_by_enumeration(stmt, set(got), decl, "dense")
+    assert accepted > 200 and rejected > 200       # both verdicts exercised
+
+
+# ---------------------------------------------------------------------------
+# Other edge cases of the emitter and the interpreter
+# ---------------------------------------------------------------------------
+
+def test_literals_must_fit_int64():
+    for v in (2**63, -2**63, 10**30):
+        with pytest.raises(ln.LoopNestError, match="lit value"):
+            ln.parse_expr(lit(v))
+    assert ln.parse_expr(lit(2**63 - 1)) == ("lit", 2**63 - 1)
+
+
+def test_empty_mapped_loop_emits_no_zero_divisor():
+    k = ln.LoopNestKernel(loop("i", 0, wr("Y", [var("i")], lit(1))), y_decl(4))
+    assert k.info["threads"] == 0 and k.info["mapped"] == ["i"]
+    assert "% 0LL" not in k.source and "/= 0LL" not in k.source
+
+
+def test_written_buffers_may_not_overlap_others():
+    k = ln.LoopNestKernel(loop("i", 4, wr("Y", [var("i")], rd("X", var("i")))),
+                          {"X": {"dtype": "int32", "shape": (4,)}, "Y": {"dtype": "int32", "shape": (4,)}})
+    base = torch.zeros(8, dtype=torch.int32)
+    with pytest.raises(ln.LoopNestError, match="overlaps"):
+        k({"X": base[0:4], "Y": base[2:6]})
+    with pytest.raises(ln.LoopNestError, match="GPU only"):   # disjoint views pass that check
+        k({"X": base[0:4], "Y": base[4:8]})
+
+
+def test_interpreter_reevaluates_loop_bounds_like_c():
+    # for (i = 0; i < Y[0]; i++) Y[0] = Y[0] - 1;  from 5: i=0 (5->4), 1 (4->3), 2 (3->2), stop
+    stmt = {"tag": "loop", "var": "i", "lo": lit(0), "hi": rd("Y", lit(0)), "ann": "none",
+            "body": wr("Y", [lit(0)], add(rd("Y", lit(0)), lit(-1)))}
+    y = np.array([5], np.int64)
+    li.run(stmt, {"Y": y}, {"Y": (1,)})
+    assert y[0] == 2
+
+
+def test_interpreter_types_each_store_by_its_own_buffers():
+    # Z = W * W stays exact in integers although a float64 buffer exists
+    w = np.array([2**31 + 1], np.int64)
+    z = np.zeros(1, np.int64)
+    f = np.zeros(1, np.float64)
+    stmt = {"tag": "seq", "s1": wr("Z", [lit(0)], mul(rd("W", lit(0)), rd("W", lit(0)))),
+            "s2": wr("F", [lit(0)], mul(rd("W", lit(0)), lit(3)))}
+    li.run(stmt, {"W": w, "Z": z, "F": f}, {"W": (1,), "Z": (1,), "F": (1,)})
+    assert int(z[0]) == (2**31 + 1) ** 2 and f[0] == 3.0 * (2**31 + 1)
+    # a floating value used as an index truncates toward zero
+    x = np.array([2.7, -0.5])
+    src = np.array([10, 20, 30], np.int64)
+    y = np.zeros(2, np.int64)
+    li.run(loop("i", 2, wr("Y", [var("i")], rd("S", rd("X", var("i"))))),
+           {"X": x, "S": src, "Y": y}, {"X": (2,), "S": (3,), "Y": (2,)})
+    assert y.tolist() == [30, 10]

@@ -1840,9 +1840,11 @@ int vt_rtc_compile(const char *source, const char *kernel_name, vt_rtc_program *
   if (r != HIPRTC_SUCCESS) return fail(VT_EHIP, "hiprtcCreateProgram: %s", hiprtcGetErrorString(r));
   // Same code-generation rules as the library's own kernels: gfx950, no
   // packed FP32 instructions; no FMA contraction, so floating-point loop
-  // nests round like the C they are emitted from.
+  // nests round like the C they are emitted from; signed overflow wraps
+  // (two's complement) instead of being undefined, so an integer nest's
+  // stores keep the low bits of the exact result.
   const char *opts[] = {"--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off",
-                        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"};
+                        "-fwrapv", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"};
   r = hiprtcCompileProgram(prog, (int)(sizeof opts / sizeof opts[0]), opts);
   if (r != HIPRTC_SUCCESS) {
     size_t n = 0;

@@ -445,9 +445,21 @@ def pack_b(B, *, out=None, stream=None):
     if stream is None:
         with torch.cuda.device(B.device):
             stream = torch.cuda.current_stream(B.device).cuda_stream
+    elif out is None:
+        _keep_for_stream(data, stream)
     _lib.pack_b_raw(B.data_ptr(), data.data_ptr(), k, n, B.stride(-2), batch,
                     B.stride(0) if B.dim() == 3 else 0, size, stream)
     return out if out is not None else PackedB(data, k, n, batch)
+
+
+def _keep_for_stream(t, stream):
+    """t was allocated on torch's current stream but is written on the
+    caller's raw stream: record that use, so the caching allocator does not
+    hand t's memory out again while that stream may still be writing it."""
+    torch = _torch()
+    with torch.cuda.device(t.device):
+        if stream != torch.cuda.current_stream(t.device).cuda_stream:
+            t.record_stream(torch.cuda.ExternalStream(stream, device=t.device))
 
 
 def _check_packed(B, plan, device):
@@ -502,7 +514,9 @@ def run(plan, A, B, D=None, *, out=None, stream=None, runner=None):
     validated first and any mismatch raises HipGemmError before a kernel is
     launched. `runner` (plan, A, B, D, C, stream) replaces the native call
     (dependency injection for host-only tests); `stream` is a raw hipStream_t
-    handle, default torch's current stream.
+    handle, default torch's current stream. On another stream the caller
+    orders the operands' producers before it, as with any raw stream; a C
+    allocated here is recorded as used on that stream.
     """
     ok, reason = validate_plan(plan)
     if not ok:
@@ -526,7 +540,8 @@ def run(plan, A, B, D=None, *, out=None, stream=None, runner=None):
         _check_tensor("D", D, c_shape, torch.int32, device)
     elif D is not None:
         raise HipGemmError("plan has_d=False but D was given")
-    if out is None:
+    allocated = out is None
+    if allocated:
         out = torch.empty(c_shape, dtype=torch.int32, device=device)
     else:
         _check_tensor("out", out, c_shape, torch.int32, device)
@@ -538,6 +553,8 @@ def run(plan, A, B, D=None, *, out=None, stream=None, runner=None):
         if stream is None:
             with torch.cuda.device(device):
                 stream = torch.cuda.current_stream(device).cuda_stream
+        elif allocated:
+            _keep_for_stream(out, stream)
     runner(plan, A, B, D, out, stream)
     return out
 
