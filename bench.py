@@ -83,25 +83,28 @@ def time_steps(plan, sets, steps, warmup, stream):
 
 
 def cpu_baseline(A_np, B_np, budget_s=8.0):
-    """Oracle C restatement (i-t-j order, OpenMP over rows) on a row sample."""
+    """Oracle C restatement (i-t-j order, OpenMP over rows) on a row sample,
+    from the fastest build the host runs (-O3 x86-64-v4 where it has AVX-512,
+    else x86-64-v3)."""
     from oracle import cref
     threads = len(os.sched_getaffinity(0))
     omp = os.environ.get("OMP_NUM_THREADS")
     if omp and omp.isdigit():
         threads = min(threads, int(omp))
+    tuned = "v4" if cref.host_has_avx512() else "default"
     K, N = B_np.shape
     rows = 16
     t = 0.0
     while True:
         t0 = time.perf_counter()
-        cref.gemm_i8(A_np[:rows], B_np, threads=threads, order="ikj")
+        cref.gemm_i8(A_np[:rows], B_np, threads=threads, order="ikj", variant=tuned)
         t = time.perf_counter() - t0
         if t > budget_s / 4 or rows >= A_np.shape[0]:
             break
         rows = min(A_np.shape[0], rows * max(2, int(budget_s / 4 / max(t, 1e-3))))
     # faithful i-j-t order (the emitted veritac_scalar_ref loop) on 2 rows
     t0 = time.perf_counter()
-    cref.gemm_i8(A_np[:2], B_np, threads=threads, order="ijk")
+    cref.gemm_i8(A_np[:2], B_np, threads=threads, order="ijk", variant=tuned)
     t_ijk = time.perf_counter() - t0
     ops = 2.0 * rows * N * K
     return {
@@ -110,12 +113,147 @@ def cpu_baseline(A_np, B_np, budget_s=8.0):
         "cores": threads,
         "kind": "port",
         "sample": ("A rows [0:%d) x B %dx%d of the 8192^3 workload (%.1f%% of it), "
-                   "C restatement of veritac_scalar_ref in i-t-j loop order, OpenMP "
-                   "over rows, %.2f s; the emitted i-j-t order runs at %.4f TOPS"
-                   % (rows, K, N, 100.0 * rows / A_np.shape[0], t,
+                   "C restatement of veritac_scalar_ref in i-t-j loop order, gcc -O3 %s, "
+                   "OpenMP over rows, %.2f s; the emitted i-j-t order runs at %.4f TOPS"
+                   % (rows, K, N, 100.0 * rows / A_np.shape[0],
+                      "x86-64-v4" if tuned == "v4" else "x86-64-v3", t,
                       2.0 * 2 * N * K / t_ijk / 1e12)),
         "ms_full_workload_extrapolated": t * A_np.shape[0] / rows * 1e3,
     }
+
+
+def _time_rows(fn, total, budget_s, min_rows=1):
+    """Time fn(rows) on a growing row prefix until one run takes budget_s/4
+    or covers all `total` rows; short full runs are repeated and the median
+    taken. Returns (rows, seconds per run)."""
+    rows = min(total, max(1, min_rows))
+    while True:
+        t0 = time.perf_counter()
+        fn(rows)
+        t = time.perf_counter() - t0
+        if t >= budget_s / 4 or rows >= total:
+            break
+        rows = min(total, rows * max(2, int(budget_s / 4 / max(t, 1e-4))))
+    if t < budget_s / 20:
+        reps = [t]
+        while sum(reps) < budget_s / 4 and len(reps) < 50:
+            t0 = time.perf_counter()
+            fn(rows)
+            reps.append(time.perf_counter() - t0)
+        t = statistics.median(reps)
+    return rows, t
+
+
+def cpu_paths(budget_s=4.0):
+    """The cpu_baseline leg widened to every configuration: the reference's
+    CPU paths timed on this host, beside the GPU figures of the same run.
+
+    (i)  numpy: (A.astype(int64) @ B.astype(int64) [+ D]).astype(int32), one
+         thread (numpy has no integer BLAS); B converted once, untimed.
+    (ii) emitted C: the oracle's restatement of veritac_scalar_ref
+         (backend.py:712-720, i-j-t order, OpenMP over rows on every core)
+         built with the reference runner's -O2 -fopenmp (runner.py:48) and
+         with -O3 for x86-64-v4 (v3 where the host lacks AVX-512), plus the
+         same function in i-t-j order (the form the compiler vectorises).
+    (iii) for configurations 1 and 2, the reference's own cpu_gemm path: the
+         naive loop nest in double over stride-1000 buffers (emit_c.py:29-155)
+         on the runner's inputs, one warm-up and 5 timed runs
+         (runner.py:150-186).
+    Configurations 1, 2 and 4 run in full; 3 and 5 are timed on a row prefix
+    and scaled linearly ("extrapolated").
+    Each slice's numpy and C results are compared (exact integers)."""
+    import numpy as np
+    from oracle import cref
+    from veritac_amd.specializations.hip_gemm import inputs
+    threads = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS")
+    if omp and omp.isdigit():
+        threads = min(threads, int(omp))
+    tuned = "v4" if cref.host_has_avx512() else "default"
+    cpu_model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            cpu_model = next((ln.split(":", 1)[1].strip() for ln in f
+                              if ln.startswith("model name")), "")
+    except OSError:
+        pass
+    out = {"host": {"cores_used": threads, "sched_getaffinity": len(os.sched_getaffinity(0)),
+                    "OMP_NUM_THREADS": omp, "cpu": cpu_model,
+                    "tuned_build": "x86-64-v4" if tuned == "v4" else "x86-64-v3"},
+           "configs": {}}
+    cases = [(1, None), (2, None), (3, None), (4, 1), (4, 16), (5, None)]
+    for cfg, m in cases:
+        batch, M, N, K, has_d, _ = inputs.config_shape(cfg, m)
+        c = inputs.config_inputs(cfg, seed=0, m=m)
+        A = c["A"].reshape(batch * M, K)           # config 3: shared B, rows stacked
+        B, D = c["B"], c["D"]
+        rows_total = batch * M
+        ops_full = 2.0 * rows_total * N * K
+        name = "config_%d" % cfg + ("_m%d" % m if m is not None else "")
+        log("cpu paths", name)
+        B64 = B.astype(np.int64)
+        got = {}
+
+        def numpy_path(rows):
+            r = A[:rows].astype(np.int64) @ B64
+            if D is not None:
+                r += D[:rows]
+            got["numpy"] = r.astype(np.int32)
+
+        def c_path(variant, order):
+            def run(rows):
+                got[variant + order] = cref.gemm_i8(A[:rows], B, None if D is None else D[:rows],
+                                                    threads=threads, order=order, variant=variant)
+            return run
+
+        entry = {"shape": {"batch": batch, "M": M, "N": N, "K": K, "D": has_d}}
+        timed = [("numpy_int64", numpy_path, 1, "numpy"),
+                 ("emitted_c_O2", c_path("O2", "ijk"), threads, "O2ijk"),
+                 ("emitted_c_O3", c_path(tuned, "ijk"), threads, tuned + "ijk"),
+                 ("restated_ikj_O3", c_path(tuned, "ikj"), threads, tuned + "ikj")]
+        rows_seen = {}
+        for key, fn, min_rows, tag in timed:
+            if cfg in (1, 2, 4):
+                min_rows = rows_total
+            rows, t = _time_rows(fn, rows_total, budget_s, min_rows)
+            rows_seen[tag] = rows
+            entry[key] = {"ms": t * rows_total / rows * 1e3, "rows_timed": rows,
+                          "extrapolated": rows < rows_total,
+                          "tops": ops_full / (t * rows_total / rows) / 1e12}
+        # every path's slice agrees with numpy's on their common rows
+        common = min(rows_seen.values())
+        entry["paths_agree"] = all(np.array_equal(got[t][:common], got["numpy"][:common])
+                                   for t in rows_seen)
+        if cfg in (1, 2):
+            entry["cpu_gemm_f64_loopnest"] = _loopnest_f64(cref, M, K, N)
+        out["configs"][name] = entry
+    return out
+
+
+def _loopnest_f64(cref, M, K, N, runs=5):
+    """The reference runner's protocol for its emitted double loop nest:
+    inputs (i*K+k)%7 and (k*N+j)%5 in stride-1000 buffers, C zeroed before
+    each run, one warm-up, mean of `runs` timed runs, checked on every cell."""
+    import numpy as np
+    A = np.fromfunction(lambda i, k: (i * K + k) % 7, (M, K), dtype=np.int64).astype(np.float64)
+    B = np.fromfunction(lambda k, j: (k * N + j) % 5, (K, N), dtype=np.int64).astype(np.float64)
+    flat = {}
+    for name, rows, cols in (("A", M, K), ("B", K, N), ("C", M, N)):
+        flat[name] = np.zeros((rows - 1) * 1000 + cols)
+    for name, mat in (("A", A), ("B", B)):
+        for r in range(mat.shape[0]):
+            flat[name][r * 1000:r * 1000 + mat.shape[1]] = mat[r]
+    cref.matmul_f64_stride1000(flat["A"], flat["B"], flat["C"], M, K, N, variant="O2")  # warm-up
+    times = []
+    for _ in range(runs):
+        flat["C"][:] = 0.0
+        t0 = time.perf_counter()
+        cref.matmul_f64_stride1000(flat["A"], flat["B"], flat["C"], M, K, N, variant="O2")
+        times.append(time.perf_counter() - t0)
+    C = np.array([flat["C"][i * 1000:i * 1000 + N] for i in range(M)])
+    return {"ms": statistics.mean(times) * 1e3, "runs": runs, "threads": 1,
+            "correct": bool(np.array_equal(C, A @ B)),
+            "build": "-O2 -fopenmp (runner.py:48); the nest has no pragma, so one thread"}
 
 
 def bench_decode(dev, steps, warmup, packed=False):
@@ -347,16 +485,22 @@ def main():
     ap.add_argument("--provenance", default=None, metavar="PATH",
                     help="write a hash-bound report of the last timed step's result to PATH")
     ap.add_argument("--workload", choices=("all", "gemm", "decode", "decode_packed", "configs",
-                                           "gemm_operands", "copy"),
+                                           "gemm_operands", "copy", "cpu_paths"),
                     default="all",
                     help="all: the JSON line below; gemm / decode / decode_packed: only that "
                          "kernel (for profiler runs); copy: a plain 1 GiB device copy "
-                         "(counter calibration)")
+                         "(counter calibration); cpu_paths: the reference's CPU paths on "
+                         "every configuration, on this host (no GPU needed)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(--gpus %d requested)" % args.gpus, file=sys.stderr)
         sys.exit(2)
+    if args.workload == "cpu_paths":
+        res = cpu_paths()
+        print(json.dumps(res), flush=True)
+        sys.exit(0 if all(v["paths_agree"] and v.get("cpu_gemm_f64_loopnest", {}).get("correct", True)
+                          for v in res["configs"].values()) else 1)
 
     import numpy as np
     import torch
@@ -445,7 +589,9 @@ def main():
                      "traffic": TRAFFIC_GEMM_8192["read"] + TRAFFIC_GEMM_8192["written"],
                      "traffic_split": TRAFFIC_GEMM_8192,
                      "kernel": "gemm_dma_kernel (256x256, persistent)", "kernel_avg_ms": avg_ms,
-                     "kernel_min_ms": min(durs), "ops_per_launch": ops},
+                     "kernel_min_ms": min(durs), "kernel_median_ms": statistics.median(durs),
+                     "kernel_p90_ms": sorted(durs)[min(len(durs) - 1, int(0.9 * len(durs)))],
+                     "ops_per_launch": ops},
         "parity": {"exact_check_mod_2^32": parity_ok, "vectors": check["vectors"],
                    "method": check["method"]},
     }

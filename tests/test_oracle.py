@@ -207,3 +207,68 @@ def test_reference_vectors_pin_the_byte_mapping():
     stream = go.lcg8_stream(c["m"] * c["k"] + c["k"] * c["n"], c["seed"])
     assert [b - 128 for b in stream[:c["m"] * c["k"]]] == c["A"]
     assert [go.to_int8(b) for b in stream[:c["m"] * c["k"]]] != c["A"]
+
+
+def _oracle_builds():
+    builds = ["default", "O2"]
+    if cref.host_has_avx512():
+        builds.append("v4")
+    return builds
+
+
+@pytest.mark.parametrize("variant", _oracle_builds())
+def test_every_oracle_build_matches_the_spike_outputs_and_brute_force(golden, variant):
+    """The -O2 (reference runner flags) and -O3 builds of the C restatement
+    compute the same function: the recorded Spike outputs and a brute-force
+    sum with D and a K that is not a multiple of 16."""
+    for run in golden["runs"]:
+        A, B = _case_arrays(run, "lcg")
+        want = np.array(decode_cout(run["cout"]["lcg"]), dtype=np.int32).reshape(A.shape[0], B.shape[1])
+        for order in ("ijk", "ikj"):
+            assert np.array_equal(cref.gemm_i8(A, B, order=order, variant=variant), want), run["name"]
+    rng = np.random.default_rng(7)
+    A = rng.integers(-128, 128, (5, 37), dtype=np.int8)
+    B = rng.integers(-128, 128, (37, 11), dtype=np.int8)
+    D = rng.integers(-2**31, 2**31, (5, 11), dtype=np.int64).astype(np.int32)
+    brute = [[(int(D[i, j]) + sum(int(A[i, t]) * int(B[t, j]) for t in range(37)) + 2**31) % 2**32 - 2**31
+              for j in range(11)] for i in range(5)]
+    for order in ("ijk", "ikj"):
+        assert cref.gemm_i8(A, B, D, order=order, variant=variant).tolist() == brute
+
+
+def test_unavailable_builds_refuse_to_load():
+    with pytest.raises(ValueError):
+        cref.load(variant="O7")
+    if not cref.host_has_avx512():
+        with pytest.raises(RuntimeError, match="AVX-512"):
+            cref.load(variant="v4")
+
+
+def _stride1000(mat):
+    rows, cols = mat.shape
+    flat = np.zeros((rows - 1) * 1000 + cols)
+    for r in range(rows):
+        flat[r * 1000:r * 1000 + cols] = mat[r]
+    return flat
+
+
+@pytest.mark.parametrize("variant", ["default", "O2"])
+def test_f64_stride1000_nest_is_the_reference_runner_gemm(variant):
+    """The reference's CPU GEMM (naive nest, stride-1000 double buffers) on the
+    runner's own inputs A = (i*K+k)%7, B = (k*N+j)%5 (runner.py:150-151),
+    at a non-square shape so a swapped index or stride cannot pass; C starts
+    nonzero because the nest accumulates onto it."""
+    M, K, N = 7, 13, 5
+    A = np.fromfunction(lambda i, k: (i * K + k) % 7, (M, K), dtype=np.int64).astype(float)
+    B = np.fromfunction(lambda k, j: (k * N + j) % 5, (K, N), dtype=np.int64).astype(float)
+    C0 = np.arange(M * N, dtype=float).reshape(M, N) - 9.0
+    a, b, c = _stride1000(A), _stride1000(B), _stride1000(C0)
+    cref.matmul_f64_stride1000(a, b, c, M, K, N, variant=variant)
+    got = np.array([[c[i * 1000 + j] for j in range(N)] for i in range(M)])
+    want = C0 + np.array([[sum(A[i, t] * B[t, j] for t in range(K)) for j in range(N)]
+                          for i in range(M)])
+    assert np.array_equal(got, want)
+    # cells between the rows' ends and the next row's start stay untouched
+    assert not np.any(c[N:1000])
+    with pytest.raises(ValueError):
+        cref.matmul_f64_stride1000(a[:10], b, c, M, K, N)
