@@ -10,7 +10,7 @@ synthetic input already resident in HBM. The timed steps cycle through
 256 MB Infinity Cache. Secondary figures: the M=16 x K=4096 x N=14336 decode
 GEMM (configuration 4) in GB/s of algorithmic traffic, once with row-major B
 and once with B prepacked by vt_pack_b_i8 (the pack is timed on its own and
-is not part of the steps).
+is not part of the steps), and the same two at M=1 (secondary_m1).
 
 Prints ONE JSON line with the metric, the roofline of the dominant kernel
 (average launch duration from HIP events recorded on the launch stream), a
@@ -39,8 +39,12 @@ N_SETS = 5
 # profiles/ (FETCH_SIZE scaled by 2.00, WRITE_SIZE by 1.00: the factors a plain
 # 1 GiB copy gives). Update them with the kernels.
 TRAFFIC_GEMM_8192 = {"read": 805.6e6, "written": 269.9e6}
-TRAFFIC_DECODE_M16 = {"read": 58.9e6 + 3.7e6, "written": 3.7e6 + 0.92e6}
-TRAFFIC_DECODE_PACKED_M16 = {"read": 59.3e6, "written": 0.92e6}
+TRAFFIC_DECODE = {  # (packed B, M) -> bytes per step
+    (False, 16): {"read": 58.9e6 + 3.7e6, "written": 3.7e6 + 0.92e6},
+    (True, 16): {"read": 59.3e6, "written": 0.92e6},
+    (False, 1): {"read": 58.78e6 + 0.27e6, "written": 0.26e6 + 0.06e6},
+    (True, 1): {"read": 58.80e6, "written": 0.06e6},
+}
 
 
 def log(*a):
@@ -256,10 +260,11 @@ def _loopnest_f64(cref, M, K, N, runs=5):
             "build": "-O2 -fopenmp (runner.py:48); the nest has no pragma, so one thread"}
 
 
-def bench_decode(dev, steps, warmup, packed=False):
-    """Decode-shaped GEMM (config 4, M=16): `steps` launches captured in one
-    HIP graph (launch overhead would otherwise dominate a ~10-15 us kernel)
-    and replayed; the launches cycle through 6 buffer sets (> 256 MB).
+def bench_decode(dev, steps, warmup, packed=False, m=16):
+    """Decode-shaped GEMM (config 4, M = m of 1 or 16): `steps` launches
+    captured in one HIP graph (launch overhead would otherwise dominate a
+    ~10-15 us kernel) and replayed; the launches cycle through 6 buffer sets
+    (> 256 MB).
 
     packed=False: row-major B (vt_gemm_i8, skinny variant). packed=True: the
     same B packed once per set by pack_b (vt_pack_b_i8, timed separately and
@@ -268,14 +273,14 @@ def bench_decode(dev, steps, warmup, packed=False):
     import torch
     from veritac_amd.specializations.hip_gemm import backend as hg
     from veritac_amd.specializations.hip_gemm import inputs
-    c = inputs.config_inputs(4, seed=0, m=16)
+    c = inputs.config_inputs(4, seed=0, m=m)
     A = torch.from_numpy(c["A"]).to(dev)
     B = torch.from_numpy(c["B"]).to(dev)
-    sets = make_sets(dev, A, B, None, (16, 14336), N_SETS + 1)
+    sets = make_sets(dev, A, B, None, (m, 14336), N_SETS + 1)
     stream = torch.cuda.Stream(dev)
     pack_ms = None
     if packed:
-        plan = hg.make_plan(16, 14336, 4096, variant=hg.PACKED_VARIANT)
+        plan = hg.make_plan(m, 14336, 4096, variant=hg.PACKED_VARIANT)
         packs = [hg.pack_b(s[1], stream=stream.cuda_stream) for s in sets]
         stream.synchronize()
         # the one-time pack, timed on its own: repack every set in place
@@ -291,7 +296,7 @@ def bench_decode(dev, steps, warmup, packed=False):
         pack_ms = statistics.median(times)
         sets = [(s[0], pb, s[2], s[3]) for s, pb in zip(sets, packs)]
     else:
-        plan = hg.make_plan(16, 14336, 4096)
+        plan = hg.make_plan(m, 14336, 4096)
     with torch.cuda.stream(stream):
         for i in range(max(warmup, len(sets))):
             s = sets[i % len(sets)]
@@ -325,9 +330,12 @@ def bench_decode(dev, steps, warmup, packed=False):
     exact = all(verify.exact_check(s[0], B_rm, s[3])["passed"] for s in sets)
     alg = hg.algorithmic_bytes(plan)
     gbps = alg / (ms / 1e3) / 1e9
-    traffic = TRAFFIC_DECODE_PACKED_M16 if packed else TRAFFIC_DECODE_M16
+    traffic = TRAFFIC_DECODE.get((packed, m))
+    split = plan["k_split"] > 1
+    kernels = ("packed_skinny_kernel<4,8,2>" if packed else "skinny_kernel<256,16,2>") + \
+        (" + skinny_reduce_kernel" if split else "") + " per step"
     out = {
-        "metric": ("HBM GB/s @M=16 decode shape (M=16, K=4096, N=14336)"
+        "metric": ("HBM GB/s @M=%d decode shape (M=%d, K=4096, N=14336)" % (m, m)
                    + (", B prepacked" if packed else "")),
         "value": gbps,
         "unit": "GB/s",
@@ -338,9 +346,7 @@ def bench_decode(dev, steps, warmup, packed=False):
         "roofline": {"bound": "hbm", "achieved": gbps, "peak": PEAK_GBPS, "unit": "GB/s",
                      "frac": gbps / PEAK_GBPS,
                      "traffic": (traffic["read"] + traffic["written"]) if traffic else None,
-                     "traffic_split": traffic, "algorithmic_bytes": alg,
-                     "kernels": ("packed_skinny_kernel<4,8,2> per step" if packed else
-                                 "skinny_kernel<256,16,2> + skinny_reduce_kernel per step")},
+                     "traffic_split": traffic, "algorithmic_bytes": alg, "kernels": kernels},
         "parity": ("exact (mod 2^32) on the GPU: 16 projections + checksums, every set"
                    if exact else "MISMATCH"),
         "rotated_sets": len(sets),
@@ -478,7 +484,9 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--no-decode", action="store_true", help="skip the decode-shape figure")
+    ap.add_argument("--no-decode", action="store_true", help="skip the decode-shape figures")
+    ap.add_argument("--decode-m", type=int, choices=(1, 16), default=16,
+                    help="rows M of the decode / decode_packed workloads (default 16)")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the configuration 1-3 figures")
     ap.add_argument("--variant", default="auto", help="kernel variant for the headline GEMM")
@@ -522,18 +530,19 @@ def main():
         sys.exit(0 if all(v["parity"].startswith("exact") for v in res.values()) else 1)
     if args.workload in ("decode", "decode_packed"):
         res = bench_decode(dev, max(args.steps, 6), args.warmup,
-                           packed=args.workload == "decode_packed")
+                           packed=args.workload == "decode_packed", m=args.decode_m)
         print(json.dumps(res), flush=True)
         sys.exit(0 if res["parity"].startswith("exact") else 1)
     decode = None
     if args.workload == "all" and not args.no_decode:
         # The decode figures come first: right after the 8192^3 GEMM the board
         # is still power-throttled and a ~10 us streaming kernel reads ~7% slower.
-        log("decode shape")
-        row_major = bench_decode(dev, 120, args.warmup)
-        log("decode shape, packed B")
-        decode = (row_major, bench_decode(dev, 120, args.warmup, packed=True))
-        torch.cuda.empty_cache()
+        decode = {}
+        for m in (16, 1):
+            for packed in (False, True):
+                log("decode shape M=%d%s" % (m, ", packed B" if packed else ""))
+                decode[(m, packed)] = bench_decode(dev, 120, args.warmup, packed=packed, m=m)
+                torch.cuda.empty_cache()
     configs = None
     if args.workload == "all" and not args.no_configs:
         log("configurations 1-3")
@@ -601,8 +610,11 @@ def main():
         print(json.dumps(result), flush=True)
         sys.exit(0 if parity_ok else 1)
     if decode:
-        result["secondary"], result["secondary_packed_b"] = decode
-        if not all(r["parity"].startswith("exact") for r in decode):
+        result["secondary"] = decode[(16, False)]
+        result["secondary_packed_b"] = decode[(16, True)]
+        result["secondary_m1"] = {"row_major_b": decode[(1, False)],
+                                  "packed_b": decode[(1, True)]}
+        if not all(r["parity"].startswith("exact") for r in decode.values()):
             parity_ok = False
     if configs:
         result["configs_1_to_3"] = configs
