@@ -254,9 +254,11 @@ int vt_pack_b_i8(const int8_t *B, int8_t *Bp, int64_t K, int64_t N, int64_t ldb,
  * stride_bp 0 = one packed B shared by every batch. Needs N % 16 == 0,
  * K % 16 == 0, lda and strides multiples of 16, 16-byte aligned A and Bp.
  * Any M: rows run in groups of 16, each group streaming B once (the kernel
- * is built for M <= 16). k_split: workgroups along K (0 = automatic: 1 when
- * N gives enough column groups, else a split whose partial sums a second
- * kernel adds).
+ * is built for M <= 16). Columns go to workgroups in groups of 8-column
+ * half blocks: whole groups of four 16-column blocks when N gives 192 or
+ * more of them, else smaller groups, about one per CU. k_split: workgroups
+ * along K (0 = automatic: 1 unless even half-block groups are too few, else a
+ * split whose partial sums a second kernel adds).
  */
 int vt_gemm_i8_packed(const int8_t *A, const int8_t *Bp, const int32_t *D, int32_t *C,
                       int64_t M, int64_t N, int64_t K,

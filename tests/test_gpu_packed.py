@@ -206,3 +206,44 @@ def test_repack_in_place(dev):
     assert np.array_equal(Bp.data.cpu().numpy(), pk.pack_b(B2))
     with pytest.raises(HipGemmError, match="out must be"):
         hg.pack_b(to_dev(dev, B2[:, :80]), out=Bp)
+
+
+# N -> (8-column half blocks per group, groups) on a 256-CU MI355X (packed_columns):
+# 400 -> (1, 50): every group is half a block; 3200 -> (2, 200); 4832 -> (3, 202):
+# the last group is the upper half of the last block; 6400 -> (4, 200);
+# 8208 -> (5, 206): last group again an upper half; 11200 -> (6, 234): last group
+# one block; 11600 -> (6, 242); 12224 -> (6, 255); 13600 -> (8, 213): whole
+# groups, the last one two blocks; 17600 -> (8, 275): two rounds of the CUs
+HALF_BLOCK_NS = [400, 3200, 4832, 6400, 8208, 11200, 11600, 12224, 13600, 17600]
+
+
+@pytest.mark.parametrize("n", HALF_BLOCK_NS)
+@pytest.mark.parametrize("m", [1, 16])
+def test_half_block_column_groups_write_every_column_once(dev, m, n):
+    """Column groups that start or end on half a 16-column block: C starts as
+    D (added in place) and every cell must equal D + A.B."""
+    k = 320
+    plan = hg.make_plan(m, n, k, has_d=True, d_max_abs=1 << 20, variant=hg.PACKED_VARIANT)
+    hpw, groups = hg.packed_columns(plan)
+    say("half blocks", m, n, "hpw", hpw, "groups", groups)
+    assert hg.packed_split(plan)[0] == 1          # K = 320: one slice per wave at most
+    rng = np.random.default_rng(n + m)
+    A = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    B = rng.integers(-128, 128, (k, n), dtype=np.int8)
+    D = rng.integers(-2**20, 2**20, (m, n), dtype=np.int32)
+    Dt = to_dev(dev, D)
+    C = hg.run(plan, to_dev(dev, A), hg.pack_b(to_dev(dev, B)), Dt, out=Dt)
+    assert np.array_equal(C.cpu().numpy(), go.gemm_i8(A, B, D))
+
+
+def test_half_block_groups_across_batches(dev):
+    batch, m, k, n = 2, 16, 256, 4800          # 1200 half blocks -> 5 per group, 240 groups
+    plan = hg.make_plan(m, n, k, batch=batch, variant=hg.PACKED_VARIANT)
+    assert hg.packed_columns(plan) == (5, 120)
+    rng = np.random.default_rng(2)
+    A = rng.integers(-128, 128, (batch, m, k), dtype=np.int8)
+    B = rng.integers(-128, 128, (batch, k, n), dtype=np.int8)
+    out = torch.full((batch, m, n), INT32_MIN, dtype=torch.int32, device=dev)
+    C = hg.run(plan, to_dev(dev, A), hg.pack_b(to_dev(dev, B)), out=out).cpu().numpy()
+    for b in range(batch):
+        assert np.array_equal(C[b], go.gemm_i8(A[b], B[b])), b

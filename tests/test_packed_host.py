@@ -75,13 +75,30 @@ def test_library_size_query_matches_layout():
 def test_packed_plans_validate():
     p = hg.make_plan(16, 14336, 4096, variant=hg.PACKED_VARIANT)
     assert hg.validate_plan(p) == (True, "ok")
+    # 896 blocks: 224 whole groups of 4 blocks (8 half blocks)
+    assert hg.packed_columns(p) == (8, 224)
     assert hg.required_resources(p) == (32768, 224)
     assert hg.packed_split(p) == (1, 64)
-    # few column groups: split K; rows beyond 16 run as row groups
+    # 2048 columns: 256 groups of one half block each, no K split
     p = hg.make_plan(40, 2048, 1024, variant=hg.PACKED_VARIANT)
+    assert hg.packed_columns(p) == (1, 256) and hg.packed_split(p) == (1, 16)
+    # few column groups: split K; rows beyond 16 run as row groups
+    p = hg.make_plan(40, 64, 1024, variant=hg.PACKED_VARIANT)
     assert hg.validate_plan(p)[0]
+    assert hg.packed_columns(p) == (1, 8)
     assert hg.packed_split(p) == (2, 8)
-    assert hg.required_resources(p)[1] == 32 * 2 * 3
+    assert hg.required_resources(p)[1] == 8 * 2 * 3
+    # fewer than 192 whole groups: one group per CU, down to half a block;
+    # at most 8 half blocks (4 tiles) per group; batches share the chip
+    assert hg.packed_columns(dict(p, n=4800)) == (3, 200)
+    assert hg.packed_columns(dict(p, n=8192)) == (4, 256)
+    assert hg.packed_columns(dict(p, n=11200)) == (6, 234)
+    assert hg.packed_columns(dict(p, n=12224)) == (6, 255)
+    assert hg.packed_columns(dict(p, n=12272)) == (8, 192)
+    assert hg.packed_columns(dict(p, n=4832)) == (3, 202)
+    assert hg.packed_columns(dict(p, n=8208)) == (5, 206)
+    assert hg.packed_columns(dict(p, n=4800, batch=2)) == (5, 120)
+    assert hg.packed_columns(dict(p, n=16)) == (1, 2)
     for bad in (dict(n=24), dict(k=40), dict(batch=70000), dict(k_split=-1)):
         assert not hg.validate_plan(dict(p, **bad))[0], bad
     # packed is never an automatic candidate for a row-major B

@@ -927,20 +927,29 @@ struct PackedArgs {
   int64_t sa, sbp, sd, sc;
   int M, N, K;
   int kbt;           // 64-row blocks of the packed layout
-  int groups;        // column groups of NBW 16-column blocks
+  int hpw;           // 8-column half blocks per column group (1 .. 2*NBW)
+  int groups;        // column groups: ceil(2 * N/16 / hpw)
   int k_split;       // workgroups along K per column group
   int kb_per_split;  // 64-row blocks per K slice
   int32_t *ws;       // [batch][k_split][M][N] partials when k_split > 1
 };
 
-// M <= 16. One workgroup = WAVES waves over NBW 16-column blocks and one K
-// slice. Wave w takes the 64-row blocks kb_beg + w, kb_beg + w + WAVES, ...;
+// M <= 16. One workgroup = WAVES waves over one column group and one K slice.
+// A column group is hpw consecutive 8-column half blocks, so it touches at
+// most NBW 16-column blocks; tiles past its last block are dead and store
+// nothing. Whole groups (hpw = 2 * NBW, MASKED false) load every tile, a dead
+// tile of the last group re-reading the last block. Smaller groups (MASKED)
+// load only live columns: dead tiles load nothing, and with hpw odd the first
+// or last block may be live in one half only, whose other half's lanes
+// neither load B (a packed tile's half is whole 128-byte lines) nor store C.
+// Small groups let a small N spread over every CU without splitting K.
+// Wave w takes the 64-row blocks kb_beg + w, kb_beg + w + WAVES, ...;
 // per block it loads its A fragment (16 bytes per lane, rows past M and k past
 // K zero) and the NBW packed B tiles, S blocks ahead of the MFMAs
 // (non-temporal loads: B is streamed once). The WAVES partial sums of each
 // column block are added through LDS and written once (plus D), or go to the
 // workspace when K is split across workgroups.
-template <int NBW, int WAVES, int S, bool HAS_D>
+template <int NBW, int WAVES, int S, bool HAS_D, bool MASKED>
 __global__ __launch_bounds__(64 * WAVES) void packed_skinny_kernel(PackedArgs p) {
   __shared__ v4i red[WAVES * NBW * 64];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -951,18 +960,28 @@ __global__ __launch_bounds__(64 * WAVES) void packed_skinny_kernel(PackedArgs p)
   const int wl = x * q + (x < r ? x : r) + (w >> 3);
   const int group = wl % p.groups, split = wl / p.groups;
   const int bidx = blockIdx.y;
-  const int nb0 = group * NBW, nbt = p.N / 16;
+  const int nbt = p.N / 16;
+  const int h0 = group * p.hpw, h1 = min(h0 + p.hpw, 2 * nbt);   // half blocks [h0, h1)
+  const int nb0 = h0 >> 1, nb_last = (h1 - 1) >> 1;
   const int kb_beg = split * p.kb_per_split;
   const int kb_end = min(kb_beg + p.kb_per_split, p.kbt);
   const int arow = lane & 15, acol = (lane >> 4) * 16;
   const bool arow_ok = arow < p.M;
   const int8_t *a_src = p.A + bidx * p.sa + (int64_t)(arow_ok ? arow : 0) * p.lda + acol;
   const int8_t *Bb = p.Bp + bidx * p.sbp;
-  // Column blocks past the last one (a partial group) re-read the last block
-  // and are never stored.
+  // Tiles 0 .. live-1 are blocks nb0 .. nb_last. Live columns of tile n within
+  // its block: [col_lo(n), col_hi(n)); with MASKED a lane loads B only for a
+  // live column (l % 16).
+  const int live = nb_last - nb0 + 1;
+  auto col_lo = [&](int n) { return (MASKED && n == 0 && (h0 & 1)) ? 8 : 0; };
+  auto col_hi = [&](int n) { return n >= live ? 0 : (MASKED && n == live - 1 && (h1 & 1)) ? 8 : 16; };
+  bool b_live[NBW];
   int64_t b_off[NBW];
 #pragma unroll
-  for (int n = 0; n < NBW; ++n) b_off[n] = (int64_t)min(nb0 + n, nbt - 1) * p.kbt * 1024 + lane * 16;
+  for (int n = 0; n < NBW; ++n) {
+    b_live[n] = (lane & 15) >= col_lo(n) && (lane & 15) < col_hi(n);
+    b_off[n] = (int64_t)min(nb0 + n, nbt - 1) * p.kbt * 1024 + lane * 16;
+  }
   v4i acc[NBW];
 #pragma unroll
   for (int n = 0; n < NBW; ++n) acc[n] = v4i{0, 0, 0, 0};
@@ -975,7 +994,9 @@ __global__ __launch_bounds__(64 * WAVES) void packed_skinny_kernel(PackedArgs p)
       const int kb = first + s * WAVES;
 #pragma unroll
       for (int n = 0; n < NBW; ++n)
-        bv[n] = __builtin_nontemporal_load((const v4i *)(Bb + b_off[n] + (int64_t)kb * 1024));
+        bv[n] = (!MASKED || b_live[n])
+                    ? __builtin_nontemporal_load((const v4i *)(Bb + b_off[n] + (int64_t)kb * 1024))
+                    : v4i{0, 0, 0, 0};
       av = (arow_ok && kb * 64 + acol < p.K) ? *(const v4i *)(a_src + kb * 64) : v4i{0, 0, 0, 0};
     } else {
 #pragma unroll
@@ -1011,9 +1032,9 @@ __global__ __launch_bounds__(64 * WAVES) void packed_skinny_kernel(PackedArgs p)
 #pragma unroll
     for (int wv = 0; wv < WAVES; ++wv)
       s = add_wrap(s, ((const int32_t *)&red[(wv * NBW + n) * 64 + src])[e]);
-    const int nb = nb0 + n;
-    if (nb >= nbt || row >= p.M) continue;
-    const int col = nb * 16 + c;
+    if (MASKED ? (c < col_lo(n) || c >= col_hi(n)) : n >= live) continue;
+    if (row >= p.M) continue;
+    const int col = (nb0 + n) * 16 + c;
     if (p.k_split == 1) {
       if (HAS_D) s = add_wrap(s, Db[(int64_t)row * p.ldd + col]);
       Cb[(int64_t)row * p.ldc + col] = s;
@@ -1434,11 +1455,25 @@ constexpr int kPackedNBW = 4, kPackedWaves = 8, kPackedS = 2;
 
 int64_t packed_kbt(int64_t K) { return (K + 63) / 64; }
 
-// Workgroups along K for the packed kernel: 1 when the column groups alone
-// give most CUs a workgroup, else enough K slices for ~224 workgroups, each
-// slice at least one row block per wave.
-int packed_k_split(int64_t N, int64_t K, int64_t batch) {
-  const int64_t groups = (N / 16 + kPackedNBW - 1) / kPackedNBW * batch;
+// Half blocks per column group. Whole groups of NBW blocks when they alone
+// give 192 or more workgroups (N = 14336: 224 groups). Below that, groups as
+// small as needed for one per CU, at half-block granularity, instead of a K
+// split and a second kernel: measured at K = 4096, N = 1024 .. 8192 run 16-22 %
+// faster that way. At N = 14336, 256 groups of 3.5 blocks ran 3 % slower than
+// 224 groups of 4, so larger N keeps whole groups.
+int packed_hpw(int64_t N, int64_t batch, int num_cus) {
+  const int64_t nbt = N / 16;
+  if ((nbt + kPackedNBW - 1) / kPackedNBW * batch >= 192) return 2 * kPackedNBW;
+  int64_t h = (2 * nbt * batch + num_cus - 1) / num_cus;
+  if (h < 1) h = 1;
+  if (h > 2 * kPackedNBW) h = 2 * kPackedNBW;
+  return (int)h;
+}
+
+// Workgroups along K for the packed kernel, given the column groups of all
+// batches: 1 when those alone give most CUs a workgroup, else enough K slices
+// for ~224 workgroups, each slice at least one row block per wave.
+int packed_k_split(int64_t groups, int64_t K) {
   if (groups >= 192) return 1;
   int64_t ks = (224 + groups - 1) / groups;
   const int64_t max_by_k = (packed_kbt(K) + kPackedWaves - 1) / kPackedWaves;
@@ -1457,8 +1492,9 @@ int launch_packed_rows(const Problem &q, int k_split, DeviceState *st, void *str
   a.sa = q.sa; a.sbp = q.sb; a.sd = q.sd; a.sc = q.sc;
   a.M = (int)q.M; a.N = (int)q.N; a.K = (int)q.K;
   a.kbt = (int)packed_kbt(q.K);
-  a.groups = (int)((q.N / 16 + kPackedNBW - 1) / kPackedNBW);
-  const int ks0 = k_split > 0 ? k_split : packed_k_split(q.N, q.K, q.batch);
+  a.hpw = packed_hpw(q.N, q.batch, st->num_cus);
+  a.groups = (int)((2 * (q.N / 16) + a.hpw - 1) / a.hpw);
+  const int ks0 = k_split > 0 ? k_split : packed_k_split((int64_t)a.groups * q.batch, q.K);
   a.kb_per_split = (a.kbt + ks0 - 1) / ks0;
   a.k_split = (a.kbt + a.kb_per_split - 1) / a.kb_per_split;
   a.ws = nullptr;
@@ -1473,10 +1509,15 @@ int launch_packed_rows(const Problem &q, int k_split, DeviceState *st, void *str
   }
   hipStream_t s = (hipStream_t)stream;
   dim3 grid((unsigned)(a.groups * a.k_split), (unsigned)q.batch), block(64 * kPackedWaves);
-  if (q.D && a.k_split == 1)
-    hipLaunchKernelGGL((packed_skinny_kernel<kPackedNBW, kPackedWaves, kPackedS, true>), grid, block, 0, s, a);
+  const bool d_in = q.D && a.k_split == 1, masked = a.hpw != 2 * kPackedNBW;
+  if (d_in && masked)
+    hipLaunchKernelGGL((packed_skinny_kernel<kPackedNBW, kPackedWaves, kPackedS, true, true>), grid, block, 0, s, a);
+  else if (d_in)
+    hipLaunchKernelGGL((packed_skinny_kernel<kPackedNBW, kPackedWaves, kPackedS, true, false>), grid, block, 0, s, a);
+  else if (masked)
+    hipLaunchKernelGGL((packed_skinny_kernel<kPackedNBW, kPackedWaves, kPackedS, false, true>), grid, block, 0, s, a);
   else
-    hipLaunchKernelGGL((packed_skinny_kernel<kPackedNBW, kPackedWaves, kPackedS, false>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((packed_skinny_kernel<kPackedNBW, kPackedWaves, kPackedS, false, false>), grid, block, 0, s, a);
   VT_HIP_CHECK(hipGetLastError());
   if (a.k_split > 1) {
     ReduceArgs r;

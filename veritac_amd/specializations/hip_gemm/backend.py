@@ -116,15 +116,32 @@ def _auto_k_split(n, k, batch):
     return max(1, min(ks, 64))
 
 
+PACKED_NBW = 4   # 16-column blocks one packed workgroup holds
+
+
+def packed_columns(plan, num_cus=NUM_CUS):
+    """(8-column half blocks per column group, column groups per batch) of the
+    packed kernel: whole groups of PACKED_NBW blocks when they give 192 or
+    more workgroups, else groups as small as one per CU needs (down to half a
+    block) instead of a K split. Mirrors packed_hpw / launch_packed_rows in
+    csrc/vt_hip_gemm.hip, which use the device's CU count (256 on an MI355X)."""
+    nbt, batch = plan["n"] // 16, plan["batch"]
+    if -(-nbt // PACKED_NBW) * batch >= 192:
+        hpw = 2 * PACKED_NBW
+    else:
+        hpw = max(1, min(-(-2 * nbt * batch // num_cus), 2 * PACKED_NBW))
+    return hpw, -(-2 * nbt // hpw)
+
+
 def packed_split(plan):
     """(k_split, 64-row blocks per slice) the packed kernel launches.
 
     Mirrors packed_k_split / launch_packed_rows in csrc/vt_hip_gemm.hip.
     """
-    n, k, batch, ks = plan["n"], plan["k"], plan["batch"], plan["k_split"]
+    k, batch, ks = plan["k"], plan["batch"], plan["k_split"]
     kbt = -(-k // 64)
     if ks <= 0:
-        groups = -(-(n // 16) // 4) * batch
+        groups = packed_columns(plan)[1] * batch
         if groups >= 192:
             ks = 1
         else:
@@ -152,7 +169,7 @@ def required_resources(plan):
         return lds + 16 * skinny_a_stride(chunk), -(-n // tn) * ks * batch
     if variant == PACKED_VARIANT:
         ks, _ = packed_split(plan)
-        return lds, -(-n // tn) * ks * batch * -(-m // tm)
+        return lds, packed_columns(plan)[1] * ks * batch * -(-m // tm)
     return 0, -(-n // tn) * min(-(-m // tm), 65535) * min(batch, 65535)
 
 
@@ -280,8 +297,8 @@ def modeled_counts(plan):
         ks, _ = packed_split(plan)
         groups = -(-m // 16)
         partial = 2 * 4 * b * m * n * ks if ks > 1 else 0
-        # B once per 16-row group; each workgroup reads its A rows once
-        l2_bytes = (groups * (b * -(-k // 64) * 64 * n) + b * m * k * -(-n // tn)
+        # B once per 16-row group; each column group reads its A rows once
+        l2_bytes = (groups * (b * -(-k // 64) * 64 * n) + b * m * k * packed_columns(plan)[1]
                     + 4 * b * m * n * (2 if plan["has_d"] else 1) + partial)
     else:
         l2_bytes = b * (m * n * k + -(-m // 4) * n * k) + 4 * b * m * n
