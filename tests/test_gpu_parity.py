@@ -321,17 +321,48 @@ MULTI_TILE_SHAPES = [(5120, 7680, 512, 1), (5888, 5888, 128, 1), (4096, 8192, 19
 
 
 @pytest.mark.parametrize("shape", MULTI_TILE_SHAPES)
-def test_staggered_tile_schedule(dev, shape):
+def test_persistent_multi_tile_walks(dev, shape):
+    """Every workgroup of the persistent kernel walks two or more tiles, with
+    and without D; with D also in place (C is D's buffer)."""
     m, n, k, batch = shape
     rng = np.random.default_rng(m + n + k + batch)
     A = rng.integers(-128, 128, (batch, m, k) if batch > 1 else (m, k), dtype=np.int8)
     B = rng.integers(-128, 128, (batch, k, n) if batch > 1 else (k, n), dtype=np.int8)
+    D = rng.integers(-(1 << 20), (1 << 20) + 1, (batch, m, n) if batch > 1 else (m, n),
+                     dtype=np.int32)
     tiles = batch * (m // 256) * (n // 256)
     assert tiles >= 512, "shape must give every workgroup at least two tiles"
     say("multi-tile", shape, "tiles", tiles)
     want = go.gemm_i8(A, B)
     for _ in range(3):
         assert np.array_equal(gpu_gemm(dev, A, B, variant="mfma_256x256"), want), shape
+    want_d = (want.astype(np.int64) + D).astype(np.int32)
+    assert np.array_equal(gpu_gemm(dev, A, B, D, variant="mfma_256x256"), want_d), shape
+    if batch == 1:
+        At, Bt = torch.from_numpy(A).to(dev), torch.from_numpy(B).to(dev)
+        Ct = torch.from_numpy(D).to(dev)
+        plan = hg.make_plan(m, n, k, has_d=True, d_max_abs=1 << 20, variant="mfma_256x256")
+        hg.run(plan, At, Bt, Ct, out=Ct)
+        assert np.array_equal(Ct.cpu().numpy(), want_d), shape
+
+
+# K of at most 128: one pair of k steps, the SHORT instantiation (both slices
+# fetched in one round trip), on edge and whole tiles, with and without D
+SHORT_K_SHAPES = [(64, 64, 64), (128, 128, 128), (200, 304, 16), (256, 256, 80),
+                  (384, 512, 128), (130, 144, 48), (512, 256, 64)]
+
+
+@pytest.mark.parametrize("variant", ["mfma_128x128", "mfma_256x128", "mfma_256x256"])
+@pytest.mark.parametrize("shape", SHORT_K_SHAPES)
+def test_short_k_path(dev, shape, variant):
+    m, n, k = shape
+    rng = np.random.default_rng(m * 7 + n * 3 + k)
+    A = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    B = rng.integers(-128, 128, (k, n), dtype=np.int8)
+    D = rng.integers(-(1 << 20), (1 << 20) + 1, (m, n), dtype=np.int32)
+    say("short k", shape, variant)
+    assert np.array_equal(gpu_gemm(dev, A, B, variant=variant), go.gemm_i8(A, B))
+    assert np.array_equal(gpu_gemm(dev, A, B, D, variant=variant), go.gemm_i8(A, B, D))
 
 
 def test_full_tile_repeated_launches_are_stable(dev):

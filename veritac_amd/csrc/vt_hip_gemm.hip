@@ -9,7 +9,7 @@
 // kernel here relies on.
 //
 // Kernels
-//   gemm_dma_kernel  full 256x256 tiles without D (the 8192^3 case).
+//   gemm_dma_kernel  full 256x256 tiles, with or without D (the 8192^3 case).
 //       Persistent: one workgroup per CU walks its tiles in XCD-contiguous
 //       order; k slices go global -> LDS by direct-to-LDS DMA
 //       (global_load_lds_dwordx4) into four stages, three slices ahead, and
@@ -25,7 +25,8 @@
 //       LDS read), so B is never transposed in memory. 16-byte chunks are
 //       XOR-swizzled so the LDS accesses are bank-conflict free. Workgroup ids
 //       are remapped so consecutive tiles share an XCD (and its L2), then
-//       grouped along M.
+//       grouped along M. A K of at most 128 runs the SHORT instantiation,
+//       which fetches its two slices in one round trip.
 //   skinny_kernel<NB>  M <= 16 (decode). Bandwidth-bound: each workgroup
 //       streams an NB-column slab of B exactly once over a K slice with
 //       non-temporal loads, U stages of 64 rows in flight in registers, LDS
@@ -128,12 +129,31 @@ __device__ __forceinline__ int a_off(int row, int c) {
 // written with non-temporal stores: every CU reaches a tile end at about the
 // same time, and streaming the whole C tile out keeps that burst from
 // displacing the A/B panels the L2 still serves.
+//
+// With D, each 32-row block first loads all of its D values and only then
+// stores: C may be D itself (in place), so a D load that followed a C store
+// in program order could not be moved above it, and loading per element
+// would make every element wait one full memory round trip (this took an
+// 8192^3 GEMM with D from ~480 to ~870 us). Each element's D is still read
+// before its own C is written, and no other lane writes that element.
 template <int MI, int NI, bool EDGE, bool HAS_D>
 __device__ __forceinline__ void store_tile(const v16i (&acc)[MI][NI], int32_t *Cb,
                                            const int32_t *Db, int64_t ldc, int64_t ldd,
                                            int row0, int col0, int M, int N, int lane) {
 #pragma unroll
   for (int mi = 0; mi < MI; ++mi) {
+    int32_t d[HAS_D ? NI : 1][16];
+    if constexpr (HAS_D) {
+#pragma unroll
+      for (int ni = 0; ni < NI; ++ni) {
+        const int col = col0 + ni * 32 + (lane & 31);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int row = row0 + mi * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+          d[ni][e] = (!EDGE || (row < M && col < N)) ? Db[(int64_t)row * ldd + col] : 0;
+        }
+      }
+    }
 #pragma unroll
     for (int ni = 0; ni < NI; ++ni) {
       const int col = col0 + ni * 32 + (lane & 31);
@@ -142,7 +162,7 @@ __device__ __forceinline__ void store_tile(const v16i (&acc)[MI][NI], int32_t *C
         const int row = row0 + mi * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
         if (!EDGE || (row < M && col < N)) {
           int32_t v = acc[mi][ni][e];
-          if (HAS_D) v = add_wrap(v, Db[(int64_t)row * ldd + col]);
+          if constexpr (HAS_D) v = add_wrap(v, d[ni][e]);
           __builtin_nontemporal_store(v, Cb + (int64_t)row * ldc + col);
         }
       }
@@ -188,7 +208,7 @@ struct GemmArgs {
   int batch_count;   // batches (the persistent kernel walks all their tiles)
 };
 
-template <int BM, int BN, bool EDGE, bool HAS_D>
+template <int BM, int BN, bool EDGE, bool HAS_D, bool SHORT>
 __global__ __launch_bounds__(256, 1) void gemm_mfma_kernel(GemmArgs p) {
   constexpr int BK = 64;
   constexpr int WTM = BM / 2, WTN = BN / 2;   // wave tile (2x2 waves)
@@ -358,13 +378,25 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma_kernel(GemmArgs p) {
     load_d_tile<MI, NI, EDGE>(d_pre, p.D + bidx * p.sd, p.ldd, m0 + wm * WTM, n0 + wn * WTN, M, N,
                               lane);
 
+  // SHORT (K <= 128, one pair of steps; the host picks it): slices 0 and 1
+  // are both in flight before the first wait and nothing more is fetched,
+  // so the k loop costs one global round trip instead of three. Longer K
+  // keeps the general schedule below (the slices it fetches past the end
+  // re-read the last one and are never computed).
   v4i ra0[CA], rb0[CB], ra1[CA], rb1[CB];
-  load_slice(0, ra0, rb0);
-  store_slice(0, ra0, rb0);
-  load_slice(1, ra1, rb1);
-  store_slice(1, ra1, rb1);
-  load_slice(2, ra0, rb0);
-  load_slice(3, ra1, rb1);
+  if constexpr (SHORT) {
+    load_slice(0, ra0, rb0);
+    load_slice(1, ra1, rb1);
+    store_slice(0, ra0, rb0);
+    store_slice(1, ra1, rb1);
+  } else {
+    load_slice(0, ra0, rb0);
+    store_slice(0, ra0, rb0);
+    load_slice(1, ra1, rb1);
+    store_slice(1, ra1, rb1);
+    load_slice(2, ra0, rb0);
+    load_slice(3, ra1, rb1);
+  }
   lds_barrier();
   read_frags(0, 0, fa0, fb0);
   int b0 = 0, b1 = 1, b2 = 2;   // buffers of slices kt, kt+1, kt+2
@@ -379,10 +411,13 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma_kernel(GemmArgs p) {
       if (2 * i < NREAD) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
     }
     __builtin_amdgcn_sched_barrier(0);
-    // Second half step: slice kt+2 to LDS, slice kt+4 from memory and the
-    // next step's first fragments, interleaved with the MFMAs of k 32..63.
-    store_slice(b2, ra, rb);
-    load_slice(kt + 4, ra, rb);
+    // Second half step: slice kt+2 to LDS, slice kt+4 from memory (neither
+    // exists with SHORT) and the next step's first fragments, interleaved
+    // with the MFMAs of k 32..63.
+    if constexpr (!SHORT) {
+      store_slice(b2, ra, rb);
+      load_slice(kt + 4, ra, rb);
+    }
     read_frags(b1, 0, fa0, fb0);
     mfma_block(fa1, fb1);
 #pragma unroll
@@ -405,9 +440,14 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma_kernel(GemmArgs p) {
   // Two steps per iteration (one per staging set). An odd step count only
   // occurs on the edge path (the host routes K % 128 != 0 there), where the
   // padding step multiplies zero A columns.
-  for (int kt = 0; kt < KT; kt += 2) {
-    step(kt, ra0, rb0);
-    step(kt + 1, ra1, rb1);
+  if constexpr (SHORT) {
+    step(0, ra0, rb0);
+    step(1, ra1, rb1);
+  } else {
+    for (int kt = 0; kt < KT; kt += 2) {
+      step(kt, ra0, rb0);
+      step(kt + 1, ra1, rb1);
+    }
   }
 
   if constexpr (D_EARLY) {
@@ -438,7 +478,7 @@ __device__ __forceinline__ void dma_b128(const int8_t *base, uint32_t voff, uint
                :: "v"(voff), "s"(base), "s"(m0));
 }
 
-// Same contract as gemm_mfma_kernel<256, 256, false, HAS_D> (full tiles only:
+// Same contract as gemm_mfma_kernel<256, 256, false, HAS_D, false> (full tiles only:
 // M % 256 == 0, N % 256 == 0, K % 64 == 0), but the k slices go global -> LDS
 // by DMA (no VGPR staging, no ds_write instructions) and the kernel is
 // persistent: one workgroup per CU walks its tiles in order and the slice
@@ -1332,6 +1372,12 @@ bool offsets_fit_32(const Problem &q, int64_t m_rows) {
 // Waves per workgroup of the persistent full-tile kernel.
 constexpr int kDmaWaves = 4;
 
+template <int BM, int BN, bool EDGE, bool HAS_D>
+void launch_mfma_kernel(bool short_k, dim3 grid, dim3 block, hipStream_t stream, const GemmArgs &a) {
+  if (short_k) hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, EDGE, HAS_D, true>), grid, block, 0, stream, a);
+  else hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, EDGE, HAS_D, false>), grid, block, 0, stream, a);
+}
+
 template <int BM, int BN>
 int launch_mfma(const Problem &q, hipStream_t stream, int num_cus) {
   // Fold contiguous shared-B batches into one stacked-M GEMM.
@@ -1355,21 +1401,23 @@ int launch_mfma(const Problem &q, hipStream_t stream, int num_cus) {
   const bool has_d = r.D != nullptr;
   dim3 grid((unsigned)blocks), block(256);
   a.batch_count = (int)r.batch;
-  if (BM == 256 && BN == 256 && !has_d && !(r.M % BM) && !(r.N % BN) && !(r.K % 64)) {
+  if (BM == 256 && BN == 256 && !(r.M % BM) && !(r.N % BN) && !(r.K % 64)) {
     // Persistent: one workgroup per CU (the kernel's LDS allows no more).
     const int64_t g = blocks < num_cus ? blocks : num_cus;
     dim3 pgrid((unsigned)g);
-    hipLaunchKernelGGL((gemm_dma_kernel<kDmaWaves, false>), pgrid, dim3(64 * kDmaWaves), 0, stream, a);
+    if (has_d) hipLaunchKernelGGL((gemm_dma_kernel<kDmaWaves, true>), pgrid, dim3(64 * kDmaWaves), 0, stream, a);
+    else hipLaunchKernelGGL((gemm_dma_kernel<kDmaWaves, false>), pgrid, dim3(64 * kDmaWaves), 0, stream, a);
     VT_HIP_CHECK(hipGetLastError());
     return VT_OK;
   }
   const bool edge = (r.M % BM) || (r.N % BN) || (r.K % 128);
+  const bool short_k = r.K <= 128;
   if (edge) {
-    if (has_d) hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, true, true>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, true, false>), grid, block, 0, stream, a);
+    if (has_d) launch_mfma_kernel<BM, BN, true, true>(short_k, grid, block, stream, a);
+    else launch_mfma_kernel<BM, BN, true, false>(short_k, grid, block, stream, a);
   } else {
-    if (has_d) hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, false, true>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, false, false>), grid, block, 0, stream, a);
+    if (has_d) launch_mfma_kernel<BM, BN, false, true>(short_k, grid, block, stream, a);
+    else launch_mfma_kernel<BM, BN, false, false>(short_k, grid, block, stream, a);
   }
   VT_HIP_CHECK(hipGetLastError());
   return VT_OK;
