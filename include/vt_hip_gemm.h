@@ -81,6 +81,12 @@ extern "C" {
  * The MFMA and skinny variants need N % 16 == 0, K % 16 == 0, lda and ldb
  * multiples of 16 and 16-byte-aligned A and B; VT_VARIANT_AUTO falls back to
  * VT_VARIANT_GENERIC otherwise, an explicit variant returns VT_EUNSUPPORTED.
+ *
+ * Sizes up to 2^40, leading dimensions up to 2^40, batch up to 2^31, batch
+ * strides up to 2^56, and every operand's byte extent below 2^56. C may not
+ * share memory with A, B or D, except D == C with ldd == ldc and (batch > 1)
+ * stride_d == stride_c, which is in place. Anything else returns VT_EINVAL
+ * before the device is touched.
  */
 int vt_gemm_i8(const int8_t *A, const int8_t *B, const int32_t *D, int32_t *C,
                int64_t M, int64_t N, int64_t K,
@@ -253,7 +259,9 @@ int vt_pack_b_i8(const int8_t *B, int8_t *Bp, int64_t K, int64_t N, int64_t ldb,
  * :712-720 execution), with B given packed: Bp [batch][packed size],
  * stride_bp 0 = one packed B shared by every batch. Needs N % 16 == 0,
  * K % 16 == 0, lda and strides multiples of 16, 16-byte aligned A and Bp.
- * Any M: rows run in groups of 16, each group streaming B once (the kernel
+ * Same extent bounds and overlap refusals as vt_gemm_i8 (Bp counts as
+ * batch blocks of vt_packed_b_size bytes; vt_pack_b_i8 likewise refuses a Bp
+ * that overlaps B). Any M: rows run in groups of 16, each group streaming B once (the kernel
  * is built for M <= 16). Columns go to workgroups in groups of 8-column
  * half blocks: whole groups of four 16-column blocks when N gives 192 or
  * more of them, else smaller groups, about one per CU. k_split: workgroups

@@ -175,3 +175,54 @@ def test_device_query_fails_closed_without_gpu():
     with pytest.raises(_lib.HipGemmError) as exc:
         _lib.device_query()
     assert exc.value.code == _lib.VT_ENODEV
+
+
+# ---------------------------------------------------------------------------
+# Extents and overlapping operands (refused on the host, before any device call)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("kw", [
+    dict(lda=1 << 41), dict(ldc=1 << 41), dict(batch=2, strides=(0, 0, 0, 1 << 57)),
+    dict(M=1 << 41), dict(batch=1 << 32, strides=(0, 0, 0, 64)),
+    # M * ldc would overflow 64 bits in the stride check
+    dict(M=1 << 30, ldc=1 << 40, batch=2, strides=(0, 0, 0, 1 << 50)),
+])
+def test_extents_beyond_the_address_space_are_refused(kw):
+    assert call(**kw) == _lib.VT_EINVAL
+    assert _lib.last_error()
+
+
+def test_output_may_not_overlap_an_input():
+    # A at 1<<20 spans 4*16 bytes; C at 1<<20 + 32 overlaps it
+    assert call(C=(1 << 20) + 32) == _lib.VT_EINVAL
+    assert "overlaps A or B" in _lib.last_error()
+    assert call(C=(1 << 21) + 64) == _lib.VT_EINVAL          # inside B (16 x 16 bytes)
+    # D partially overlapping C
+    assert call(D=(1 << 22) + 64) == _lib.VT_EINVAL
+    assert "D overlaps C" in _lib.last_error()
+    # D == C but another leading dimension: not in place, refused
+    assert call(D=1 << 22, ldd=32, ldc=16) == _lib.VT_EINVAL
+    # batched: D == C with a different batch stride
+    assert call(D=1 << 22, batch=2, strides=(64, 0, 128, 64 * 4)) == _lib.VT_EINVAL
+
+
+@pytest.mark.skipif(veritac_amd.load_library().vt_device_count() > 0, reason="GPU present")
+def test_in_place_and_adjacent_operands_pass_validation():
+    # exact in place (same base, ld and stride) and operands that merely touch
+    # pass the host checks and reach the device query (no device here)
+    assert call(D=1 << 22) == _lib.VT_ENODEV
+    assert call(D=1 << 22, batch=2, strides=(64, 0, 256, 256)) == _lib.VT_ENODEV
+    assert call(C=(1 << 20) + 64) == _lib.VT_ENODEV            # right after A (4 x 16 bytes)
+
+
+def test_packed_entry_points_refuse_overlap():
+    lib = veritac_amd.load_library()
+    size = _lib.packed_b_size(64, 16)
+    # pack: Bp inside B
+    rc = lib.vt_pack_b_i8(1 << 20, (1 << 20) + 512, 64, 16, 16, 1, 0, 0, None)
+    assert rc == _lib.VT_EINVAL and "overlaps" in _lib.last_error()
+    # packed GEMM: C over the packed B
+    rc = lib.vt_gemm_i8_packed(1 << 20, 1 << 21, None, (1 << 21) + 16, 4, 16, 64, 64, 16, 16,
+                               1, 0, 0, 0, 0, 0, None)
+    assert rc == _lib.VT_EINVAL and "overlaps" in _lib.last_error()
+    assert size == 1024

@@ -1303,6 +1303,53 @@ int get_workspace(DeviceState *st, void *stream, size_t partial_bytes, Workspace
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
+// Byte range [lo, hi) a [batch][rows][ld] operand of `elem`-byte elements
+// touches when `cols` columns of each row are used (batch stride `stride`,
+// 0 = one matrix shared by every batch). Sizes are bounded by the caller;
+// the products are formed in 128 bits and must stay below 2^56 bytes.
+struct Extent {
+  uintptr_t lo = 0, hi = 0;
+};
+bool operand_extent(const void *p, int64_t batch, int64_t stride, int64_t rows, int64_t ld,
+                    int64_t cols, int64_t elem, Extent *out) {
+  const __int128 last = (__int128)(batch - 1) * stride + (__int128)(rows - 1) * ld + cols;
+  const __int128 bytes = last * elem;
+  if (bytes < 0 || bytes >= ((__int128)1 << 56)) return false;
+  out->lo = (uintptr_t)p;
+  out->hi = (uintptr_t)p + (uintptr_t)bytes;
+  return out->hi >= out->lo;
+}
+
+bool overlaps(const Extent &a, const Extent &b) { return a.lo < b.hi && b.lo < a.hi; }
+
+// The output may not share memory with an input, except that D may be C
+// itself (same base, leading dimension and batch stride: in-place C = C + A.B).
+// Every lane reads its inputs and writes its own outputs with no ordering
+// against other lanes, so any other overlap would race.
+int check_operand_overlap(const void *A, const void *B, const int32_t *D, const int32_t *C,
+                          int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb_rows,
+                          int64_t ldb, int64_t b_cols, int64_t ldd, int64_t ldc, int64_t batch,
+                          int64_t sa, int64_t sb, int64_t sd, int64_t sc, const char *who) {
+  Extent ec, ea, eb, ed;
+  if (!operand_extent(C, batch, sc, M, ldc, N, 4, &ec))
+    return fail(VT_EINVAL, "%s: C extent beyond 2^56 bytes", who);
+  if (K > 0) {
+    if (!operand_extent(A, batch, sa, M, lda, K, 1, &ea) ||
+        !operand_extent(B, batch, sb, ldb_rows, ldb, b_cols, 1, &eb))
+      return fail(VT_EINVAL, "%s: A or B extent beyond 2^56 bytes", who);
+    if (overlaps(ec, ea) || overlaps(ec, eb))
+      return fail(VT_EINVAL, "%s: C overlaps A or B in memory", who);
+  }
+  if (D) {
+    if (!operand_extent(D, batch, sd, M, ldd, N, 4, &ed))
+      return fail(VT_EINVAL, "%s: D extent beyond 2^56 bytes", who);
+    const bool in_place = (const void *)D == (const void *)C && ldd == ldc && (batch == 1 || sd == sc);
+    if (!in_place && overlaps(ec, ed))
+      return fail(VT_EINVAL, "%s: D overlaps C without being C itself (same ld and stride)", who);
+  }
+  return VT_OK;
+}
+
 struct Problem {
   const int8_t *A;
   const int8_t *B;
@@ -1364,8 +1411,8 @@ int launch_generic(const Problem &q, hipStream_t stream);
 // The MFMA kernels address A and B with 32-bit lane offsets from a per-slice
 // base: every row offset inside one batch must stay below 2^32.
 bool offsets_fit_32(const Problem &q, int64_t m_rows) {
-  const int64_t a_span = m_rows * q.lda;
-  const int64_t b_span = q.K * q.ldb;
+  const __int128 a_span = (__int128)m_rows * q.lda;
+  const __int128 b_span = (__int128)q.K * q.ldb;
   return a_span < (1ll << 32) - 4096 && b_span < (1ll << 32) - 4096;
 }
 
@@ -1766,6 +1813,12 @@ int vt_gemm_i8(const int8_t *A, const int8_t *B, const int32_t *D, int32_t *C, i
   if (k_split < 0 || k_split > 4096) return fail(VT_EINVAL, "k_split %d out of range", (int)k_split);
   if (stride_a < 0 || stride_b < 0 || stride_d < 0 || stride_c < 0)
     return fail(VT_EINVAL, "negative batch stride");
+  if (M > (1ll << 40) || N > (1ll << 40) || K > (1ll << 40) || batch > (1ll << 31))
+    return fail(VT_EINVAL, "size beyond 2^40 (batch beyond 2^31)");
+  if (lda > (1ll << 40) || ldb > (1ll << 40) || ldd > (1ll << 40) || ldc > (1ll << 40) ||
+      stride_a > (1ll << 56) || stride_b > (1ll << 56) || stride_d > (1ll << 56) ||
+      stride_c > (1ll << 56))
+    return fail(VT_EINVAL, "leading dimension beyond 2^40 or batch stride beyond 2^56");
   if (M == 0 || N == 0 || batch == 0) return VT_OK;
   if (!C) return fail(VT_EINVAL, "C is null");
   if (K > 0 && (!A || !B)) return fail(VT_EINVAL, "A or B is null");
@@ -1773,12 +1826,13 @@ int vt_gemm_i8(const int8_t *A, const int8_t *B, const int32_t *D, int32_t *C, i
   if (K > 0 && lda < K) return fail(VT_EINVAL, "lda=%lld < K=%lld", (long long)lda, (long long)K);
   if (K > 0 && ldb < N) return fail(VT_EINVAL, "ldb=%lld < N=%lld", (long long)ldb, (long long)N);
   if (D && ldd < N) return fail(VT_EINVAL, "ldd=%lld < N=%lld", (long long)ldd, (long long)N);
-  if (batch > 1 && (stride_c < M * ldc && stride_c != 0))
-    return fail(VT_EINVAL, "stride_c=%lld overlaps batches (M*ldc=%lld)", (long long)stride_c,
-                (long long)(M * ldc));
+  if (batch > 1 && stride_c != 0 && (__int128)stride_c < (__int128)M * ldc)
+    return fail(VT_EINVAL, "stride_c=%lld overlaps batches (M=%lld rows of ldc=%lld)",
+                (long long)stride_c, (long long)M, (long long)ldc);
   if (batch > 1 && stride_c == 0) return fail(VT_EINVAL, "stride_c must be nonzero for batch > 1");
-  if (M > (1ll << 40) || N > (1ll << 40) || K > (1ll << 40))
-    return fail(VT_EINVAL, "size beyond 2^40");
+  if (int rc = check_operand_overlap(A, B, D, C, M, N, K, lda, K, ldb, N, ldd, ldc, batch,
+                                     stride_a, stride_b, stride_d, stride_c, "vt_gemm_i8"))
+    return rc;
 
   Problem q = {A, B, D, C, M, N, K, lda, ldb, ldd, ldc, batch,
                stride_a, stride_b, stride_d, stride_c};
@@ -1839,7 +1893,17 @@ int vt_pack_b_i8(const int8_t *B, int8_t *Bp, int64_t K, int64_t N, int64_t ldb,
   if (batch > 65535 || (N + 255) / 256 > 65535)
     return fail(VT_EUNSUPPORTED, "pack grid too large (batch=%lld N=%lld)", (long long)batch,
                 (long long)N);
-  if ((K - 1) * ldb + N >= (1ll << 40)) return fail(VT_EINVAL, "B extent beyond 2^40");
+  if (ldb > (1ll << 40) || stride_b > (1ll << 56) || stride_bp > (1ll << 56))
+    return fail(VT_EINVAL, "ldb beyond 2^40 or batch stride beyond 2^56");
+  if ((__int128)(K - 1) * ldb + N >= ((__int128)1 << 40))
+    return fail(VT_EINVAL, "B extent beyond 2^40");
+  {
+    Extent eb, ep;
+    if (!operand_extent(B, batch, stride_b, K, ldb, N, 1, &eb) ||
+        !operand_extent(Bp, batch, stride_bp, 1, 0, size, 1, &ep))
+      return fail(VT_EINVAL, "vt_pack_b_i8: extent beyond 2^56 bytes");
+    if (overlaps(eb, ep)) return fail(VT_EINVAL, "vt_pack_b_i8: Bp overlaps B in memory");
+  }
   int dev = 0;
   DeviceState *st = nullptr;
   int rc = current_device(&dev, &st);
@@ -1864,17 +1928,26 @@ int vt_gemm_i8_packed(const int8_t *A, const int8_t *Bp, const int32_t *D, int32
   if (k_split < 0 || k_split > 4096) return fail(VT_EINVAL, "k_split %d out of range", (int)k_split);
   if (stride_a < 0 || stride_bp < 0 || stride_d < 0 || stride_c < 0)
     return fail(VT_EINVAL, "negative batch stride");
+  if (lda > (1ll << 40) || ldd > (1ll << 40) || ldc > (1ll << 40) || batch > (1ll << 31) ||
+      stride_a > (1ll << 56) || stride_bp > (1ll << 56) || stride_d > (1ll << 56) ||
+      stride_c > (1ll << 56))
+    return fail(VT_EINVAL, "leading dimension beyond 2^40, batch beyond 2^31 or stride beyond 2^56");
   if (M == 0 || N == 0 || batch == 0) return VT_OK;
   if (!C) return fail(VT_EINVAL, "C is null");
   if (K > 0 && (!A || !Bp)) return fail(VT_EINVAL, "A or Bp is null");
   if (ldc < N) return fail(VT_EINVAL, "ldc=%lld < N=%lld", (long long)ldc, (long long)N);
   if (K > 0 && lda < K) return fail(VT_EINVAL, "lda=%lld < K=%lld", (long long)lda, (long long)K);
   if (D && ldd < N) return fail(VT_EINVAL, "ldd=%lld < N=%lld", (long long)ldd, (long long)N);
-  if (batch > 1 && stride_c < M * ldc)
-    return fail(VT_EINVAL, "stride_c=%lld overlaps batches (M*ldc=%lld)", (long long)stride_c,
-                (long long)(M * ldc));
+  if (batch > 1 && (__int128)stride_c < (__int128)M * ldc)
+    return fail(VT_EINVAL, "stride_c=%lld overlaps batches (M=%lld rows of ldc=%lld)",
+                (long long)stride_c, (long long)M, (long long)ldc);
   if (M >= (1ll << 30) || N >= (1ll << 30) || K >= (1ll << 30))
     return fail(VT_EINVAL, "size beyond 2^30");
+  // packed B: one contiguous block of packed_b_size bytes per batch
+  if (int rc = check_operand_overlap(A, Bp, D, C, M, N, K, lda, 1, 0,
+                                     N * ((K + 63) / 64) * 64, ldd, ldc, batch, stride_a,
+                                     stride_bp, stride_d, stride_c, "vt_gemm_i8_packed"))
+    return rc;
   if (N % 16 || K % 16)
     return fail(VT_EUNSUPPORTED, "packed B needs N %% 16 == 0 and K %% 16 == 0 (N=%lld K=%lld)",
                 (long long)N, (long long)K);
