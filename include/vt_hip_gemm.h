@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define VT_ABI_VERSION 5
+#define VT_ABI_VERSION 6
 
 /* Status codes. */
 #define VT_OK 0
@@ -57,7 +57,11 @@ extern "C" {
                                       v_mfma_i32_16x16x64_i8, K split         */
 #define VT_VARIANT_GENERIC 4       /* any shape/stride/alignment, VALU        */
 #define VT_VARIANT_MFMA_256x128 5  /* 256x128 tile, 4 waves                   */
-#define VT_VARIANT_COUNT 6
+#define VT_VARIANT_PADDED 6        /* any shape: A and B copied with K and N
+                                      zero-padded to multiples of 16, run on
+                                      the MFMA / skinny kernels, C copied out
+                                      (plus D)                                */
+#define VT_VARIANT_COUNT 7
 
 /*
  * vt_gemm_i8 -- batched exact int8 GEMM.
@@ -79,8 +83,12 @@ extern "C" {
  *            (0 = choose automatically; ignored by other variants)
  *
  * The MFMA and skinny variants need N % 16 == 0, K % 16 == 0, lda and ldb
- * multiples of 16 and 16-byte-aligned A and B; VT_VARIANT_AUTO falls back to
- * VT_VARIANT_GENERIC otherwise, an explicit variant returns VT_EUNSUPPORTED.
+ * multiples of 16 and 16-byte-aligned A and B; an explicit one returns
+ * VT_EUNSUPPORTED otherwise. For such shapes VT_VARIANT_AUTO picks
+ * VT_VARIANT_PADDED from 2^26 multiply-adds on (M, N + 15, K + 15 < 2^30,
+ * batch <= 65535) and VT_VARIANT_GENERIC below. VT_VARIANT_PADDED keeps its
+ * zero-padded copies in a workspace the library allocates once per
+ * (device, stream) and grows as needed.
  *
  * Sizes up to 2^40, leading dimensions up to 2^40, batch up to 2^31, batch
  * strides up to 2^56, and every operand's byte extent below 2^56. C may not

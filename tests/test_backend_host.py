@@ -183,3 +183,20 @@ def test_config_inputs_properties():
     again = inputs.config_inputs(2, seed=1)
     assert np.array_equal(again["A"], c2["A"]) and np.array_equal(again["D"], c2["D"])
     assert inputs.config_shape(5) == (1, 8192, 8192, 8192, False, False)
+
+
+def test_padded_plans_take_any_n_and_k():
+    p = hg.make_plan(1000, 1000, 1000)
+    assert p["variant"] == "padded" and hg.validate_plan(p) == (True, "ok")
+    inner = hg.padded_inner_plan(p)
+    assert (inner["n"], inner["k"]) == (1008, 1008) and inner["variant"].startswith("mfma")
+    assert not inner["has_d"]
+    p = hg.make_plan(16, 14335, 4095, variant="padded")
+    assert hg.validate_plan(p)[0] and hg.padded_inner_plan(p)["variant"] == "skinny"
+    assert hg.validate_plan(dict(p, k_split=2)) == (False, "variant 'padded' chooses its own k_split (give 0)")
+    assert not hg.validate_plan(dict(p, batch=70000))[0]
+    # small unaligned shapes stay on the VALU kernel; aligned shapes never pick padded
+    assert hg.make_plan(64, 60, 64)["variant"] == "generic"
+    assert hg.optimize(1024, 1024, 1024)["winner"]["variant"].startswith("mfma")
+    counts = hg.modeled_counts(hg.make_plan(1000, 1000, 1000, has_d=True, d_max_abs=7))
+    assert counts["bytes_l2_modeled"] > counts["bytes_algorithmic"]

@@ -226,3 +226,15 @@ def test_packed_entry_points_refuse_overlap():
                                1, 0, 0, 0, 0, 0, None)
     assert rc == _lib.VT_EINVAL and "overlaps" in _lib.last_error()
     assert size == 1024
+
+
+def test_padded_variant_selection_and_refusals():
+    # unaligned shapes: the padded path from 2^26 multiply-adds, the VALU kernel below
+    assert _lib.select_variant(1000, 1000, 1000, aligned=False) == ("padded", 0)
+    assert _lib.select_variant(64, 1024, 1024, aligned=False)[0] == "padded"      # exactly 2^26
+    assert _lib.select_variant(63, 1024, 1024, aligned=False)[0] == "generic"
+    assert _lib.select_variant(17, 14335, 4095, aligned=False)[0] == "padded"
+    assert _lib.select_variant(1 << 30, 16, 16, aligned=False)[0] == "generic"     # M too large
+    # an explicit padded call is validated like any other before the device
+    assert call(variant=6, M=-1) == _lib.VT_EINVAL
+    assert call(variant=6, C=(1 << 20) + 8) == _lib.VT_EINVAL                    # C over A

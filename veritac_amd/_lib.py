@@ -14,7 +14,7 @@ import threading
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 DEFAULT_LIB = os.path.join(PKG_DIR, "libvt_hip_gemm.so")
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 VT_OK = 0
 VT_EINVAL = -1
@@ -32,6 +32,7 @@ VARIANT_IDS = {
     "skinny": 3,
     "generic": 4,
     "mfma_256x128": 5,
+    "padded": 6,
 }
 VARIANTS = tuple(VARIANT_IDS)
 

@@ -1231,6 +1231,7 @@ const VariantInfo kVariants[VT_VARIANT_COUNT] = {
     {"skinny", 16, 256, 64, 1024, 2 * 16 * 1024},
     {"generic", 4, 64, 1, 256, 0},
     {"mfma_256x128", 256, 128, 64, 256, 2 * (256 * 64 + 64 * 128)},
+    {"padded", 16, 16, 16, 256, 0},   // padding granularity; the inner kernel decides the rest
 };
 
 // Default skinny configuration: 256-column slabs (full 128-byte lines of B
@@ -1250,7 +1251,8 @@ struct DeviceState {
   bool ok = false;
   int num_cus = 256;
   std::string arch;
-  std::map<void *, Workspace> ws;   // per stream
+  std::map<void *, Workspace> ws;       // per stream: K-split partial sums
+  std::map<void *, Workspace> pad_ws;   // per stream: zero-padded operand copies
 };
 
 std::mutex g_mu;
@@ -1284,9 +1286,10 @@ int current_device(int *dev_out, DeviceState **st_out) {
 // Workspace for the skinny kernel's K-split partials on (device, stream).
 // Calls on one stream are ordered, so a stream's workspace is never shared by
 // two launches in flight.
-int get_workspace(DeviceState *st, void *stream, size_t partial_bytes, Workspace **out) {
+int get_workspace(DeviceState *st, void *stream, size_t partial_bytes, Workspace **out,
+                  bool pad = false) {
   std::lock_guard<std::mutex> lk(g_mu);
-  Workspace &w = st->ws[stream];
+  Workspace &w = pad ? st->pad_ws[stream] : st->ws[stream];
   if (w.partial_bytes < partial_bytes) {
     if (w.partials) {
       VT_HIP_CHECK(hipStreamSynchronize((hipStream_t)stream));
@@ -1379,10 +1382,19 @@ int choose_k_split(int64_t N, int64_t K, int64_t batch) {
   return (int)ks;
 }
 
+// Shapes the padded path takes: enough work to repay two copy kernels and
+// one copy-out (below 2^26 multiply-adds the VALU kernel is as fast), and
+// padded sizes the vector kernels accept.
+bool padded_fits(const Problem &q) {
+  return q.K > 0 && q.M < (1ll << 30) && q.N + 15 < (1ll << 30) && q.K + 15 < (1ll << 30) &&
+         q.batch <= 65535;
+}
+
 int select_variant(const Problem &q, bool vec, int32_t *variant, int32_t *k_split) {
   *k_split = 0;
   if (!vec || q.K == 0) {
-    *variant = VT_VARIANT_GENERIC;
+    const double macs = (double)q.M * (double)q.N * (double)q.K * (double)q.batch;
+    *variant = (padded_fits(q) && macs >= 67108864.0) ? VT_VARIANT_PADDED : VT_VARIANT_GENERIC;
     return VT_OK;
   }
   if (q.M <= 16) {
@@ -1628,6 +1640,113 @@ int launch_packed_rows(const Problem &q, int k_split, DeviceState *st, void *str
   return VT_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Padded path: any shape through the vector kernels
+// ---------------------------------------------------------------------------
+
+// Zero-padded int8 copy: dst[b][r][c] (r < rows_p, c < cols_p, cols_p % 16 == 0)
+// is src[b*ss + r*ld + c] where r < rows and c < cols, else 0. One thread
+// writes 16 bytes; the source is read bytewise (any alignment and stride).
+struct PadArgs {
+  const int8_t *src;
+  int8_t *dst;
+  int64_t ld, ss, sd;
+  int64_t rows, cols, rows_p, cols_p;
+};
+
+__global__ __launch_bounds__(256) void pad_i8_kernel(PadArgs p) {
+  const int64_t chunks = p.cols_p / 16;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= p.rows_p * chunks) return;
+  const int64_t r = i / chunks, c0 = (i - r * chunks) * 16;
+  const int64_t b = blockIdx.y;
+  v4i out = v4i{0, 0, 0, 0};
+  if (r < p.rows) {
+    const int8_t *s = p.src + b * p.ss + r * p.ld;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      uint32_t word = 0;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int64_t c = c0 + 4 * w + t;
+        if (c < p.cols) word |= (uint32_t)(uint8_t)s[c] << (8 * t);
+      }
+      out[w] = (int)word;
+    }
+  }
+  *(v4i *)(p.dst + b * p.sd + r * p.cols_p + c0) = out;
+}
+
+// C[b][r][c] = src[b][r][c] (+ D[b][r][c]) for c < N: the padded product's
+// valid columns, wrapping mod 2^32. Elementwise, so D may be C itself.
+struct UnpadArgs {
+  const int32_t *src;
+  const int32_t *D;
+  int32_t *C;
+  int64_t lds, ldd, ldc, ss, sd, sc;
+  int64_t M, N;
+};
+
+template <bool HAS_D>
+__global__ __launch_bounds__(256) void unpad_kernel(UnpadArgs p) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= p.M * p.N) return;
+  const int64_t r = i / p.N, c = i - r * p.N, b = blockIdx.y;
+  int32_t v = __builtin_nontemporal_load(p.src + b * p.ss + r * p.lds + c);
+  if (HAS_D) v = add_wrap(v, p.D[b * p.sd + r * p.ldd + c]);
+  p.C[b * p.sc + r * p.ldc + c] = v;
+}
+
+int launch_vector(const Problem &q, int32_t variant, int32_t k_split, DeviceState *st,
+                  void *stream);
+
+// A and B copied with K and N rounded up to 16 (zero columns of A meet zero
+// rows of B, so the product is unchanged), multiplied by the kernel the
+// vector path selects for the padded shape, valid columns copied out with D.
+int launch_padded(const Problem &q, DeviceState *st, void *stream) {
+  if (!padded_fits(q))
+    return fail(VT_EUNSUPPORTED, "padded path needs K > 0, M, N+15, K+15 < 2^30, batch <= 65535");
+  const int64_t Kp = (q.K + 15) / 16 * 16, Np = (q.N + 15) / 16 * 16;
+  const int64_t bA = (q.batch > 1 && q.sa == 0) ? 1 : q.batch;
+  const int64_t bB = (q.batch > 1 && q.sb == 0) ? 1 : q.batch;
+  auto round256 = [](int64_t v) { return (v + 255) / 256 * 256; };
+  const int64_t a_bytes = round256(bA * q.M * Kp), b_bytes = round256(bB * Kp * Np);
+  const int64_t c_bytes = round256(q.batch * q.M * Np * 4);
+  Workspace *w = nullptr;
+  int rc = get_workspace(st, stream, (size_t)(a_bytes + b_bytes + c_bytes), &w, true);
+  if (rc) return rc;
+  int8_t *Ap = (int8_t *)w->partials, *Bp = Ap + a_bytes;
+  int32_t *Cp = (int32_t *)(Bp + b_bytes);
+  hipStream_t s = (hipStream_t)stream;
+  const PadArgs pa = {q.A, Ap, q.lda, bA > 1 ? q.sa : 0, q.M * Kp, q.M, q.K, q.M, Kp};
+  const PadArgs pb = {q.B, Bp, q.ldb, bB > 1 ? q.sb : 0, Kp * Np, q.K, q.N, Kp, Np};
+  const struct {
+    const PadArgs &args;
+    int64_t batches;
+  } copies[2] = {{pa, bA}, {pb, bB}};
+  for (const auto &cp : copies) {
+    const int64_t threads = cp.args.rows_p * (cp.args.cols_p / 16);
+    if ((threads + 255) / 256 > 0x7fffffff) return fail(VT_EUNSUPPORTED, "padded copy grid too large");
+    hipLaunchKernelGGL(pad_i8_kernel, dim3((unsigned)((threads + 255) / 256), (unsigned)cp.batches),
+                       dim3(256), 0, s, cp.args);
+    VT_HIP_CHECK(hipGetLastError());
+  }
+  const Problem g = {Ap, Bp, nullptr, Cp, q.M, Np, Kp, Kp, Np, Np, Np, q.batch,
+                     bA > 1 ? q.M * Kp : 0, bB > 1 ? Kp * Np : 0, 0, q.M * Np};
+  int32_t v = 0, ks = 0;
+  select_variant(g, true, &v, &ks);
+  rc = launch_vector(g, v, ks, st, stream);
+  if (rc) return rc;
+  UnpadArgs u = {Cp, q.D, q.C, Np, q.ldd, q.ldc, q.M * Np, q.sd, q.sc, q.M, q.N};
+  const int64_t cells = q.M * q.N;
+  if ((cells + 255) / 256 > 0x7fffffff) return fail(VT_EUNSUPPORTED, "padded copy-out grid too large");
+  dim3 ug((unsigned)((cells + 255) / 256), (unsigned)q.batch);
+  if (q.D) hipLaunchKernelGGL(unpad_kernel<true>, ug, dim3(256), 0, s, u);
+  else hipLaunchKernelGGL(unpad_kernel<false>, ug, dim3(256), 0, s, u);
+  VT_HIP_CHECK(hipGetLastError());
+  return VT_OK;
+}
+
 int launch_generic(const Problem &q, hipStream_t stream) {
   GenericArgs a;
   a.A = q.A; a.B = q.B; a.D = q.D; a.C = q.C;
@@ -1643,6 +1762,20 @@ int launch_generic(const Problem &q, hipStream_t stream) {
                      stream, a);
   VT_HIP_CHECK(hipGetLastError());
   return VT_OK;
+}
+
+
+// The vector variants (operands already checked by vector_ok).
+int launch_vector(const Problem &q, int32_t variant, int32_t k_split, DeviceState *st,
+                  void *stream) {
+  hipStream_t s = (hipStream_t)stream;
+  switch (variant) {
+    case VT_VARIANT_MFMA_256x256: return launch_mfma<256, 256>(q, s, st->num_cus);
+    case VT_VARIANT_MFMA_128x128: return launch_mfma<128, 128>(q, s, st->num_cus);
+    case VT_VARIANT_MFMA_256x128: return launch_mfma<256, 128>(q, s, st->num_cus);
+    case VT_VARIANT_SKINNY: return launch_skinny(q, k_split, st, stream);
+    default: return fail(VT_EINVAL, "variant %d is not a vector variant", (int)variant);
+  }
 }
 
 }  // namespace
@@ -1841,7 +1974,7 @@ int vt_gemm_i8(const int8_t *A, const int8_t *B, const int32_t *D, int32_t *C, i
   if (variant == VT_VARIANT_AUTO) {
     select_variant(q, vec, &chosen, &ks);
     if (k_split > 0) ks = k_split;
-  } else if (variant != VT_VARIANT_GENERIC) {
+  } else if (variant != VT_VARIANT_GENERIC && variant != VT_VARIANT_PADDED) {
     if (!vec)
       return fail(VT_EUNSUPPORTED,
                   "variant %s needs N%%16==0, K%%16==0 (K>0), lda/ldb/strides multiples of 16 "
@@ -1850,22 +1983,17 @@ int vt_gemm_i8(const int8_t *A, const int8_t *B, const int32_t *D, int32_t *C, i
     if (variant == VT_VARIANT_SKINNY && M > 16)
       return fail(VT_EUNSUPPORTED, "variant skinny needs M <= 16 (M=%lld)", (long long)M);
   }
-  if (chosen != VT_VARIANT_GENERIC && !vec)
+  if (chosen != VT_VARIANT_GENERIC && chosen != VT_VARIANT_PADDED && !vec)
     return fail(VT_EUNSUPPORTED, "internal: vector variant selected for an unaligned problem");
+  if (chosen == VT_VARIANT_PADDED && K == 0) chosen = VT_VARIANT_GENERIC;   // C = D (or 0)
 
   int dev = 0;
   DeviceState *st = nullptr;
   int rc = current_device(&dev, &st);
   if (rc) return rc;
-  hipStream_t s = (hipStream_t)stream;
-  switch (chosen) {
-    case VT_VARIANT_MFMA_256x256: return launch_mfma<256, 256>(q, s, st->num_cus);
-    case VT_VARIANT_MFMA_128x128: return launch_mfma<128, 128>(q, s, st->num_cus);
-    case VT_VARIANT_MFMA_256x128: return launch_mfma<256, 128>(q, s, st->num_cus);
-    case VT_VARIANT_SKINNY: return launch_skinny(q, ks, st, stream);
-    case VT_VARIANT_GENERIC: return launch_generic(q, s);
-    default: return fail(VT_EINVAL, "unknown variant %d", (int)chosen);
-  }
+  if (chosen == VT_VARIANT_GENERIC) return launch_generic(q, (hipStream_t)stream);
+  if (chosen == VT_VARIANT_PADDED) return launch_padded(q, st, stream);
+  return launch_vector(q, chosen, ks, st, stream);
 }
 
 int64_t vt_packed_b_size(int64_t K, int64_t N) {

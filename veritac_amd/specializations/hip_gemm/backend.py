@@ -41,7 +41,9 @@ ACC_ELEMENT_MAX = 2**31 - 1
 INT8_DOMAIN_CONSTRAINT = "inputs are int8 in [-128,127] and k*16384 + |D| <= 2147483647"
 MAX_EXTENT = 2**40
 
-VARIANTS = ("mfma_256x256", "mfma_256x128", "mfma_128x128", "skinny", "generic")
+VARIANTS = ("mfma_256x256", "mfma_256x128", "mfma_128x128", "skinny", "generic", "padded")
+# variants that take any n and k (no multiple-of-16 rule)
+ANY_SHAPE_VARIANTS = ("generic", "padded")
 # The packed-B decode variant takes B prepacked by pack_b (vt_pack_b_i8), not
 # row-major, so it is never an automatic candidate for a row-major B.
 PACKED_VARIANT = "skinny_packed"
@@ -56,6 +58,9 @@ TILES = {
     "mfma_128x128": (128, 128, 64, 256, 2 * (128 * 64 + 64 * 128)),
     "skinny": (16, 256, 64, 1024, 2 * 16 * 1024),
     "generic": (4, 64, 1, 256, 0),
+    # padding granularity: A and B copied with k and n rounded up to 16, the
+    # product run on the vector kernel the native selection picks for that shape
+    "padded": (16, 16, 16, 256, 0),
     # 16 rows (groups of 16 for larger m), 4 column blocks, 64-row blocks,
     # 8 waves, LDS for the cross-wave sums (kPacked* in the HIP source)
     "skinny_packed": (16, 64, 64, 512, 8 * 4 * 1024),
@@ -170,7 +175,18 @@ def required_resources(plan):
     if variant == PACKED_VARIANT:
         ks, _ = packed_split(plan)
         return lds, packed_columns(plan)[1] * ks * batch * -(-m // tm)
+    if variant == "padded":
+        return required_resources(padded_inner_plan(plan))
     return 0, -(-n // tn) * min(-(-m // tm), 65535) * min(batch, 65535)
+
+
+def padded_inner_plan(plan):
+    """The plan the padded variant runs after copying A and B with k and n
+    rounded up to 16: the vector variant the native selection picks for that
+    shape (vt_gemm_select), without D (added while copying C out)."""
+    n_p, k_p = -(-plan["n"] // DIM) * DIM, -(-plan["k"] // DIM) * DIM
+    name, ks = _lib.select_variant(plan["m"], n_p, k_p, plan["batch"], k_p, n_p, True)
+    return dict(plan, n=n_p, k=k_p, variant=name, k_split=ks, has_d=False, d_max_abs=0)
 
 
 def make_plan(m, n, k, *, batch=1, b_shared=False, has_d=False, d_max_abs=0,
@@ -231,7 +247,7 @@ def validate_plan(plan):
                        % (bound, INT8_DOMAIN_CONSTRAINT))
     if max(m, n, k) >= MAX_EXTENT or batch * max(m * n, m * k) >= 2**62:
         return False, "buffer extent exceeds the supported indexing range"
-    if variant != "generic":
+    if variant not in ANY_SHAPE_VARIANTS:
         for name, val in (("n", n), ("k", k)):
             if val % dim != 0:
                 return False, ("%s=%d must be divisible by dim=%d for variant %r"
@@ -246,6 +262,11 @@ def validate_plan(plan):
             return False, "variant %r supports batch <= 65535" % PACKED_VARIANT
         if max(m, n, k) >= 2**30:
             return False, "variant %r needs m, n, k < 2^30" % PACKED_VARIANT
+    elif variant == "padded":
+        if plan["k_split"] != 0:
+            return False, "variant 'padded' chooses its own k_split (give 0)"
+        if m >= 2**30 or n + 15 >= 2**30 or k + 15 >= 2**30 or batch > 65535:
+            return False, "variant 'padded' needs m, n+15, k+15 < 2^30 and batch <= 65535"
     elif variant != "generic" and plan["k_split"] != 0:
         return False, "k_split applies to variants 'skinny' and %r only" % PACKED_VARIANT
     lds, workgroups = required_resources(plan)
@@ -300,11 +321,29 @@ def modeled_counts(plan):
         # B once per 16-row group; each column group reads its A rows once
         l2_bytes = (groups * (b * -(-k // 64) * 64 * n) + b * m * k * packed_columns(plan)[1]
                     + 4 * b * m * n * (2 if plan["has_d"] else 1) + partial)
+    elif variant == "padded":
+        inner = padded_inner_plan(plan)
+        l2_bytes = modeled_counts(inner)["bytes_l2_modeled"] + _padded_copy_bytes(plan, inner)
     else:
         l2_bytes = b * (m * n * k + -(-m // 4) * n * k) + 4 * b * m * n
     return {"ops": ops, "macs": ops // 2, "bytes_algorithmic": alg, "bytes_l2_modeled": l2_bytes,
             "workgroups": wgs, "lds_bytes": lds,
             "arithmetic_intensity": ops / alg if alg else math.inf}
+
+
+def _padded_copy_bytes(plan, inner):
+    """Bytes the padded variant moves besides its inner product: A and B read
+    and their padded copies written, C' read back and C written (plus D)."""
+    m, n, k, b = plan["m"], plan["n"], plan["k"], plan["batch"]
+    n_p, k_p = inner["n"], inner["k"]
+    shared = plan["b_shared"] or b == 1
+    return (b * m * k + (k * n if shared else b * k * n)
+            + b * m * k_p + (k_p * n_p if shared else b * k_p * n_p)
+            + 4 * b * m * n_p + 4 * b * m * n * (2 if plan["has_d"] else 1))
+
+
+# Launch floor of one kernel in a HIP graph on an MI355X (measured, seconds).
+_LAUNCH_S = 1.6e-6
 
 
 def modeled_objective(plan, counts):
@@ -318,6 +357,12 @@ def modeled_objective(plan, counts):
     """
     m, n, k, b = plan["m"], plan["n"], plan["k"], plan["batch"]
     variant = plan["variant"]
+    if variant == "padded":
+        # the inner product's objective, plus the copies at the HBM rate and
+        # three more launches (two pad copies, one copy-out)
+        inner = padded_inner_plan(plan)
+        t_inner, wgs = modeled_objective(inner, modeled_counts(inner))
+        return (t_inner + _padded_copy_bytes(plan, inner) / PEAK_HBM_BYTES + 3 * _LAUNCH_S, wgs)
     tm, tn = TILES[variant][:2]
     if variant.startswith("mfma") and plan["b_shared"] and b > 1:
         m, b = m * b, 1
