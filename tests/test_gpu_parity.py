@@ -481,3 +481,47 @@ def test_padded_variant_unaligned_pointers_and_pitches(dev):
     got = C.cpu().numpy()
     for b in range(batch):
         assert np.array_equal(got[b], cref.gemm_i8(A[b, :, :k], B[b, :, :n], order="ikj")), b
+
+
+# ---------------------------------------------------------------------------
+# Seeded random sweep over every variant
+# ---------------------------------------------------------------------------
+
+def _random_case(rng, variant):
+    """A random problem the variant accepts: shape, pitches, batch, shared B, D."""
+    def dim(lo, hi, mult):
+        return int(rng.integers(lo // mult, hi // mult + 1)) * mult
+    mult = 1 if variant in ("generic", "padded") else 16
+    m = int(rng.integers(1, 17)) if variant == "skinny" else int(rng.integers(1, 600))
+    n, k = dim(16, 640, mult), dim(16, 1024, mult)
+    pad_a = int(rng.integers(0, 3)) * (1 if mult == 1 else 16)
+    pad_b = int(rng.integers(0, 3)) * (1 if mult == 1 else 16)
+    batch = int(rng.choice([1, 1, 2, 3]))
+    shared_b = bool(rng.integers(0, 2))
+    has_d = bool(rng.integers(0, 2))
+    in_place = has_d and bool(rng.integers(0, 2))
+    return m, n, k, k + pad_a, n + pad_b, batch, shared_b, has_d, in_place
+
+
+@pytest.mark.parametrize("variant", ["mfma_256x256", "mfma_256x128", "mfma_128x128", "skinny",
+                                     "generic", "padded", "auto"])
+def test_random_problems_match_the_oracle(dev, variant):
+    rng = np.random.default_rng(sum(map(ord, variant)))
+    for case in range(24 if variant != "generic" else 12):
+        m, n, k, lda, ldb, batch, shared_b, has_d, in_place = _random_case(rng, variant)
+        say("random", variant, case, (m, n, k, lda, ldb, batch, shared_b, has_d, in_place))
+        A = rng.integers(-128, 128, (batch, m, lda), dtype=np.int8)
+        B = rng.integers(-128, 128, (1 if shared_b else batch, k, ldb), dtype=np.int8)
+        D = rng.integers(-(1 << 20), (1 << 20) + 1, (batch, m, n), dtype=np.int32)
+        At, Bt = torch.from_numpy(A).to(dev), torch.from_numpy(B).to(dev)
+        Dt = torch.from_numpy(D).to(dev)
+        C = Dt if in_place else torch.full((batch, m, n), INT32_MIN, dtype=torch.int32, device=dev)
+        _lib.gemm_raw(At.data_ptr(), Bt.data_ptr(), Dt.data_ptr() if has_d else None, C.data_ptr(),
+                      m, n, k, lda, ldb, n, n, batch, m * lda, 0 if shared_b else k * ldb,
+                      m * n, m * n, variant, 0, None)
+        _lib.sync(None)
+        got = C.cpu().numpy()
+        for b in range(batch):
+            want = cref.gemm_i8(A[b, :, :k], B[0 if shared_b else b, :, :n],
+                                D[b] if has_d else None, order="ikj")
+            assert np.array_equal(got[b], want), (variant, case, b)
