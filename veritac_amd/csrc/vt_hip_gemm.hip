@@ -1646,7 +1646,9 @@ int launch_packed_rows(const Problem &q, int k_split, DeviceState *st, void *str
 
 // Zero-padded int8 copy: dst[b][r][c] (r < rows_p, c < cols_p, cols_p % 16 == 0)
 // is src[b*ss + r*ld + c] where r < rows and c < cols, else 0. One thread
-// writes 16 bytes; the source is read bytewise (any alignment and stride).
+// writes 16 bytes. The source may have any alignment and stride: interior
+// chunks are read as aligned dwords that never leave the row, the row's
+// edges bytewise.
 struct PadArgs {
   const int8_t *src;
   int8_t *dst;
@@ -1663,15 +1665,29 @@ __global__ __launch_bounds__(256) void pad_i8_kernel(PadArgs p) {
   v4i out = v4i{0, 0, 0, 0};
   if (r < p.rows) {
     const int8_t *s = p.src + b * p.ss + r * p.ld;
+    if (c0 >= 4 && c0 + 20 <= p.cols) {
+      // Interior chunk: five aligned dwords starting at most 3 bytes before
+      // it cover its 16 bytes and stay inside this row; shift them into place.
+      const uintptr_t at = (uintptr_t)(s + c0);
+      const uint32_t *w = (const uint32_t *)(at & ~(uintptr_t)3);
+      const uint32_t sh = (uint32_t)(at & 3) * 8;
+      uint32_t d[5];
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      uint32_t word = 0;
+      for (int t = 0; t < 5; ++t) d[t] = w[t];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int64_t c = c0 + 4 * w + t;
-        if (c < p.cols) word |= (uint32_t)(uint8_t)s[c] << (8 * t);
+      for (int t = 0; t < 4; ++t)
+        out[t] = (int)(sh ? (d[t] >> sh) | (d[t + 1] << (32 - sh)) : d[t]);
+    } else {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int64_t c = c0 + 4 * w + t;
+          if (c < p.cols) word |= (uint32_t)(uint8_t)s[c] << (8 * t);
+        }
+        out[w] = (int)word;
       }
-      out[w] = (int)word;
     }
   }
   *(v4i *)(p.dst + b * p.sd + r * p.cols_p + c0) = out;
