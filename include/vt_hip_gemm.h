@@ -85,7 +85,7 @@ extern "C" {
  * The MFMA and skinny variants need N % 16 == 0, K % 16 == 0, lda and ldb
  * multiples of 16 and 16-byte-aligned A and B; an explicit one returns
  * VT_EUNSUPPORTED otherwise. For such shapes VT_VARIANT_AUTO picks
- * VT_VARIANT_PADDED from 2^26 multiply-adds on (M, N + 15, K + 15 < 2^30,
+ * VT_VARIANT_PADDED from 3 * 2^24 multiply-adds on (M, N + 15, K + 15 < 2^30,
  * batch <= 65535) and VT_VARIANT_GENERIC below. VT_VARIANT_PADDED keeps its
  * zero-padded copies in a workspace the library allocates once per
  * (device, stream) and grows as needed.

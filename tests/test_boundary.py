@@ -229,10 +229,10 @@ def test_packed_entry_points_refuse_overlap():
 
 
 def test_padded_variant_selection_and_refusals():
-    # unaligned shapes: the padded path from 2^26 multiply-adds, the VALU kernel below
+    # unaligned shapes: the padded path from 3 * 2^24 multiply-adds, the VALU kernel below
     assert _lib.select_variant(1000, 1000, 1000, aligned=False) == ("padded", 0)
-    assert _lib.select_variant(64, 1024, 1024, aligned=False)[0] == "padded"      # exactly 2^26
-    assert _lib.select_variant(63, 1024, 1024, aligned=False)[0] == "generic"
+    assert _lib.select_variant(48, 1024, 1024, aligned=False)[0] == "padded"      # exactly 3 * 2^24
+    assert _lib.select_variant(47, 1024, 1024, aligned=False)[0] == "generic"
     assert _lib.select_variant(17, 14335, 4095, aligned=False)[0] == "padded"
     assert _lib.select_variant(1 << 30, 16, 16, aligned=False)[0] == "generic"     # M too large
     # an explicit padded call is validated like any other before the device

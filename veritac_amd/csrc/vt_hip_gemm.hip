@@ -1108,8 +1108,20 @@ __global__ __launch_bounds__(256) void generic_kernel(GenericArgs p) {
          i += (int64_t)gridDim.y * 4) {
       uint32_t s = p.D ? (uint32_t)p.D[b * p.sd + i * p.ldd + j] : 0u;
       const int8_t *arow = Ab + i * p.lda;
-      for (int64_t t = 0; t < p.K; ++t)
-        s += (uint32_t)((int32_t)arow[t] * (int32_t)Bb[t * p.ldb + j]);
+      const int8_t *bcol = Bb + j;
+      int64_t t = 0;
+      // 16 independent loads of A and B per step, so their latencies overlap
+      for (; t + 16 <= p.K; t += 16) {
+        int32_t av[16], bv[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          av[u] = arow[t + u];
+          bv[u] = bcol[(t + u) * p.ldb];
+        }
+#pragma unroll
+        for (int u = 0; u < 16; ++u) s += (uint32_t)(av[u] * bv[u]);
+      }
+      for (; t < p.K; ++t) s += (uint32_t)((int32_t)arow[t] * (int32_t)bcol[t * p.ldb]);
       p.C[b * p.sc + i * p.ldc + j] = (int32_t)s;
     }
   }
@@ -1382,9 +1394,9 @@ int choose_k_split(int64_t N, int64_t K, int64_t batch) {
   return (int)ks;
 }
 
-// Shapes the padded path takes: enough work to repay two copy kernels and
-// one copy-out (below 2^26 multiply-adds the VALU kernel is as fast), and
-// padded sizes the vector kernels accept.
+// Shapes the padded path takes: padded sizes the vector kernels accept. Auto
+// selection takes it from 3 * 2^24 multiply-adds: below that the VALU
+// kernel is faster than one copy launch, the product and the copy-out.
 bool padded_fits(const Problem &q) {
   return q.K > 0 && q.M < (1ll << 30) && q.N + 15 < (1ll << 30) && q.K + 15 < (1ll << 30) &&
          q.batch <= 65535;
@@ -1394,7 +1406,7 @@ int select_variant(const Problem &q, bool vec, int32_t *variant, int32_t *k_spli
   *k_split = 0;
   if (!vec || q.K == 0) {
     const double macs = (double)q.M * (double)q.N * (double)q.K * (double)q.batch;
-    *variant = (padded_fits(q) && macs >= 67108864.0) ? VT_VARIANT_PADDED : VT_VARIANT_GENERIC;
+    *variant = (padded_fits(q) && macs >= 50331648.0) ? VT_VARIANT_PADDED : VT_VARIANT_GENERIC;
     return VT_OK;
   }
   if (q.M <= 16) {
@@ -1648,20 +1660,23 @@ int launch_packed_rows(const Problem &q, int k_split, DeviceState *st, void *str
 // is src[b*ss + r*ld + c] where r < rows and c < cols, else 0. One thread
 // writes 16 bytes. The source may have any alignment and stride: interior
 // chunks are read as aligned dwords that never leave the row, the row's
-// edges bytewise.
+// edges bytewise. A and B are copied by one launch: blockIdx.z picks the
+// operand, and blocks past that operand's grid or batch count exit.
 struct PadArgs {
   const int8_t *src;
   int8_t *dst;
   int64_t ld, ss, sd;
   int64_t rows, cols, rows_p, cols_p;
+  int64_t batches;
 };
 
-__global__ __launch_bounds__(256) void pad_i8_kernel(PadArgs p) {
+__global__ __launch_bounds__(256) void pad_i8_kernel(PadArgs pa, PadArgs pb) {
+  const PadArgs p = blockIdx.z ? pb : pa;
   const int64_t chunks = p.cols_p / 16;
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= p.rows_p * chunks) return;
-  const int64_t r = i / chunks, c0 = (i - r * chunks) * 16;
   const int64_t b = blockIdx.y;
+  if (i >= p.rows_p * chunks || b >= p.batches) return;
+  const int64_t r = i / chunks, c0 = (i - r * chunks) * 16;
   v4i out = v4i{0, 0, 0, 0};
   if (r < p.rows) {
     const int8_t *s = p.src + b * p.ss + r * p.ld;
@@ -1734,19 +1749,14 @@ int launch_padded(const Problem &q, DeviceState *st, void *stream) {
   int8_t *Ap = (int8_t *)w->partials, *Bp = Ap + a_bytes;
   int32_t *Cp = (int32_t *)(Bp + b_bytes);
   hipStream_t s = (hipStream_t)stream;
-  const PadArgs pa = {q.A, Ap, q.lda, bA > 1 ? q.sa : 0, q.M * Kp, q.M, q.K, q.M, Kp};
-  const PadArgs pb = {q.B, Bp, q.ldb, bB > 1 ? q.sb : 0, Kp * Np, q.K, q.N, Kp, Np};
-  const struct {
-    const PadArgs &args;
-    int64_t batches;
-  } copies[2] = {{pa, bA}, {pb, bB}};
-  for (const auto &cp : copies) {
-    const int64_t threads = cp.args.rows_p * (cp.args.cols_p / 16);
-    if ((threads + 255) / 256 > 0x7fffffff) return fail(VT_EUNSUPPORTED, "padded copy grid too large");
-    hipLaunchKernelGGL(pad_i8_kernel, dim3((unsigned)((threads + 255) / 256), (unsigned)cp.batches),
-                       dim3(256), 0, s, cp.args);
-    VT_HIP_CHECK(hipGetLastError());
-  }
+  const PadArgs pa = {q.A, Ap, q.lda, bA > 1 ? q.sa : 0, q.M * Kp, q.M, q.K, q.M, Kp, bA};
+  const PadArgs pb = {q.B, Bp, q.ldb, bB > 1 ? q.sb : 0, Kp * Np, q.K, q.N, Kp, Np, bB};
+  const int64_t blocks_a = (q.M * (Kp / 16) + 255) / 256, blocks_b = (Kp * (Np / 16) + 255) / 256;
+  const int64_t blocks = blocks_a > blocks_b ? blocks_a : blocks_b;
+  if (blocks > 0x7fffffff) return fail(VT_EUNSUPPORTED, "padded copy grid too large");
+  hipLaunchKernelGGL(pad_i8_kernel, dim3((unsigned)blocks, (unsigned)(bA > bB ? bA : bB), 2),
+                     dim3(256), 0, s, pa, pb);
+  VT_HIP_CHECK(hipGetLastError());
   const Problem g = {Ap, Bp, nullptr, Cp, q.M, Np, Kp, Kp, Np, Np, Np, q.batch,
                      bA > 1 ? q.M * Kp : 0, bB > 1 ? Kp * Np : 0, 0, q.M * Np};
   int32_t v = 0, ks = 0;

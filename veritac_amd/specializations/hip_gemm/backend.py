@@ -359,10 +359,10 @@ def modeled_objective(plan, counts):
     variant = plan["variant"]
     if variant == "padded":
         # the inner product's objective, plus the copies at the HBM rate and
-        # three more launches (two pad copies, one copy-out)
+        # two more launches (one copy of A and B, one copy-out)
         inner = padded_inner_plan(plan)
         t_inner, wgs = modeled_objective(inner, modeled_counts(inner))
-        return (t_inner + _padded_copy_bytes(plan, inner) / PEAK_HBM_BYTES + 3 * _LAUNCH_S, wgs)
+        return (t_inner + _padded_copy_bytes(plan, inner) / PEAK_HBM_BYTES + 2 * _LAUNCH_S, wgs)
     tm, tn = TILES[variant][:2]
     if variant.startswith("mfma") and plan["b_shared"] and b > 1:
         m, b = m * b, 1
