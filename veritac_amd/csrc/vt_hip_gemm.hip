@@ -892,16 +892,29 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(ReduceArgs p) {
   const int64_t e = i * 4;
   const int row = (int)(e / p.N), col = (int)(e - (int64_t)row * p.N);
   const int32_t *w = p.ws + (int64_t)bidx * p.k_split * p.M * p.N + e;
-  v4i s = __builtin_nontemporal_load((const v4i *)w);
-  for (int q = 1; q < p.k_split; ++q) {
-    const v4i o = __builtin_nontemporal_load((const v4i *)(w + (int64_t)q * p.M * p.N));
-#pragma unroll
-    for (int t = 0; t < 4; ++t) s[t] = add_wrap(s[t], o[t]);
-  }
+  const int64_t slice = (int64_t)p.M * p.N;
   int32_t *c = p.C + bidx * p.sc + (int64_t)row * p.ldc + col;
-  const int32_t *d = HAS_D ? p.D + bidx * p.sd + (int64_t)row * p.ldd + col : nullptr;
+  v4i s = v4i{0, 0, 0, 0};
+  if constexpr (HAS_D) {
+    const int32_t *d = p.D + bidx * p.sd + (int64_t)row * p.ldd + col;
 #pragma unroll
-  for (int t = 0; t < 4; ++t) c[t] = HAS_D ? add_wrap(s[t], d[t]) : s[t];
+    for (int t = 0; t < 4; ++t) s[t] = d[t];
+  }
+  // Up to 8 partials in flight at once: every load of a batch is issued
+  // before the first add waits.
+  for (int q = 0; q < p.k_split; q += 8) {
+    v4i o[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      o[u] = q + u < p.k_split ? __builtin_nontemporal_load((const v4i *)(w + (q + u) * slice))
+                               : v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) s[t] = add_wrap(s[t], o[u][t]);
+  }
+#pragma unroll
+  for (int t = 0; t < 4; ++t) c[t] = s[t];
 }
 
 // ---------------------------------------------------------------------------
