@@ -86,9 +86,10 @@ extern "C" {
  * multiples of 16 and 16-byte-aligned A and B; an explicit one returns
  * VT_EUNSUPPORTED otherwise. For such shapes VT_VARIANT_AUTO picks
  * VT_VARIANT_PADDED from 3 * 2^24 multiply-adds on (M, N + 15, K + 15 < 2^30,
- * batch <= 65535) and VT_VARIANT_GENERIC below. VT_VARIANT_PADDED keeps its
- * zero-padded copies in a workspace the library allocates once per
- * (device, stream) and grows as needed.
+ * batch <= 65535) and VT_VARIANT_GENERIC below. VT_VARIANT_PADDED copies
+ * the operands the vector variants cannot read as they are, zero padded, to
+ * a workspace the library allocates once per (device, stream) and grows as
+ * needed; when N % 16 == 0 the product writes C directly.
  *
  * Sizes up to 2^40, leading dimensions up to 2^40, batch up to 2^31, batch
  * strides up to 2^56, and every operand's byte extent below 2^56. C may not

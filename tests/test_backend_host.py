@@ -195,6 +195,15 @@ def test_padded_plans_take_any_n_and_k():
     assert hg.validate_plan(p)[0] and hg.padded_inner_plan(p)["variant"] == "skinny"
     assert hg.validate_plan(dict(p, k_split=2)) == (False, "variant 'padded' chooses its own k_split (give 0)")
     assert not hg.validate_plan(dict(p, batch=70000))[0]
+    # only operands the vector kernels cannot read as they are get copied, and
+    # with n % 16 == 0 the product writes C and adds D itself (no copy-out)
+    p = hg.make_plan(3000, 2000, 1500, has_d=True, d_max_abs=5, variant="padded")
+    assert hg._padded_copies(p) == (True, True, False)
+    inner = hg.padded_inner_plan(p)
+    assert inner["has_d"] and inner["d_max_abs"] == 5 and (inner["n"], inner["k"]) == (2000, 1504)
+    assert hg._padded_copy_bytes(p, inner) < 3000 * 2000 * 4              # no C traffic priced
+    assert hg._padded_copies(hg.make_plan(300, 1001, 1024, variant="padded")) == (False, True, True)
+    assert hg._padded_copies(hg.make_plan(256, 256, 256, variant="padded")) == (False, False, False)
     # small unaligned shapes stay on the VALU kernel; aligned shapes never pick padded
     assert hg.make_plan(64, 60, 64)["variant"] == "generic"
     assert hg.optimize(1024, 1024, 1024)["winner"]["variant"].startswith("mfma")

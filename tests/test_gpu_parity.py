@@ -430,14 +430,21 @@ def test_decode_kernel_padded_strides(dev):
 # ---------------------------------------------------------------------------
 
 PADDED_SHAPES = [(1000, 1000, 1000, 1), (1001, 999, 1003, 1), (16, 14335, 4095, 1),
-                 (1, 4097, 4095, 1), (300, 500, 1000, 3), (5, 7, 9, 1)]
+                 (1, 4097, 4095, 1), (300, 500, 1000, 3), (5, 7, 9, 1),
+                 # N % 16 == 0: the product writes C and adds D itself
+                 (500, 2000, 1500, 1), (200, 512, 777, 3), (7, 4096, 1001, 1),
+                 # K % 16 == 0: A is read in place, only B is copied
+                 (300, 1001, 1024, 1), (16, 14335, 4096, 1), (100, 333, 512, 2),
+                 # aligned: nothing is copied
+                 (256, 256, 256, 1), (64, 512, 512, 2)]
 
 
 @pytest.mark.parametrize("shape", PADDED_SHAPES)
 def test_padded_variant(dev, shape):
-    """K and N not multiples of 16: zero-padded copies through the MFMA or
-    skinny kernel, then C (plus D, also in place) copied out; compared with
-    the C oracle and with the VALU kernel."""
+    """K and N not multiples of 16: zero-padded copies of the operands that
+    need them through the MFMA or skinny kernel, then C (plus D, also in
+    place) copied out or, when N % 16 == 0, written by the product; compared
+    with the C oracle and with the VALU kernel."""
     m, n, k, batch = shape
     rng = np.random.default_rng(m + n + k + batch)
     A = rng.integers(-128, 128, (batch, m, k) if batch > 1 else (m, k), dtype=np.int8)
@@ -481,6 +488,37 @@ def test_padded_variant_unaligned_pointers_and_pitches(dev):
     got = C.cpu().numpy()
     for b in range(batch):
         assert np.array_equal(got[b], cref.gemm_i8(A[b, :, :k], B[b, :, :n], order="ikj")), b
+
+
+@pytest.mark.parametrize("case", ["a_offset", "b_pitch", "b_stride"])
+def test_padded_variant_copies_only_misaligned_operands(dev, case):
+    """K and N multiples of 16 with one operand the vector kernels cannot read
+    (A at an odd address, B with an odd pitch or batch stride): only that
+    operand is copied and the product writes C itself, here with D in place
+    and C at a pitch that is not a multiple of 16."""
+    batch, m, n, k = 2, 200, 320, 512
+    a_off = 1 if case == "a_offset" else 0
+    ldb = n + 5 if case == "b_pitch" else n
+    sb = k * ldb + (4 if case == "b_stride" else 0)
+    ldc = n + 3
+    rng = np.random.default_rng(11)
+    A = rng.integers(-128, 128, (batch, m, k), dtype=np.int8)
+    Bflat = rng.integers(-128, 128, batch * sb, dtype=np.int8)
+    Bs = [Bflat[b * sb:b * sb + k * ldb].reshape(k, ldb)[:, :n] for b in range(batch)]
+    D = rng.integers(-(1 << 20), (1 << 20) + 1, (batch, m, ldc), dtype=np.int32)
+    Abuf = torch.zeros(A.size + 16, dtype=torch.int8, device=dev)
+    Abuf[a_off:a_off + A.size] = torch.from_numpy(A.reshape(-1)).to(dev)
+    Bt = torch.from_numpy(Bflat).to(dev)
+    C = torch.from_numpy(D.copy()).to(dev)
+    say("padded copies", case)
+    _lib.gemm_raw(Abuf.data_ptr() + a_off, Bt.data_ptr(), C.data_ptr(), C.data_ptr(), m, n, k,
+                  k, ldb, ldc, ldc, batch, m * k, sb, m * ldc, m * ldc, "padded", 0, None)
+    _lib.sync(None)
+    got = C.cpu().numpy()
+    for b in range(batch):
+        want = (cref.gemm_i8(A[b], Bs[b], order="ikj").astype(np.int64) + D[b, :, :n]).astype(np.int32)
+        assert np.array_equal(got[b, :, :n], want), b
+        assert np.array_equal(got[b, :, n:], D[b, :, n:]), b                 # past N untouched
 
 
 # ---------------------------------------------------------------------------

@@ -208,7 +208,7 @@ struct GemmArgs {
   int batch_count;   // batches (the persistent kernel walks all their tiles)
 };
 
-template <int BM, int BN, bool EDGE, bool HAS_D, bool SHORT>
+template <int BM, int BN, bool EDGE, bool HAS_D, bool SHORT, bool EARLY_D>
 __global__ __launch_bounds__(256, 1) void gemm_mfma_kernel(GemmArgs p) {
   constexpr int BK = 64;
   constexpr int WTM = BM / 2, WTN = BN / 2;   // wave tile (2x2 waves)
@@ -368,12 +368,18 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma_kernel(GemmArgs p) {
   // wait on LDS latency across steps. The single barrier per step also
   // guarantees every wave has finished reading buffer kt%3 before step kt+1
   // overwrites it with slice kt+3.
-  // Small wave tiles (at most 4 accumulator blocks, 64 registers) load their
-  // initial partial sums D here, so that memory round trip overlaps the k
-  // loop instead of following it: the epilogue's block-by-block D loads
-  // otherwise add ~6 us to a 128^3..512^3 GEMM.
-  constexpr bool D_EARLY = HAS_D && MI * NI <= 4;
-  int32_t d_pre[D_EARLY ? MI : 1][D_EARLY ? NI : 1][16];
+  // Small wave tiles (at most 4 accumulator blocks) hold the whole tile's
+  // initial partial sums D in 64 registers, loaded in one round trip before
+  // any C store (block-by-block loads would each wait for the previous
+  // block's stores: vmcnt is in order). With EARLY_D they are loaded here,
+  // so the round trip overlaps the k loop (~6 us less on a 128^3..512^3
+  // GEMM), but 64 registers live across the loop cut occupancy from 3 waves
+  // per SIMD to 1: the host asks for it only when the grid fits one
+  // workgroup per CU. Otherwise they are loaded after the loop, when its
+  // registers are free.
+  constexpr bool D_TILE = HAS_D && MI * NI <= 4;
+  constexpr bool D_EARLY = D_TILE && EARLY_D;
+  int32_t d_pre[D_TILE ? MI : 1][D_TILE ? NI : 1][16];
   if constexpr (D_EARLY)
     load_d_tile<MI, NI, EDGE>(d_pre, p.D + bidx * p.sd, p.ldd, m0 + wm * WTM, n0 + wn * WTN, M, N,
                               lane);
@@ -450,7 +456,10 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma_kernel(GemmArgs p) {
     }
   }
 
-  if constexpr (D_EARLY) {
+  if constexpr (D_TILE) {
+    if constexpr (!D_EARLY)
+      load_d_tile<MI, NI, EDGE>(d_pre, p.D + bidx * p.sd, p.ldd, m0 + wm * WTM, n0 + wn * WTN, M,
+                                N, lane);
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
@@ -1457,9 +1466,17 @@ bool offsets_fit_32(const Problem &q, int64_t m_rows) {
 constexpr int kDmaWaves = 4;
 
 template <int BM, int BN, bool EDGE, bool HAS_D>
-void launch_mfma_kernel(bool short_k, dim3 grid, dim3 block, hipStream_t stream, const GemmArgs &a) {
-  if (short_k) hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, EDGE, HAS_D, true>), grid, block, 0, stream, a);
-  else hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, EDGE, HAS_D, false>), grid, block, 0, stream, a);
+void launch_mfma_kernel(bool short_k, bool early_d, dim3 grid, dim3 block, hipStream_t stream,
+                        const GemmArgs &a) {
+  if constexpr (HAS_D) {
+    if (early_d) {
+      if (short_k) hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, EDGE, true, true, true>), grid, block, 0, stream, a);
+      else hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, EDGE, true, false, true>), grid, block, 0, stream, a);
+      return;
+    }
+  }
+  if (short_k) hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, EDGE, HAS_D, true, false>), grid, block, 0, stream, a);
+  else hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, EDGE, HAS_D, false, false>), grid, block, 0, stream, a);
 }
 
 template <int BM, int BN>
@@ -1496,12 +1513,13 @@ int launch_mfma(const Problem &q, hipStream_t stream, int num_cus) {
   }
   const bool edge = (r.M % BM) || (r.N % BN) || (r.K % 128);
   const bool short_k = r.K <= 128;
+  const bool early_d = blocks <= num_cus;   // one workgroup per CU: occupancy costs nothing
   if (edge) {
-    if (has_d) launch_mfma_kernel<BM, BN, true, true>(short_k, grid, block, stream, a);
-    else launch_mfma_kernel<BM, BN, true, false>(short_k, grid, block, stream, a);
+    if (has_d) launch_mfma_kernel<BM, BN, true, true>(short_k, early_d, grid, block, stream, a);
+    else launch_mfma_kernel<BM, BN, true, false>(short_k, early_d, grid, block, stream, a);
   } else {
-    if (has_d) launch_mfma_kernel<BM, BN, false, true>(short_k, grid, block, stream, a);
-    else launch_mfma_kernel<BM, BN, false, false>(short_k, grid, block, stream, a);
+    if (has_d) launch_mfma_kernel<BM, BN, false, true>(short_k, early_d, grid, block, stream, a);
+    else launch_mfma_kernel<BM, BN, false, false>(short_k, early_d, grid, block, stream, a);
   }
   VT_HIP_CHECK(hipGetLastError());
   return VT_OK;
@@ -1689,7 +1707,11 @@ __global__ __launch_bounds__(256) void pad_i8_kernel(PadArgs pa, PadArgs pb) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t b = blockIdx.y;
   if (i >= p.rows_p * chunks || b >= p.batches) return;
-  const int64_t r = i / chunks, c0 = (i - r * chunks) * 16;
+  // 32-bit division whenever the index fits (64-bit division is a long
+  // software sequence)
+  const int64_t r = p.rows_p * chunks <= 0xffffffffll ? (int64_t)((uint32_t)i / (uint32_t)chunks)
+                                                      : i / chunks;
+  const int64_t c0 = (i - r * chunks) * 16;
   v4i out = v4i{0, 0, 0, 0};
   if (r < p.rows) {
     const int8_t *s = p.src + b * p.ss + r * p.ld;
@@ -1735,7 +1757,8 @@ template <bool HAS_D>
 __global__ __launch_bounds__(256) void unpad_kernel(UnpadArgs p) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= p.M * p.N) return;
-  const int64_t r = i / p.N, c = i - r * p.N, b = blockIdx.y;
+  const int64_t r = p.M * p.N <= 0xffffffffll ? (int64_t)((uint32_t)i / (uint32_t)p.N) : i / p.N;
+  const int64_t c = i - r * p.N, b = blockIdx.y;
   int32_t v = __builtin_nontemporal_load(p.src + b * p.ss + r * p.lds + c);
   if (HAS_D) v = add_wrap(v, p.D[b * p.sd + r * p.ldd + c]);
   p.C[b * p.sc + r * p.ldc + c] = v;
@@ -1747,36 +1770,69 @@ int launch_vector(const Problem &q, int32_t variant, int32_t k_split, DeviceStat
 // A and B copied with K and N rounded up to 16 (zero columns of A meet zero
 // rows of B, so the product is unchanged), multiplied by the kernel the
 // vector path selects for the padded shape, valid columns copied out with D.
+// An operand the vector kernels can already read (K, and N for B, multiples
+// of 16, 16-byte aligned base, pitch and batch stride) is used in place, and
+// when N is a multiple of 16 the product writes C (with D) directly.
 int launch_padded(const Problem &q, DeviceState *st, void *stream) {
   if (!padded_fits(q))
     return fail(VT_EUNSUPPORTED, "padded path needs K > 0, M, N+15, K+15 < 2^30, batch <= 65535");
   const int64_t Kp = (q.K + 15) / 16 * 16, Np = (q.N + 15) / 16 * 16;
   const int64_t bA = (q.batch > 1 && q.sa == 0) ? 1 : q.batch;
   const int64_t bB = (q.batch > 1 && q.sb == 0) ? 1 : q.batch;
+  const bool copy_a = Kp != q.K || q.lda % 16 || q.sa % 16 || !aligned16(q.A);
+  const bool copy_b = Kp != q.K || Np != q.N || q.ldb % 16 || q.sb % 16 || !aligned16(q.B);
+  const bool copy_c = Np != q.N;
   auto round256 = [](int64_t v) { return (v + 255) / 256 * 256; };
-  const int64_t a_bytes = round256(bA * q.M * Kp), b_bytes = round256(bB * Kp * Np);
-  const int64_t c_bytes = round256(q.batch * q.M * Np * 4);
-  Workspace *w = nullptr;
-  int rc = get_workspace(st, stream, (size_t)(a_bytes + b_bytes + c_bytes), &w, true);
-  if (rc) return rc;
-  int8_t *Ap = (int8_t *)w->partials, *Bp = Ap + a_bytes;
-  int32_t *Cp = (int32_t *)(Bp + b_bytes);
+  const int64_t a_bytes = copy_a ? round256(bA * q.M * Kp) : 0;
+  const int64_t b_bytes = copy_b ? round256(bB * Kp * Np) : 0;
+  const int64_t c_bytes = copy_c ? round256(q.batch * q.M * Np * 4) : 0;
+  Problem g = q;
+  g.N = Np;
+  g.K = Kp;
   hipStream_t s = (hipStream_t)stream;
-  const PadArgs pa = {q.A, Ap, q.lda, bA > 1 ? q.sa : 0, q.M * Kp, q.M, q.K, q.M, Kp, bA};
-  const PadArgs pb = {q.B, Bp, q.ldb, bB > 1 ? q.sb : 0, Kp * Np, q.K, q.N, Kp, Np, bB};
-  const int64_t blocks_a = (q.M * (Kp / 16) + 255) / 256, blocks_b = (Kp * (Np / 16) + 255) / 256;
-  const int64_t blocks = blocks_a > blocks_b ? blocks_a : blocks_b;
-  if (blocks > 0x7fffffff) return fail(VT_EUNSUPPORTED, "padded copy grid too large");
-  hipLaunchKernelGGL(pad_i8_kernel, dim3((unsigned)blocks, (unsigned)(bA > bB ? bA : bB), 2),
-                     dim3(256), 0, s, pa, pb);
-  VT_HIP_CHECK(hipGetLastError());
-  const Problem g = {Ap, Bp, nullptr, Cp, q.M, Np, Kp, Kp, Np, Np, Np, q.batch,
-                     bA > 1 ? q.M * Kp : 0, bB > 1 ? Kp * Np : 0, 0, q.M * Np};
+  if (a_bytes + b_bytes + c_bytes > 0) {
+    Workspace *w = nullptr;
+    int rc = get_workspace(st, stream, (size_t)(a_bytes + b_bytes + c_bytes), &w, true);
+    if (rc) return rc;
+    int8_t *Ap = (int8_t *)w->partials, *Bp = Ap + a_bytes;
+    int32_t *Cp = (int32_t *)(Bp + b_bytes);
+    const PadArgs pa = {q.A, Ap, q.lda, bA > 1 ? q.sa : 0, q.M * Kp, q.M, q.K, q.M, Kp, bA};
+    const PadArgs pb = {q.B, Bp, q.ldb, bB > 1 ? q.sb : 0, Kp * Np, q.K, q.N, Kp, Np, bB};
+    // grid z = the operands copied; z = 0 takes the first of them
+    const int64_t blocks_a = copy_a ? (q.M * (Kp / 16) + 255) / 256 : 0;
+    const int64_t blocks_b = copy_b ? (Kp * (Np / 16) + 255) / 256 : 0;
+    const int64_t blocks = blocks_a > blocks_b ? blocks_a : blocks_b;
+    const int64_t ys = (copy_a && bA > bB) || !copy_b ? bA : bB;
+    if (blocks > 0x7fffffff) return fail(VT_EUNSUPPORTED, "padded copy grid too large");
+    if (blocks > 0) {
+      hipLaunchKernelGGL(pad_i8_kernel, dim3((unsigned)blocks, (unsigned)ys, copy_a && copy_b ? 2 : 1),
+                         dim3(256), 0, s, copy_a ? pa : pb, pb);
+      VT_HIP_CHECK(hipGetLastError());
+    }
+    if (copy_a) {
+      g.A = Ap;
+      g.lda = Kp;
+      g.sa = bA > 1 ? q.M * Kp : 0;
+    }
+    if (copy_b) {
+      g.B = Bp;
+      g.ldb = Np;
+      g.sb = bB > 1 ? Kp * Np : 0;
+    }
+    if (copy_c) {
+      g.C = Cp;
+      g.ldc = Np;
+      g.sc = q.M * Np;
+      g.D = nullptr;
+      g.ldd = Np;
+      g.sd = 0;
+    }
+  }
   int32_t v = 0, ks = 0;
   select_variant(g, true, &v, &ks);
-  rc = launch_vector(g, v, ks, st, stream);
-  if (rc) return rc;
-  UnpadArgs u = {Cp, q.D, q.C, Np, q.ldd, q.ldc, q.M * Np, q.sd, q.sc, q.M, q.N};
+  int rc = launch_vector(g, v, ks, st, stream);
+  if (rc || !copy_c) return rc;
+  UnpadArgs u = {g.C, q.D, q.C, Np, q.ldd, q.ldc, q.M * Np, q.sd, q.sc, q.M, q.N};
   const int64_t cells = q.M * q.N;
   if ((cells + 255) / 256 > 0x7fffffff) return fail(VT_EUNSUPPORTED, "padded copy-out grid too large");
   dim3 ug((unsigned)((cells + 255) / 256), (unsigned)q.batch);

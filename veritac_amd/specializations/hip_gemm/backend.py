@@ -183,10 +183,20 @@ def required_resources(plan):
 def padded_inner_plan(plan):
     """The plan the padded variant runs after copying A and B with k and n
     rounded up to 16: the vector variant the native selection picks for that
-    shape (vt_gemm_select), without D (added while copying C out)."""
+    shape (vt_gemm_select). D goes to the product when n is a multiple of 16
+    (it writes C directly), else it is added while copying C out."""
     n_p, k_p = -(-plan["n"] // DIM) * DIM, -(-plan["k"] // DIM) * DIM
     name, ks = _lib.select_variant(plan["m"], n_p, k_p, plan["batch"], k_p, n_p, True)
-    return dict(plan, n=n_p, k=k_p, variant=name, k_split=ks, has_d=False, d_max_abs=0)
+    d = plan["has_d"] and n_p == plan["n"]
+    return dict(plan, n=n_p, k=k_p, variant=name, k_split=ks, has_d=d,
+                d_max_abs=plan["d_max_abs"] if d else 0)
+
+
+def _padded_copies(plan):
+    """(copy A, copy B, copy C out) for contiguous, 16-byte-aligned operands:
+    an operand the vector kernels can read as it is is not copied."""
+    k_odd, n_odd = plan["k"] % DIM != 0, plan["n"] % DIM != 0
+    return k_odd, k_odd or n_odd, n_odd
 
 
 def make_plan(m, n, k, *, batch=1, b_shared=False, has_d=False, d_max_abs=0,
@@ -332,14 +342,15 @@ def modeled_counts(plan):
 
 
 def _padded_copy_bytes(plan, inner):
-    """Bytes the padded variant moves besides its inner product: A and B read
-    and their padded copies written, C' read back and C written (plus D)."""
+    """Bytes the padded variant moves besides its inner product: each copied
+    operand read and its padded copy written, and, when C is copied out, C'
+    read back and C written (plus D)."""
     m, n, k, b = plan["m"], plan["n"], plan["k"], plan["batch"]
     n_p, k_p = inner["n"], inner["k"]
-    shared = plan["b_shared"] or b == 1
-    return (b * m * k + (k * n if shared else b * k * n)
-            + b * m * k_p + (k_p * n_p if shared else b * k_p * n_p)
-            + 4 * b * m * n_p + 4 * b * m * n * (2 if plan["has_d"] else 1))
+    b_mats = 1 if plan["b_shared"] or b == 1 else b
+    copy_a, copy_b, copy_c = _padded_copies(plan)
+    return ((b * m * (k + k_p) if copy_a else 0) + (b_mats * (k * n + k_p * n_p) if copy_b else 0)
+            + (4 * b * m * n_p + 4 * b * m * n * (2 if plan["has_d"] else 1) if copy_c else 0))
 
 
 # Launch floor of one kernel in a HIP graph on an MI355X (measured, seconds).
@@ -359,10 +370,12 @@ def modeled_objective(plan, counts):
     variant = plan["variant"]
     if variant == "padded":
         # the inner product's objective, plus the copies at the HBM rate and
-        # two more launches (one copy of A and B, one copy-out)
+        # their launches (one for the operands, one for the copy-out)
         inner = padded_inner_plan(plan)
         t_inner, wgs = modeled_objective(inner, modeled_counts(inner))
-        return (t_inner + _padded_copy_bytes(plan, inner) / PEAK_HBM_BYTES + 2 * _LAUNCH_S, wgs)
+        copy_a, copy_b, copy_c = _padded_copies(plan)
+        launches = int(copy_a or copy_b) + int(copy_c)
+        return (t_inner + _padded_copy_bytes(plan, inner) / PEAK_HBM_BYTES + launches * _LAUNCH_S, wgs)
     tm, tn = TILES[variant][:2]
     if variant.startswith("mfma") and plan["b_shared"] and b > 1:
         m, b = m * b, 1
