@@ -1744,7 +1744,10 @@ __global__ __launch_bounds__(256) void pad_i8_kernel(PadArgs pa, PadArgs pb) {
 }
 
 // C[b][r][c] = src[b][r][c] (+ D[b][r][c]) for c < N: the padded product's
-// valid columns, wrapping mod 2^32. Elementwise, so D may be C itself.
+// valid columns, wrapping mod 2^32. Elementwise, so D may be C itself. One
+// thread takes 4 columns: the source (workspace base, row pitch lds and
+// batch stride ss all multiples of 16 bytes, lds >= N rounded up to 4) is
+// read as one 16-byte load, C and D, of any alignment, per element.
 struct UnpadArgs {
   const int32_t *src;
   const int32_t *D;
@@ -1755,13 +1758,24 @@ struct UnpadArgs {
 
 template <bool HAS_D>
 __global__ __launch_bounds__(256) void unpad_kernel(UnpadArgs p) {
+  const int64_t quads = (p.N + 3) / 4;
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= p.M * p.N) return;
-  const int64_t r = p.M * p.N <= 0xffffffffll ? (int64_t)((uint32_t)i / (uint32_t)p.N) : i / p.N;
-  const int64_t c = i - r * p.N, b = blockIdx.y;
-  int32_t v = __builtin_nontemporal_load(p.src + b * p.ss + r * p.lds + c);
-  if (HAS_D) v = add_wrap(v, p.D[b * p.sd + r * p.ldd + c]);
-  p.C[b * p.sc + r * p.ldc + c] = v;
+  if (i >= p.M * quads) return;
+  const int64_t r = p.M * quads <= 0xffffffffll ? (int64_t)((uint32_t)i / (uint32_t)quads)
+                                                : i / quads;
+  const int64_t c0 = (i - r * quads) * 4, b = blockIdx.y;
+  const v4i v = __builtin_nontemporal_load((const v4i *)(p.src + b * p.ss + r * p.lds + c0));
+  const int32_t *d = HAS_D ? p.D + b * p.sd + r * p.ldd + c0 : nullptr;
+  int32_t *c = p.C + b * p.sc + r * p.ldc + c0;
+  int32_t dv[4] = {0, 0, 0, 0};
+  if constexpr (HAS_D) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      if (c0 + t < p.N) dv[t] = d[t];
+  }
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+    if (c0 + t < p.N) c[t] = add_wrap(v[t], dv[t]);
 }
 
 int launch_vector(const Problem &q, int32_t variant, int32_t k_split, DeviceState *st,
@@ -1833,7 +1847,7 @@ int launch_padded(const Problem &q, DeviceState *st, void *stream) {
   int rc = launch_vector(g, v, ks, st, stream);
   if (rc || !copy_c) return rc;
   UnpadArgs u = {g.C, q.D, q.C, Np, q.ldd, q.ldc, q.M * Np, q.sd, q.sc, q.M, q.N};
-  const int64_t cells = q.M * q.N;
+  const int64_t cells = q.M * ((q.N + 3) / 4);   // one thread per 4 columns
   if ((cells + 255) / 256 > 0x7fffffff) return fail(VT_EUNSUPPORTED, "padded copy-out grid too large");
   dim3 ug((unsigned)((cells + 255) / 256), (unsigned)q.batch);
   if (q.D) hipLaunchKernelGGL(unpad_kernel<true>, ug, dim3(256), 0, s, u);
