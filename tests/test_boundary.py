@@ -46,7 +46,12 @@ def test_native_selection_for_benchmark_configs():
     assert _lib.select_variant(1, 14336, 4096)[0] == "skinny"
     assert _lib.select_variant(8192, 8192, 8192) == ("mfma_256x256", 0)
     assert _lib.select_variant(512, 1024, 1024, 64)[0].startswith("mfma")
-    assert _lib.select_variant(64, 64, 64)[0] == "mfma_128x128"
+    # tiny problems (M > 16, K <= 64, at most 2^20 multiply-adds) run on the VALU kernel
+    assert _lib.select_variant(64, 64, 64)[0] == "generic"
+    assert _lib.select_variant(64, 256, 64)[0] == "generic"                      # exactly 2^20
+    assert _lib.select_variant(64, 272, 64)[0] == "mfma_128x128"
+    assert _lib.select_variant(16, 256, 64)[0] == "skinny"
+    assert _lib.select_variant(128, 128, 128)[0] == "mfma_128x128"
     assert _lib.select_variant(64, 60, 64, aligned=False)[0] == "generic"
 
 

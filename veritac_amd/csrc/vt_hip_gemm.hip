@@ -1431,6 +1431,15 @@ int select_variant(const Problem &q, bool vec, int32_t *variant, int32_t *k_spli
     *variant = (padded_fits(q) && macs >= 50331648.0) ? VT_VARIANT_PADDED : VT_VARIANT_GENERIC;
     return VT_OK;
   }
+  // Tiny problems past the skinny kernel's rows: with K <= 64 the VALU
+  // kernel's K loop is four batches of loads, under the MFMA kernels' fixed
+  // cost (64^3: 2.5 us against 4.3 us per launch in a HIP graph; from 128^3
+  // on the MFMA kernel is faster).
+  if (q.M > 16 && q.K <= 64 &&
+      (double)q.M * (double)q.N * (double)q.K * (double)q.batch <= 1048576.0) {
+    *variant = VT_VARIANT_GENERIC;
+    return VT_OK;
+  }
   if (q.M <= 16) {
     *variant = VT_VARIANT_SKINNY;
     *k_split = choose_k_split(q.N, q.K, q.batch);
@@ -1844,7 +1853,7 @@ int launch_padded(const Problem &q, DeviceState *st, void *stream) {
   }
   int32_t v = 0, ks = 0;
   select_variant(g, true, &v, &ks);
-  int rc = launch_vector(g, v, ks, st, stream);
+  int rc = v == VT_VARIANT_GENERIC ? launch_generic(g, s) : launch_vector(g, v, ks, st, stream);
   if (rc || !copy_c) return rc;
   UnpadArgs u = {g.C, q.D, q.C, Np, q.ldd, q.ldc, q.M * Np, q.sd, q.sc, q.M, q.N};
   const int64_t cells = q.M * ((q.N + 3) / 4);   // one thread per 4 columns

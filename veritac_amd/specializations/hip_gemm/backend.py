@@ -353,8 +353,14 @@ def _padded_copy_bytes(plan, inner):
             + (4 * b * m * n_p + 4 * b * m * n * (2 if plan["has_d"] else 1) if copy_c else 0))
 
 
-# Launch floor of one kernel in a HIP graph on an MI355X (measured, seconds).
+# Latency floors measured on an MI355X (seconds): one kernel launch in a HIP
+# graph; one load -> MFMA -> store round trip of a vector kernel; one 64-deep
+# K slice of an MFMA workgroup; 16 K steps of the VALU kernel (its loads of
+# A and B are issued 16 at a time).
 _LAUNCH_S = 1.6e-6
+_ROUND_TRIP_S = 2.0e-6
+_SLICE_S = 0.35e-6
+_GENERIC_STEP_S = 0.3e-6
 
 
 def modeled_objective(plan, counts):
@@ -386,7 +392,18 @@ def modeled_objective(plan, counts):
     eff = _MODEL_MFMA_EFF[variant] * (fill if variant.startswith("mfma") else 1.0)
     t_compute = padded_ops / (PEAK_INT8_OPS * eff)
     t_memory = counts["bytes_algorithmic"] / (PEAK_HBM_BYTES * min(1.0, wgs / NUM_CUS))
-    return (max(t_compute, t_memory), wgs)
+    t = max(t_compute, t_memory)
+    # latency floors: a launch each, and a workgroup's K loop
+    if variant == "generic":
+        return (_LAUNCH_S + max(t, -(-k // 16) * _GENERIC_STEP_S), wgs)
+    launches = 1
+    if variant == "skinny":
+        launches += skinny_split(plan)[0] > 1
+    elif variant == PACKED_VARIANT:
+        launches += packed_split(plan)[0] > 1
+    else:
+        t = max(t, -(-k // 64) * _SLICE_S)
+    return (launches * _LAUNCH_S + _ROUND_TRIP_S + t, wgs)
 
 
 def gen_candidates(m, n, k, *, batch=1, b_shared=False, has_d=False, d_max_abs=0):
