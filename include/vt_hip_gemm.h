@@ -89,7 +89,10 @@ extern "C" {
  * batch <= 65535) and VT_VARIANT_GENERIC below. VT_VARIANT_PADDED copies
  * the operands the vector variants cannot read as they are, zero padded, to
  * a workspace the library allocates once per (device, stream) and grows as
- * needed; when N % 16 == 0 the product writes C directly.
+ * needed; when N % 16 == 0 the product writes C directly. For aligned
+ * shapes VT_VARIANT_AUTO picks VT_VARIANT_SKINNY for M <= 16,
+ * VT_VARIANT_GENERIC when K <= 64 and M * N * K * batch <= 2^20 (faster than
+ * any MFMA launch there), and an MFMA variant otherwise.
  *
  * Sizes up to 2^40, leading dimensions up to 2^40, batch up to 2^31, batch
  * strides up to 2^56, and every operand's byte extent below 2^56. C may not
