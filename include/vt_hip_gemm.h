@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define VT_ABI_VERSION 6
+#define VT_ABI_VERSION 7
 
 /* Status codes. */
 #define VT_OK 0
@@ -92,7 +92,20 @@ extern "C" {
  * needed; when N % 16 == 0 the product writes C directly. For aligned
  * shapes VT_VARIANT_AUTO picks VT_VARIANT_SKINNY for M <= 16,
  * VT_VARIANT_GENERIC when K <= 64 and M * N * K * batch <= 2^20 (faster than
- * any MFMA launch there), and an MFMA variant otherwise.
+ * any MFMA launch there), and an MFMA variant otherwise. The MFMA variants
+ * address each tile from a 64-bit base with 32-bit offsets inside it, so
+ * they need 256 * lda and 64 * ldb below 2^32 (K < 2^24 for contiguous A):
+ * VT_VARIANT_AUTO picks VT_VARIANT_GENERIC beyond that, and an explicit MFMA
+ * variant returns VT_EUNSUPPORTED.
+ *
+ * Workspace: the skinny variant's K-split partial sums and the padded
+ * variant's copies live in workspaces the library allocates per (device,
+ * stream, kind). A workspace only grows, and a superseded one is kept (not
+ * freed) until the process ends, so a HIP graph captured with an earlier
+ * workspace stays valid. Growth is refused while the stream is being
+ * captured: a call that needs more workspace than its stream has returns
+ * VT_EUNSUPPORTED during capture, so make the largest call once on the
+ * stream before capturing (vt_gemm_check reports the bytes a call needs).
  *
  * Sizes up to 2^40, leading dimensions up to 2^40, batch up to 2^31, batch
  * strides up to 2^56, and every operand's byte extent below 2^56. C may not
@@ -108,12 +121,41 @@ int vt_gemm_i8(const int8_t *A, const int8_t *B, const int32_t *D, int32_t *C,
                int32_t variant, int32_t k_split, void *stream);
 
 /*
- * vt_gemm_select -- the variant (and K split) VT_VARIANT_AUTO would launch.
- * Mirrors the reference's candidate selection (`optimize`,
- * backend.py:1072-1093) at the native layer; no device call.
+ * vt_gemm_check -- the host-side acceptance check of vt_gemm_i8, without
+ * operands: returns VT_OK when vt_gemm_i8 would accept a call with these
+ * sizes, strides, D present or not (has_d), variant and k_split on distinct
+ * 16-byte aligned buffers, else the VT_E* code vt_gemm_i8 would return, with
+ * the reason in vt_last_error(). On VT_OK it stores the variant and K split
+ * that would run (VT_VARIANT_AUTO resolved; VT_VARIANT_AUTO and 0 when there
+ * is nothing to compute) and the bytes of workspace the call takes. Any
+ * output pointer may be NULL. No device call: it runs without a GPU.
+ *
+ * The counterpart of the reference's external plan checker `gemmini_check`
+ * (specializations/gemmini_gemm/backend.py:164-196), whose verdict
+ * `optimize` records per candidate as check{accepted, reason}
+ * (backend.py:1083-1091).
+ */
+int vt_gemm_check(int64_t M, int64_t N, int64_t K,
+                  int64_t lda, int64_t ldb, int64_t ldd, int64_t ldc,
+                  int64_t batch, int64_t stride_a, int64_t stride_b,
+                  int64_t stride_d, int64_t stride_c,
+                  int32_t has_d, int32_t variant, int32_t k_split,
+                  int32_t *variant_out, int32_t *k_split_out,
+                  int64_t *scratch_bytes_out);
+
+/* vt_gemm_select flags. */
+#define VT_SELECT_ALIGNED 1   /* A and B 16-byte aligned (else: unaligned) */
+#define VT_SELECT_B_SHARED 2  /* batch > 1 shares one B (stride_b == 0)    */
+
+/*
+ * vt_gemm_select -- the variant (and K split) VT_VARIANT_AUTO would launch
+ * for contiguous operands (stride_a = M*lda, stride_c = M*N, stride_b 0 with
+ * VT_SELECT_B_SHARED else K*ldb). Mirrors the reference's candidate
+ * selection (`optimize`, backend.py:1072-1093) at the native layer; no
+ * device call.
  */
 int vt_gemm_select(int64_t M, int64_t N, int64_t K, int64_t batch,
-                   int64_t lda, int64_t ldb, int32_t aligned16,
+                   int64_t lda, int64_t ldb, int32_t flags,
                    int32_t *variant_out, int32_t *k_split_out);
 
 /*

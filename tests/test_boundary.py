@@ -243,3 +243,98 @@ def test_padded_variant_selection_and_refusals():
     # an explicit padded call is validated like any other before the device
     assert call(variant=6, M=-1) == _lib.VT_EINVAL
     assert call(variant=6, C=(1 << 20) + 8) == _lib.VT_EINVAL                    # C over A
+
+
+# ---------------------------------------------------------------------------
+# vt_gemm_check: the native acceptance check, no device needed
+# ---------------------------------------------------------------------------
+
+def test_gemm_check_accepts_and_resolves_the_benchmark_configs():
+    assert _lib.gemm_check(8192, 8192, 8192, 8192, 8192, 8192, 8192) == (
+        0, "ok", "mfma_256x256", 0, 0)
+    st, _, v, ks, ws = _lib.gemm_check(16, 14336, 4096, 4096, 14336, 14336, 14336)
+    assert (st, v, ks) == (0, "skinny", 4) and ws == 4 * 16 * 14336 * 4
+    # config 3: shared B folds into one GEMM with stacked M
+    st, _, v, _, ws = _lib.gemm_check(512, 1024, 1024, 1024, 1024, 1024, 1024, batch=64,
+                                      stride_a=512 * 1024, stride_b=0, stride_c=512 * 1024)
+    assert (st, v, ws) == (0, "mfma_256x256", 0)
+    # nothing to compute
+    assert _lib.gemm_check(0, 16, 16, 16, 16, 16, 16)[:3] == (0, "ok", "auto")
+
+
+def test_gemm_check_refusals_carry_the_native_reason():
+    st, reason, *_ = _lib.gemm_check(16, 14336, 4095, 4095, 14336, 14336, 14336, variant="skinny")
+    assert st == _lib.VT_EUNSUPPORTED and "K%16==0" in reason
+    st, reason, *_ = _lib.gemm_check(32, 16, 16, 8, 16, 16, 16)
+    assert st == _lib.VT_EINVAL and "lda" in reason
+    st, reason, *_ = _lib.gemm_check(32, 16, 16, 16, 16, 16, 16, batch=2, stride_c=16)
+    assert st == _lib.VT_EINVAL and "stride_c" in reason
+    st, reason, *_ = _lib.gemm_check(32, 16, 16, 16, 16, 8, 16, has_d=True)
+    assert st == _lib.VT_EINVAL and "ldd" in reason
+    st, reason, *_ = _lib.gemm_check(32, 16, 16, 16, 16, 16, 16, variant="skinny")
+    assert st == _lib.VT_EUNSUPPORTED and "M <= 16" in reason
+
+
+def test_mfma_variant_refuses_rows_too_long_for_tile_offsets():
+    """256 * lda >= 2^32: an explicit MFMA variant refuses (no silent VALU
+    run); auto picks the VALU kernel, and the check says which."""
+    k = 1 << 24
+    for variant in ("mfma_256x256", "mfma_256x128", "mfma_128x128"):
+        st, reason, *_ = _lib.gemm_check(32, 64, k, k, 64, 64, 64, variant=variant)
+        assert st == _lib.VT_EUNSUPPORTED and "256*lda" in reason, variant
+    st, _, chosen, _, _ = _lib.gemm_check(32, 64, k, k, 64, 64, 64)
+    assert st == 0 and chosen == "generic"
+    assert _lib.select_variant(32, 64, k)[0] == "generic"
+    # below the limit the MFMA variants accept rows of any length
+    k = (1 << 24) - 4096
+    assert _lib.gemm_check(32, 64, k, k, 64, 64, 64, variant="mfma_128x128")[0] == 0
+
+
+def test_gemm_check_reports_padded_and_skinny_workspace():
+    # padded: A and B copied with K and N rounded to 16, C copied out
+    st, _, v, _, ws = _lib.gemm_check(1000, 1000, 1000, 1000, 1000, 1000, 1000)
+    assert (st, v) == (0, "padded")
+    r256 = lambda x: -(-x // 256) * 256
+    assert ws == r256(1000 * 1008) + r256(1008 * 1008) + r256(1000 * 1008 * 4)
+    # explicit k_split of the skinny kernel
+    st, _, v, ks, ws = _lib.gemm_check(16, 2048, 4096, 4096, 2048, 2048, 2048, variant="skinny",
+                                       k_split=8)
+    assert (st, v, ks) == (0, "skinny", 8) and ws == 8 * 16 * 2048 * 4
+
+
+def test_select_follows_b_sharing():
+    """The fold into a stacked-M GEMM needs one shared B: with per-batch B
+    the selection is the one vt_gemm_i8 makes for unshared batches."""
+    shared = _lib.select_variant(128, 51200, 128, 2, b_shared=True)
+    unshared = _lib.select_variant(128, 51200, 128, 2, b_shared=False)
+    assert shared == ("mfma_256x128", 0) and unshared == ("mfma_256x256", 0)
+    assert _lib.gemm_check(128, 51200, 128, 128, 51200, 51200, 51200, batch=2,
+                           stride_a=128 * 128, stride_b=128 * 51200,
+                           stride_c=128 * 51200)[2] == unshared[0]
+    assert _lib.gemm_check(128, 51200, 128, 128, 51200, 51200, 51200, batch=2,
+                           stride_a=128 * 128, stride_b=0,
+                           stride_c=128 * 51200)[2] == shared[0]
+    assert hg.make_plan(128, 51200, 128, batch=2)["variant"] == unshared[0]
+    assert hg.make_plan(128, 51200, 128, batch=2, b_shared=True)["variant"] == shared[0]
+    lib = veritac_amd.load_library()
+    v, ks = ctypes.c_int32(), ctypes.c_int32()
+    assert lib.vt_gemm_select(16, 16, 16, 1, 16, 16, 4, ctypes.byref(v), ctypes.byref(ks)) \
+        == _lib.VT_EINVAL
+
+
+def test_optimize_candidates_carry_the_native_check():
+    """Each candidate has the reference's keys (backend.py:1083-1085); only
+    valid, accepted candidates are scored; the winner is one of them."""
+    r = hg.optimize(16, 14336, 4096)
+    keys = {"plan", "valid", "invalid_reason", "check", "counts", "objective"}
+    for c in r["candidates"]:
+        assert keys <= set(c)
+        assert set(c["check"]) == {"accepted", "reason"}
+        if c["valid"] and c["check"]["accepted"]:
+            assert c["objective"] is not None and "vt_gemm_check" in c["check"]["reason"]
+        else:
+            assert c["objective"] is None
+    assert r["winner"]["variant"] == "skinny"
+    # a plan the Python validation accepts but the native check refuses
+    plan = dict(hg.make_plan(16, 64, 64), variant="mfma_128x128", k=1 << 24)
+    assert hg.native_check(plan)[0] is False

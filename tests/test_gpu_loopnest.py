@@ -231,6 +231,20 @@ def test_loop_bound_is_reevaluated_every_iteration(dev):
     assert st == 0 and k.info["mapped"] == []
 
 
+def test_iteration_cap_stops_a_thread_and_reports_it(dev):
+    """for (i = 0; i < Y[0]; i++) Y[0] = Y[0] - 1 from 10^6 runs 500000
+    iterations; with a cap of 1000 the thread stops after its 1000th
+    iteration, leaves Y[0] = 10^6 - 1000 and sets STATUS_ITERATIONS."""
+    stmt = {"tag": "loop", "var": "i", "lo": lit(0), "hi": rd("Y", lit(0)), "ann": "none",
+            "body": wr("Y", [lit(0)], {"tag": "add", "left": rd("Y", lit(0)), "right": lit(-1)})}
+    k = ln.LoopNestKernel(stmt, {"Y": {"dtype": "int32", "shape": (1,)}}, max_iterations=1000)
+    y = torch.tensor([10**6], dtype=torch.int32, device=dev)
+    status = k({"Y": y})
+    torch.cuda.synchronize()
+    assert int(status.item()) == ln.STATUS_ITERATIONS
+    assert int(y.item()) == 10**6 - 1000
+
+
 def test_each_store_typed_by_its_own_buffers_and_int64_wraps(dev):
     mul = lambda a, b: {"tag": "mul", "left": a, "right": b}      # noqa: E731
     stmt = {"tag": "seq",

@@ -455,3 +455,50 @@ def test_interpreter_types_each_store_by_its_own_buffers():
     li.run(loop("i", 2, wr("Y", [var("i")], rd("S", rd("X", var("i"))))),
            {"X": x, "S": src, "Y": y}, {"X": (2,), "S": (3,), "Y": (2,)})
     assert y.tolist() == [30, 10]
+
+
+def test_sequential_work_per_thread_is_bounded():
+    """A nest whose threads would run more than the cap of sequential
+    iterations is refused when emitted, with no device involved."""
+    one = {"Y": {"dtype": "int64", "shape": (1,)}}
+    # Y[0] += 1, 2^62 times: no loop is independent, so one thread runs it all
+    runaway = loop("i", 2**62, wr("Y", [lit(0)], add(rd("Y", lit(0)), lit(1))))
+    with pytest.raises(ln.LoopNestError, match="beyond the cap"):
+        ln.emit_kernel(runaway, one)
+    # nested: 2^14 x 2^13 sequential iterations exceed 2^26 only through the product
+    nested = loop("i", 2**14, loop("j", 2**13, wr("Y", [lit(0)], add(rd("Y", lit(0)), lit(1)))))
+    with pytest.raises(ln.LoopNestError, match="beyond the cap"):
+        ln.emit_kernel(nested, one)
+    # the reference's largest nest, 1000^3: (i, j) are threads, 1000 per thread
+    info = ln.emit_kernel(ln.matmul_stmt(1000, 1000, 1000),
+                          {"A": {"dtype": "float64", "shape": (1000, 1000)},
+                           "B": {"dtype": "float64", "shape": (1000, 1000)},
+                           "C": {"dtype": "float64", "shape": (1000, 1000)}}, layout="reference")
+    assert ln.thread_iterations(ln.parse_stmt(ln.matmul_stmt(1000, 1000, 1000)),
+                                set(info["mapped"]), ln._var_ranges(
+                                    ln.parse_stmt(ln.matmul_stmt(1000, 1000, 1000)), {})) == 1000
+    assert "vt_iters" not in info["source"]
+    # a triangular nest is bounded through its outer variable's range
+    tri = loop("i", 3000, {"tag": "loop", "var": "j", "lo": lit(0), "hi": var("i"), "ann": "none",
+                           "body": wr("Y", [lit(0)], add(rd("Y", lit(0)), lit(1)))})
+    assert ln.thread_iterations(ln.parse_stmt(tri), set(), ln._var_ranges(ln.parse_stmt(tri), {})) \
+        == 3000 * (1 + 2999)
+    ln.emit_kernel(tri, one)
+    with pytest.raises(ln.LoopNestError):
+        ln.emit_kernel(tri, one, max_iterations=1000)
+    with pytest.raises(ln.LoopNestError, match="max_iterations"):
+        ln.emit_kernel(tri, one, max_iterations=0)
+
+
+def test_memory_bounds_are_counted_at_run_time():
+    """A bound that reads memory cannot be bounded statically: every
+    sequential loop then counts its iterations against the cap in the
+    emitted kernel, which stops the thread and sets STATUS_ITERATIONS."""
+    stmt = {"tag": "loop", "var": "i", "lo": lit(0), "hi": rd("Y", lit(0)), "ann": "none",
+            "body": wr("Y", [lit(0)], add(rd("Y", lit(0)), lit(-1)))}
+    info = ln.emit_kernel(stmt, {"Y": {"dtype": "int32", "shape": (1,)}}, max_iterations=777)
+    src = info["source"]
+    assert "unsigned long long vt_iters = 0;" in src
+    assert "if (++vt_iters > 777ULL) { atomicOr(vt_status, %d); return; }" \
+        % ln.STATUS_ITERATIONS in src
+    assert any("counted" in n for n in info["notes"])

@@ -14,7 +14,7 @@ import threading
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 DEFAULT_LIB = os.path.join(PKG_DIR, "libvt_hip_gemm.so")
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 VT_OK = 0
 VT_EINVAL = -1
@@ -37,7 +37,7 @@ VARIANT_IDS = {
 VARIANTS = tuple(VARIANT_IDS)
 
 # Every function include/vt_hip_gemm.h declares.
-EXPORTS = ("vt_gemm_i8", "vt_gemm_select", "vt_variant_info", "vt_variant_name",
+EXPORTS = ("vt_gemm_i8", "vt_gemm_check", "vt_gemm_select", "vt_variant_info", "vt_variant_name",
            "vt_last_error", "vt_sync", "vt_device_count", "vt_abi_version", "vt_replay_i8",
            "vt_device_query", "vt_packed_b_size", "vt_pack_b_i8", "vt_gemm_i8_packed",
            "vt_rtc_compile", "vt_rtc_code_size", "vt_rtc_launch", "vt_rtc_release")
@@ -95,6 +95,9 @@ def _declare(lib):
     lib.vt_gemm_i8.argtypes = [p, p, p, p, i64, i64, i64, i64, i64, i64, i64,
                                i64, i64, i64, i64, i64, i32, i32, p]
     lib.vt_gemm_i8.restype = ctypes.c_int
+    lib.vt_gemm_check.argtypes = [i64] * 12 + [i32, i32, i32, pi32, pi32,
+                                                ctypes.POINTER(ctypes.c_int64)]
+    lib.vt_gemm_check.restype = ctypes.c_int
     lib.vt_gemm_select.argtypes = [i64, i64, i64, i64, i64, i64, i32, pi32, pi32]
     lib.vt_gemm_select.restype = ctypes.c_int
     lib.vt_variant_info.argtypes = [i32, pi32, pi32, pi32, pi32, pi32]
@@ -167,15 +170,40 @@ def check(status, what="vt_gemm_i8"):
     return status
 
 
-def select_variant(m, n, k, batch=1, lda=None, ldb=None, aligned=True):
-    """(variant name, k_split) that VT_VARIANT_AUTO launches for this shape."""
+SELECT_ALIGNED, SELECT_B_SHARED = 1, 2   # vt_gemm_select flags
+
+
+def select_variant(m, n, k, batch=1, lda=None, ldb=None, aligned=True, b_shared=False):
+    """(variant name, k_split) that VT_VARIANT_AUTO launches for this shape
+    (contiguous operands; b_shared: one B for every batch)."""
     lib = load_library()
     v, ks = ctypes.c_int32(), ctypes.c_int32()
+    flags = (SELECT_ALIGNED if aligned else 0) | (SELECT_B_SHARED if b_shared else 0)
     check(lib.vt_gemm_select(m, n, k, batch, k if lda is None else lda,
-                             n if ldb is None else ldb, int(bool(aligned)),
+                             n if ldb is None else ldb, flags,
                              ctypes.byref(v), ctypes.byref(ks)), "vt_gemm_select")
     names = {i: nm for nm, i in VARIANT_IDS.items()}
     return names[v.value], ks.value
+
+
+def gemm_check(M, N, K, lda, ldb, ldd, ldc, batch=1, stride_a=0, stride_b=0, stride_d=0,
+               stride_c=0, has_d=False, variant="auto", k_split=0):
+    """vt_gemm_check: (status, reason, variant name, k_split, workspace bytes).
+
+    Never raises for a refusal: status is VT_OK or the VT_E* code vt_gemm_i8
+    would return, reason the native message. Loading the library can raise
+    HipGemmError (the caller decides how to fail closed).
+    """
+    lib = load_library()
+    vid = VARIANT_IDS[variant] if isinstance(variant, str) else int(variant)
+    v, ks, ws = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int64()
+    st = lib.vt_gemm_check(M, N, K, lda, ldb, ldd, ldc, batch, stride_a, stride_b, stride_d,
+                           stride_c, int(bool(has_d)), vid, k_split, ctypes.byref(v),
+                           ctypes.byref(ks), ctypes.byref(ws))
+    if st != VT_OK:
+        return st, last_error(), None, None, None
+    names = {i: nm for nm, i in VARIANT_IDS.items()}
+    return st, "ok", names[v.value], ks.value, ws.value
 
 
 def variant_info(name):

@@ -247,20 +247,22 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma_kernel(GemmArgs p) {
   const int n0 = (within / gm) * BN;
 
   const int M = p.M, N = p.N, K = p.K;
-  const int8_t *Ab = p.A + bidx * p.sa;
-  const int8_t *Bb = p.B + bidx * p.sb;
+  // 64-bit bases at the tile's origin (row m0 of A, column n0 of B), so only
+  // offsets within one tile need 32 bits (the host checks BM*lda and
+  // BK*ldb), whatever the size of the whole matrix.
+  const int8_t *Ab = p.A + bidx * p.sa + (int64_t)m0 * p.lda;
+  const int8_t *Bb = p.B + bidx * p.sb + n0;
 
   // Per-thread global source offsets for one 64-deep k slice, relative to a
-  // wave-uniform base that advances by one slice per step (the host checks
-  // that every offset fits in 32 bits).
+  // wave-uniform base that advances by one slice per step.
   uint32_t a_goff[CA];
   int a_lds[CA], a_k[CA];
 #pragma unroll
   for (int i = 0; i < CA; ++i) {
     const int row = (tid >> 2) + 64 * i, c = tid & 3;
-    int grow = m0 + row;
-    if (EDGE) grow = min(grow, M - 1);
-    a_goff[i] = (uint32_t)((int64_t)grow * p.lda + c * 16);
+    int trow = row;
+    if (EDGE) trow = min(m0 + row, M - 1) - m0;
+    a_goff[i] = (uint32_t)((int64_t)trow * p.lda + c * 16);
     a_lds[i] = a_off(row, c);
     a_k[i] = c * 16;
   }
@@ -269,10 +271,10 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma_kernel(GemmArgs p) {
 #pragma unroll
   for (int i = 0; i < CB; ++i) {
     const int row = tid / BCH + (256 / BCH) * i, c = tid % BCH;
-    int col = n0 + c * 16;
-    if (EDGE) col = min(col, N - 16);
+    int tcol = c * 16;
+    if (EDGE) tcol = min(n0 + tcol, N - 16) - n0;
     b_row[i] = row;
-    b_goff[i] = (uint32_t)((int64_t)row * p.ldb + col);
+    b_goff[i] = (uint32_t)((int64_t)row * p.ldb + tcol);
     b_lds[i] = row * BN + ((c ^ b_swz<BCH>(row)) << 4);
   }
 
@@ -1275,9 +1277,13 @@ constexpr int kSkinnyNB = 256, kSkinnyWaves = 16, kSkinnyU = 2;
 constexpr int kMaxReplayLds = 152 * 1024;
 constexpr int kMaxSkinnyLds = 160 * 1024;
 
+// Scratch memory of one call: the K-split partial sums of the decode
+// kernels and the padded variant's operand copies.
+enum ScratchKind { kPartials = 0, kPadded = 1, kScratchKinds = 2 };
+
 struct Workspace {
-  int32_t *partials = nullptr;
-  size_t partial_bytes = 0;
+  void *ptr = nullptr;
+  size_t bytes = 0;
 };
 
 struct DeviceState {
@@ -1285,12 +1291,19 @@ struct DeviceState {
   bool ok = false;
   int num_cus = 256;
   std::string arch;
-  std::map<void *, Workspace> ws;       // per stream: K-split partial sums
-  std::map<void *, Workspace> pad_ws;   // per stream: zero-padded operand copies
+  hipError_t attr_err = hipSuccess;   // dynamic-LDS limits, set once on this device
+  std::map<void *, Workspace> ws[kScratchKinds];   // per stream, per kind
+  // Workspaces superseded by larger ones. They are never freed: a HIP graph
+  // captured earlier may still hold their addresses, and a host thread may
+  // still be launching with one.
+  std::vector<void *> retired;
+  int8_t *scratch = nullptr;   // this device's address of the static scratch array
 };
 
 std::mutex g_mu;
 std::map<int, DeviceState> g_dev;
+
+void set_kernel_attributes(DeviceState &st);
 
 int current_device(int *dev_out, DeviceState **st_out) {
   int count = 0;
@@ -1307,36 +1320,73 @@ int current_device(int *dev_out, DeviceState **st_out) {
     st.arch = prop.gcnArchName;
     st.num_cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
     st.ok = strncmp(prop.gcnArchName, "gfx950", 6) == 0;
+    // Kernel attributes belong to a device: set them here, once per device,
+    // with that device current.
+    if (st.ok) set_kernel_attributes(st);
     st.probed = true;
   }
   if (!st.ok)
     return fail(VT_ENODEV, "device %d is %s; this library is built for gfx950", dev,
                 st.arch.c_str());
+  if (st.attr_err != hipSuccess)
+    return fail(VT_EHIP, "hipFuncSetAttribute (dynamic LDS) failed on device %d: %s", dev,
+                hipGetErrorString(st.attr_err));
   *dev_out = dev;
   *st_out = &st;
   return VT_OK;
 }
 
-// Workspace for the skinny kernel's K-split partials on (device, stream).
-// Calls on one stream are ordered, so a stream's workspace is never shared by
-// two launches in flight.
-int get_workspace(DeviceState *st, void *stream, size_t partial_bytes, Workspace **out,
-                  bool pad = false) {
+// The library's workspace of one kind on (device, stream). Calls on one
+// stream are ordered, so a stream's workspace is never used by two launches
+// in flight. It only grows, at least doubling, and is allocated outside
+// stream capture only: a call that needs more than the stream has while the
+// stream is being captured is refused (run it once before capturing).
+int get_workspace(DeviceState *st, void *stream, ScratchKind kind, size_t bytes, void **out) {
   std::lock_guard<std::mutex> lk(g_mu);
-  Workspace &w = pad ? st->pad_ws[stream] : st->ws[stream];
-  if (w.partial_bytes < partial_bytes) {
-    if (w.partials) {
-      VT_HIP_CHECK(hipStreamSynchronize((hipStream_t)stream));
-      VT_HIP_CHECK(hipFree(w.partials));
-      w = Workspace();
-    }
-    const size_t pb = partial_bytes > (1u << 20) ? partial_bytes : (1u << 20);
-    VT_HIP_CHECK(hipMalloc((void **)&w.partials, pb));
-    w.partial_bytes = pb;
+  Workspace &w = st->ws[kind][stream];
+  if (w.bytes < bytes) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    VT_HIP_CHECK(hipStreamIsCapturing((hipStream_t)stream, &cs));
+    if (cs != hipStreamCaptureStatusNone)
+      return fail(VT_EUNSUPPORTED,
+                  "this call needs %zu bytes of workspace and the stream, which is being "
+                  "captured, has %zu: make the same call once on this stream before capture",
+                  bytes, w.bytes);
+    size_t nb = bytes > 2 * w.bytes ? bytes : 2 * w.bytes;
+    if (nb < (1u << 20)) nb = 1u << 20;
+    void *p = nullptr;
+    VT_HIP_CHECK(hipMalloc(&p, nb));
+    if (w.ptr) st->retired.push_back(w.ptr);
+    w.ptr = p;
+    w.bytes = nb;
   }
-  *out = &w;
+  *out = w.ptr;
   return VT_OK;
 }
+
+// Where a call's scratch memory comes from: the per-stream workspaces above,
+// or consecutive 256-byte aligned pieces of a fixed device buffer of
+// kScratchBytes.
+constexpr size_t kScratchBytes = (size_t)32 << 20;
+
+struct Scratch {
+  DeviceState *st = nullptr;
+  void *stream = nullptr;
+  int8_t *fixed = nullptr;   // device address of `scratch`, or null
+  size_t used = 0;
+
+  int take(ScratchKind kind, size_t bytes, void **out) {
+    if (!fixed) return get_workspace(st, stream, kind, bytes, out);
+    const size_t need = (bytes + 255) / 256 * 256;
+    if (need > kScratchBytes - used)
+      return fail(VT_EUNSUPPORTED,
+                  "this call needs %zu bytes of scratch and the fixed scratch buffer holds %zu",
+                  used + need, kScratchBytes);
+    *out = fixed + used;
+    used += need;
+    return VT_OK;
+  }
+};
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
@@ -1424,6 +1474,14 @@ bool padded_fits(const Problem &q) {
          q.batch <= 65535;
 }
 
+// The MFMA kernels address A and B from 64-bit bases at each tile's origin
+// plus 32-bit lane offsets within one tile (256 rows of A, 64 rows of B).
+bool mfma_addressable(const Problem &q) {
+  return (__int128)256 * q.lda < (1ll << 32) - 4096 && (__int128)64 * q.ldb < (1ll << 32) - 4096;
+}
+
+int launch_generic(const Problem &q, hipStream_t stream);
+
 int select_variant(const Problem &q, bool vec, int32_t *variant, int32_t *k_split) {
   *k_split = 0;
   if (!vec || q.K == 0) {
@@ -1445,6 +1503,12 @@ int select_variant(const Problem &q, bool vec, int32_t *variant, int32_t *k_spli
     *k_split = choose_k_split(q.N, q.K, q.batch);
     return VT_OK;
   }
+  // Rows too long for the MFMA kernels' tile-relative 32-bit offsets
+  // (lda >= 2^24 bytes) go to the VALU kernel.
+  if (!mfma_addressable(q)) {
+    *variant = VT_VARIANT_GENERIC;
+    return VT_OK;
+  }
   // Batched B-reuse with contiguous batches is one GEMM with stacked M.
   const bool fold = q.batch > 1 && q.sb == 0 && q.sa == q.M * q.lda && q.sc == q.M * q.ldc &&
                     (!q.D || q.sd == q.M * q.ldd);
@@ -1461,15 +1525,6 @@ int select_variant(const Problem &q, bool vec, int32_t *variant, int32_t *k_spli
   return VT_OK;
 }
 
-int launch_generic(const Problem &q, hipStream_t stream);
-
-// The MFMA kernels address A and B with 32-bit lane offsets from a per-slice
-// base: every row offset inside one batch must stay below 2^32.
-bool offsets_fit_32(const Problem &q, int64_t m_rows) {
-  const __int128 a_span = (__int128)m_rows * q.lda;
-  const __int128 b_span = (__int128)q.K * q.ldb;
-  return a_span < (1ll << 32) - 4096 && b_span < (1ll << 32) - 4096;
-}
 
 // Waves per workgroup of the persistent full-tile kernel.
 constexpr int kDmaWaves = 4;
@@ -1497,7 +1552,10 @@ int launch_mfma(const Problem &q, hipStream_t stream, int num_cus) {
     r.M *= r.batch;
     r.batch = 1;
   }
-  if (!offsets_fit_32(r, (r.M + BM - 1) / BM * BM)) return launch_generic(q, stream);
+  if (!mfma_addressable(r))
+    return fail(VT_EUNSUPPORTED,
+                "MFMA variants need 256*lda and 64*ldb below 2^32 (lda=%lld ldb=%lld)",
+                (long long)r.lda, (long long)r.ldb);
   GemmArgs a;
   a.A = r.A; a.B = r.B; a.D = r.D; a.C = r.C;
   a.lda = r.lda; a.ldb = r.ldb; a.ldd = r.ldd; a.ldc = r.ldc;
@@ -1534,15 +1592,20 @@ int launch_mfma(const Problem &q, hipStream_t stream, int num_cus) {
   return VT_OK;
 }
 
+// K slices of the skinny kernel: rows per slice (a multiple of the pipeline
+// length, shrunk until the A part fits in LDS), the split count that gives,
+// and the dynamic LDS bytes.
+struct SkinnyGeom {
+  int64_t chunk, lds;
+  int ks;
+};
+
 template <int NB, int WAVES, int U>
-int launch_skinny_cfg(const Problem &q, int k_split, DeviceState *st, void *stream) {
+SkinnyGeom skinny_geometry(const Problem &q, int k_split) {
   constexpr int R = WAVES * 1024 / NB;           // rows per stage
   constexpr int64_t kAlign = (int64_t)R * U;     // rows per unrolled pipeline
   constexpr int64_t kStageLds = 2 * (int64_t)R * NB;
-  if (q.M > 16) return fail(VT_EUNSUPPORTED, "skinny variant needs M <= 16 (M=%lld)", (long long)q.M);
   if (k_split <= 0) k_split = choose_k_split(q.N, q.K, q.batch);
-  // Slice length: a multiple of the pipeline length; recompute the split
-  // count it implies; shrink slices whose A part would not fit in LDS.
   int64_t chunk = (q.K + k_split - 1) / k_split;
   chunk = (chunk + kAlign - 1) / kAlign * kAlign;
   int64_t lds = 16 * (int64_t)skinny_a_stride((int)chunk) + kStageLds;
@@ -1550,7 +1613,15 @@ int launch_skinny_cfg(const Problem &q, int k_split, DeviceState *st, void *stre
     chunk = ((kMaxSkinnyLds - kStageLds) / 16 - 48) / kAlign * kAlign;
     lds = 16 * (int64_t)skinny_a_stride((int)chunk) + kStageLds;
   }
-  const int ks = (int)((q.K + chunk - 1) / chunk);
+  return SkinnyGeom{chunk, lds, (int)((q.K + chunk - 1) / chunk)};
+}
+
+template <int NB, int WAVES, int U>
+int launch_skinny_cfg(const Problem &q, int k_split, Scratch &scr) {
+  if (q.M > 16) return fail(VT_EUNSUPPORTED, "skinny variant needs M <= 16 (M=%lld)", (long long)q.M);
+  const SkinnyGeom geo = skinny_geometry<NB, WAVES, U>(q, k_split);
+  const int64_t chunk = geo.chunk, lds = geo.lds;
+  const int ks = geo.ks;
   SkinnyArgs a;
   a.A = q.A; a.B = q.B; a.D = q.D; a.C = q.C;
   a.lda = q.lda; a.ldb = q.ldb; a.ldd = q.ldd; a.ldc = q.ldc;
@@ -1563,25 +1634,13 @@ int launch_skinny_cfg(const Problem &q, int k_split, DeviceState *st, void *stre
   if ((int64_t)a.tiles_n * ks > 0x7fffffff || q.batch > 65535)
     return fail(VT_EUNSUPPORTED, "skinny grid too large");
   if (ks > 1) {
-    Workspace *w = nullptr;
+    void *w = nullptr;
     const size_t pbytes = (size_t)q.batch * ks * q.M * q.N * sizeof(int32_t);
-    int rc = get_workspace(st, stream, pbytes, &w);
+    int rc = scr.take(kPartials, pbytes, &w);
     if (rc) return rc;
-    a.ws = w->partials;
+    a.ws = (int32_t *)w;
   }
-  // Allow dynamic LDS up to the per-CU size (once per kernel instantiation).
-  static std::once_flag lds_attr_once;
-  static hipError_t attr_err = hipSuccess;
-  std::call_once(lds_attr_once, [&] {
-    hipError_t e1 = hipFuncSetAttribute((const void *)skinny_kernel<NB, WAVES, U, true>,
-                                        hipFuncAttributeMaxDynamicSharedMemorySize, kMaxSkinnyLds);
-    hipError_t e2 = hipFuncSetAttribute((const void *)skinny_kernel<NB, WAVES, U, false>,
-                                        hipFuncAttributeMaxDynamicSharedMemorySize, kMaxSkinnyLds);
-    attr_err = e1 != hipSuccess ? e1 : e2;
-  });
-  if (attr_err != hipSuccess)
-    return fail(VT_EHIP, "hipFuncSetAttribute(skinny LDS) failed: %s", hipGetErrorString(attr_err));
-  hipStream_t s = (hipStream_t)stream;
+  hipStream_t s = (hipStream_t)scr.stream;
   dim3 grid((unsigned)(a.tiles_n * ks), (unsigned)q.batch), block(64 * WAVES);
   // With a K split the slices write partials and the reduction applies D.
   if (q.D && ks == 1)
@@ -1603,8 +1662,8 @@ int launch_skinny_cfg(const Problem &q, int k_split, DeviceState *st, void *stre
   return VT_OK;
 }
 
-int launch_skinny(const Problem &q, int k_split, DeviceState *st, void *stream) {
-  return launch_skinny_cfg<kSkinnyNB, kSkinnyWaves, kSkinnyU>(q, k_split, st, stream);
+int launch_skinny(const Problem &q, int k_split, Scratch &scr) {
+  return launch_skinny_cfg<kSkinnyNB, kSkinnyWaves, kSkinnyU>(q, k_split, scr);
 }
 
 // Packed-B decode configuration: 4 column blocks (64 columns) per workgroup,
@@ -1644,14 +1703,14 @@ int packed_k_split(int64_t groups, int64_t K) {
 
 // One launch (plus the partial-sum reduction when K is split) over at most
 // 16 rows of A / C / D.
-int launch_packed_rows(const Problem &q, int k_split, DeviceState *st, void *stream) {
+int launch_packed_rows(const Problem &q, int k_split, Scratch &scr) {
   PackedArgs a;
   a.A = q.A; a.Bp = q.B; a.D = q.D; a.C = q.C;
   a.lda = q.lda; a.ldd = q.ldd; a.ldc = q.ldc;
   a.sa = q.sa; a.sbp = q.sb; a.sd = q.sd; a.sc = q.sc;
   a.M = (int)q.M; a.N = (int)q.N; a.K = (int)q.K;
   a.kbt = (int)packed_kbt(q.K);
-  a.hpw = packed_hpw(q.N, q.batch, st->num_cus);
+  a.hpw = packed_hpw(q.N, q.batch, scr.st->num_cus);
   a.groups = (int)((2 * (q.N / 16) + a.hpw - 1) / a.hpw);
   const int ks0 = k_split > 0 ? k_split : packed_k_split((int64_t)a.groups * q.batch, q.K);
   a.kb_per_split = (a.kbt + ks0 - 1) / ks0;
@@ -1660,13 +1719,13 @@ int launch_packed_rows(const Problem &q, int k_split, DeviceState *st, void *str
   if ((int64_t)a.groups * a.k_split > 0x7fffffff || q.batch > 65535)
     return fail(VT_EUNSUPPORTED, "packed grid too large");
   if (a.k_split > 1) {
-    Workspace *w = nullptr;
+    void *w = nullptr;
     const size_t pbytes = (size_t)q.batch * a.k_split * q.M * q.N * sizeof(int32_t);
-    int rc = get_workspace(st, stream, pbytes, &w);
+    int rc = scr.take(kPartials, pbytes, &w);
     if (rc) return rc;
-    a.ws = w->partials;
+    a.ws = (int32_t *)w;
   }
-  hipStream_t s = (hipStream_t)stream;
+  hipStream_t s = (hipStream_t)scr.stream;
   dim3 grid((unsigned)(a.groups * a.k_split), (unsigned)q.batch), block(64 * kPackedWaves);
   const bool d_in = q.D && a.k_split == 1, masked = a.hpw != 2 * kPackedNBW;
   if (d_in && masked)
@@ -1787,8 +1846,7 @@ __global__ __launch_bounds__(256) void unpad_kernel(UnpadArgs p) {
     if (c0 + t < p.N) c[t] = add_wrap(v[t], dv[t]);
 }
 
-int launch_vector(const Problem &q, int32_t variant, int32_t k_split, DeviceState *st,
-                  void *stream);
+int launch_vector(const Problem &q, int32_t variant, int32_t k_split, Scratch &scr);
 
 // A and B copied with K and N rounded up to 16 (zero columns of A meet zero
 // rows of B, so the product is unchanged), multiplied by the kernel the
@@ -1796,28 +1854,91 @@ int launch_vector(const Problem &q, int32_t variant, int32_t k_split, DeviceStat
 // An operand the vector kernels can already read (K, and N for B, multiples
 // of 16, 16-byte aligned base, pitch and batch stride) is used in place, and
 // when N is a multiple of 16 the product writes C (with D) directly.
-int launch_padded(const Problem &q, DeviceState *st, void *stream) {
+// What the padded variant copies: K and N rounded up to 16, the A and B
+// matrices (shared ones once) and, when N is not a multiple of 16, the
+// padded product before its valid columns go out to C.
+struct PaddedLayout {
+  int64_t Kp, Np, bA, bB;
+  bool copy_a, copy_b, copy_c;
+  int64_t a_bytes, b_bytes, c_bytes;   // each rounded up to 256
+};
+
+PaddedLayout padded_layout(const Problem &q) {
+  PaddedLayout L;
+  L.Kp = (q.K + 15) / 16 * 16;
+  L.Np = (q.N + 15) / 16 * 16;
+  L.bA = (q.batch > 1 && q.sa == 0) ? 1 : q.batch;
+  L.bB = (q.batch > 1 && q.sb == 0) ? 1 : q.batch;
+  L.copy_a = L.Kp != q.K || q.lda % 16 || q.sa % 16 || !aligned16(q.A);
+  L.copy_b = L.Kp != q.K || L.Np != q.N || q.ldb % 16 || q.sb % 16 || !aligned16(q.B);
+  L.copy_c = L.Np != q.N;
+  auto round256 = [](int64_t v) { return (v + 255) / 256 * 256; };
+  L.a_bytes = L.copy_a ? round256(L.bA * q.M * L.Kp) : 0;
+  L.b_bytes = L.copy_b ? round256(L.bB * L.Kp * L.Np) : 0;
+  L.c_bytes = L.copy_c ? round256(q.batch * q.M * L.Np * 4) : 0;
+  return L;
+}
+
+// The problem the vector kernels run for the padded variant, with the
+// copies at Ap, Bp, Cp.
+Problem padded_inner(const Problem &q, const PaddedLayout &L, int8_t *Ap, int8_t *Bp,
+                     int32_t *Cp) {
+  Problem g = q;
+  g.N = L.Np;
+  g.K = L.Kp;
+  if (L.copy_a) {
+    g.A = Ap;
+    g.lda = L.Kp;
+    g.sa = L.bA > 1 ? q.M * L.Kp : 0;
+  }
+  if (L.copy_b) {
+    g.B = Bp;
+    g.ldb = L.Np;
+    g.sb = L.bB > 1 ? L.Kp * L.Np : 0;
+  }
+  if (L.copy_c) {
+    g.C = Cp;
+    g.ldc = L.Np;
+    g.sc = q.M * L.Np;
+    g.D = nullptr;
+    g.ldd = L.Np;
+    g.sd = 0;
+  }
+  return g;
+}
+
+// Bytes of scratch a launch of `variant` takes, counted as the fixed
+// scratch buffer hands them out (each piece rounded up to 256).
+int64_t scratch_need(const Problem &q, int32_t variant, int32_t k_split) {
+  auto round256 = [](int64_t v) { return (v + 255) / 256 * 256; };
+  if (variant == VT_VARIANT_SKINNY) {
+    const SkinnyGeom geo = skinny_geometry<kSkinnyNB, kSkinnyWaves, kSkinnyU>(q, k_split);
+    return geo.ks > 1 ? round256(q.batch * geo.ks * q.M * q.N * 4) : 0;
+  }
+  if (variant != VT_VARIANT_PADDED || !padded_fits(q)) return 0;
+  const PaddedLayout L = padded_layout(q);
+  // distinct dummy bases, 16-byte aligned like the copies
+  const Problem g = padded_inner(q, L, (int8_t *)(uintptr_t)256, (int8_t *)(uintptr_t)512,
+                                 (int32_t *)(uintptr_t)768);
+  int32_t v = 0, ks = 0;
+  select_variant(g, true, &v, &ks);
+  return L.a_bytes + L.b_bytes + L.c_bytes + scratch_need(g, v, ks);
+}
+
+int launch_padded(const Problem &q, Scratch &scr) {
   if (!padded_fits(q))
     return fail(VT_EUNSUPPORTED, "padded path needs K > 0, M, N+15, K+15 < 2^30, batch <= 65535");
-  const int64_t Kp = (q.K + 15) / 16 * 16, Np = (q.N + 15) / 16 * 16;
-  const int64_t bA = (q.batch > 1 && q.sa == 0) ? 1 : q.batch;
-  const int64_t bB = (q.batch > 1 && q.sb == 0) ? 1 : q.batch;
-  const bool copy_a = Kp != q.K || q.lda % 16 || q.sa % 16 || !aligned16(q.A);
-  const bool copy_b = Kp != q.K || Np != q.N || q.ldb % 16 || q.sb % 16 || !aligned16(q.B);
-  const bool copy_c = Np != q.N;
-  auto round256 = [](int64_t v) { return (v + 255) / 256 * 256; };
-  const int64_t a_bytes = copy_a ? round256(bA * q.M * Kp) : 0;
-  const int64_t b_bytes = copy_b ? round256(bB * Kp * Np) : 0;
-  const int64_t c_bytes = copy_c ? round256(q.batch * q.M * Np * 4) : 0;
+  const PaddedLayout L = padded_layout(q);
+  const int64_t Kp = L.Kp, Np = L.Np, bA = L.bA, bB = L.bB;
+  const bool copy_a = L.copy_a, copy_b = L.copy_b, copy_c = L.copy_c;
+  const int64_t a_bytes = L.a_bytes, b_bytes = L.b_bytes, c_bytes = L.c_bytes;
   Problem g = q;
-  g.N = Np;
-  g.K = Kp;
-  hipStream_t s = (hipStream_t)stream;
+  hipStream_t s = (hipStream_t)scr.stream;
   if (a_bytes + b_bytes + c_bytes > 0) {
-    Workspace *w = nullptr;
-    int rc = get_workspace(st, stream, (size_t)(a_bytes + b_bytes + c_bytes), &w, true);
+    void *w = nullptr;
+    int rc = scr.take(kPadded, (size_t)(a_bytes + b_bytes + c_bytes), &w);
     if (rc) return rc;
-    int8_t *Ap = (int8_t *)w->partials, *Bp = Ap + a_bytes;
+    int8_t *Ap = (int8_t *)w, *Bp = Ap + a_bytes;
     int32_t *Cp = (int32_t *)(Bp + b_bytes);
     const PadArgs pa = {q.A, Ap, q.lda, bA > 1 ? q.sa : 0, q.M * Kp, q.M, q.K, q.M, Kp, bA};
     const PadArgs pb = {q.B, Bp, q.ldb, bB > 1 ? q.sb : 0, Kp * Np, q.K, q.N, Kp, Np, bB};
@@ -1832,28 +1953,13 @@ int launch_padded(const Problem &q, DeviceState *st, void *stream) {
                          dim3(256), 0, s, copy_a ? pa : pb, pb);
       VT_HIP_CHECK(hipGetLastError());
     }
-    if (copy_a) {
-      g.A = Ap;
-      g.lda = Kp;
-      g.sa = bA > 1 ? q.M * Kp : 0;
-    }
-    if (copy_b) {
-      g.B = Bp;
-      g.ldb = Np;
-      g.sb = bB > 1 ? Kp * Np : 0;
-    }
-    if (copy_c) {
-      g.C = Cp;
-      g.ldc = Np;
-      g.sc = q.M * Np;
-      g.D = nullptr;
-      g.ldd = Np;
-      g.sd = 0;
-    }
+    g = padded_inner(q, L, Ap, Bp, Cp);
+  } else {
+    g = padded_inner(q, L, nullptr, nullptr, nullptr);
   }
   int32_t v = 0, ks = 0;
   select_variant(g, true, &v, &ks);
-  int rc = v == VT_VARIANT_GENERIC ? launch_generic(g, s) : launch_vector(g, v, ks, st, stream);
+  int rc = v == VT_VARIANT_GENERIC ? launch_generic(g, s) : launch_vector(g, v, ks, scr);
   if (rc || !copy_c) return rc;
   UnpadArgs u = {g.C, q.D, q.C, Np, q.ldd, q.ldc, q.M * Np, q.sd, q.sc, q.M, q.N};
   const int64_t cells = q.M * ((q.N + 3) / 4);   // one thread per 4 columns
@@ -1884,15 +1990,115 @@ int launch_generic(const Problem &q, hipStream_t stream) {
 
 
 // The vector variants (operands already checked by vector_ok).
-int launch_vector(const Problem &q, int32_t variant, int32_t k_split, DeviceState *st,
-                  void *stream) {
-  hipStream_t s = (hipStream_t)stream;
+int launch_vector(const Problem &q, int32_t variant, int32_t k_split, Scratch &scr) {
+  hipStream_t s = (hipStream_t)scr.stream;
+  const int cus = scr.st->num_cus;
   switch (variant) {
-    case VT_VARIANT_MFMA_256x256: return launch_mfma<256, 256>(q, s, st->num_cus);
-    case VT_VARIANT_MFMA_128x128: return launch_mfma<128, 128>(q, s, st->num_cus);
-    case VT_VARIANT_MFMA_256x128: return launch_mfma<256, 128>(q, s, st->num_cus);
-    case VT_VARIANT_SKINNY: return launch_skinny(q, k_split, st, stream);
+    case VT_VARIANT_MFMA_256x256: return launch_mfma<256, 256>(q, s, cus);
+    case VT_VARIANT_MFMA_128x128: return launch_mfma<128, 128>(q, s, cus);
+    case VT_VARIANT_MFMA_256x128: return launch_mfma<256, 128>(q, s, cus);
+    case VT_VARIANT_SKINNY: return launch_skinny(q, k_split, scr);
     default: return fail(VT_EINVAL, "variant %d is not a vector variant", (int)variant);
+  }
+}
+
+// One validated vt_gemm_i8 problem and the kernel it runs.
+struct GemmCall {
+  Problem q;
+  int32_t variant = VT_VARIANT_AUTO, k_split = 0;
+  bool empty = false;   // nothing to compute (M, N or batch is 0)
+};
+
+// The host-side checks of vt_gemm_i8, in order, then the variant choice.
+// Nothing here touches the device. With `pointers` false (vt_gemm_check) the
+// operands are taken to be distinct allocations aligned to 16 bytes, as
+// fresh device allocations are.
+int prepare_gemm(const int8_t *A, const int8_t *B, const int32_t *D, int32_t *C, bool has_d,
+                 bool pointers, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                 int64_t ldd, int64_t ldc, int64_t batch, int64_t stride_a, int64_t stride_b,
+                 int64_t stride_d, int64_t stride_c, int32_t variant, int32_t k_split,
+                 const char *who, GemmCall *out) {
+  if (M < 0 || N < 0 || K < 0 || batch < 0)
+    return fail(VT_EINVAL, "negative size (M=%lld N=%lld K=%lld batch=%lld)", (long long)M,
+                (long long)N, (long long)K, (long long)batch);
+  if (variant < 0 || variant >= VT_VARIANT_COUNT)
+    return fail(VT_EINVAL, "unknown variant %d", (int)variant);
+  if (k_split < 0 || k_split > 4096) return fail(VT_EINVAL, "k_split %d out of range", (int)k_split);
+  if (stride_a < 0 || stride_b < 0 || stride_d < 0 || stride_c < 0)
+    return fail(VT_EINVAL, "negative batch stride");
+  if (M > (1ll << 40) || N > (1ll << 40) || K > (1ll << 40) || batch > (1ll << 31))
+    return fail(VT_EINVAL, "size beyond 2^40 (batch beyond 2^31)");
+  if (lda > (1ll << 40) || ldb > (1ll << 40) || ldd > (1ll << 40) || ldc > (1ll << 40) ||
+      stride_a > (1ll << 56) || stride_b > (1ll << 56) || stride_d > (1ll << 56) ||
+      stride_c > (1ll << 56))
+    return fail(VT_EINVAL, "leading dimension beyond 2^40 or batch stride beyond 2^56");
+  out->empty = M == 0 || N == 0 || batch == 0;
+  if (out->empty) return VT_OK;
+  if (pointers && !C) return fail(VT_EINVAL, "C is null");
+  if (pointers && K > 0 && (!A || !B)) return fail(VT_EINVAL, "A or B is null");
+  if (ldc < N) return fail(VT_EINVAL, "ldc=%lld < N=%lld", (long long)ldc, (long long)N);
+  if (K > 0 && lda < K) return fail(VT_EINVAL, "lda=%lld < K=%lld", (long long)lda, (long long)K);
+  if (K > 0 && ldb < N) return fail(VT_EINVAL, "ldb=%lld < N=%lld", (long long)ldb, (long long)N);
+  if (has_d && ldd < N) return fail(VT_EINVAL, "ldd=%lld < N=%lld", (long long)ldd, (long long)N);
+  if (batch > 1 && stride_c != 0 && (__int128)stride_c < (__int128)M * ldc)
+    return fail(VT_EINVAL, "stride_c=%lld overlaps batches (M=%lld rows of ldc=%lld)",
+                (long long)stride_c, (long long)M, (long long)ldc);
+  if (batch > 1 && stride_c == 0) return fail(VT_EINVAL, "stride_c must be nonzero for batch > 1");
+  if (pointers) {
+    if (int rc = check_operand_overlap(A, B, D, C, M, N, K, lda, K, ldb, N, ldd, ldc, batch,
+                                       stride_a, stride_b, stride_d, stride_c, who))
+      return rc;
+  }
+  // Without pointers D stands for a distinct buffer: any non-null marker.
+  const int32_t *d_mark = has_d ? (D ? D : (const int32_t *)(uintptr_t)16) : nullptr;
+  Problem q = {A, B, d_mark, C, M, N, K, lda, ldb, ldd, ldc, batch,
+               stride_a, stride_b, stride_d, stride_c};
+  const bool vec = vector_ok(q);
+  int32_t chosen = variant, ks = k_split;
+  if (variant == VT_VARIANT_AUTO) {
+    select_variant(q, vec, &chosen, &ks);
+    if (k_split > 0) ks = k_split;
+  } else if (variant != VT_VARIANT_GENERIC && variant != VT_VARIANT_PADDED) {
+    if (!vec)
+      return fail(VT_EUNSUPPORTED,
+                  "variant %s needs N%%16==0, K%%16==0 (K>0), lda/ldb/strides multiples of 16 "
+                  "and 16-byte aligned A, B",
+                  kVariants[variant].name);
+    if (variant == VT_VARIANT_SKINNY && M > 16)
+      return fail(VT_EUNSUPPORTED, "variant skinny needs M <= 16 (M=%lld)", (long long)M);
+    if (variant != VT_VARIANT_SKINNY && !mfma_addressable(q))
+      return fail(VT_EUNSUPPORTED,
+                  "variant %s needs 256*lda and 64*ldb below 2^32 (lda=%lld ldb=%lld)",
+                  kVariants[variant].name, (long long)lda, (long long)ldb);
+  }
+  if (chosen != VT_VARIANT_GENERIC && chosen != VT_VARIANT_PADDED && !vec)
+    return fail(VT_EUNSUPPORTED, "internal: vector variant selected for an unaligned problem");
+  if (chosen == VT_VARIANT_PADDED && K == 0) chosen = VT_VARIANT_GENERIC;   // C = D (or 0)
+  if (chosen == VT_VARIANT_PADDED && !padded_fits(q))
+    return fail(VT_EUNSUPPORTED, "padded path needs K > 0, M, N+15, K+15 < 2^30, batch <= 65535");
+  out->q = q;
+  out->variant = chosen;
+  out->k_split = ks;
+  return VT_OK;
+}
+
+int launch_gemm(const GemmCall &c, Scratch &scr) {
+  if (c.variant == VT_VARIANT_GENERIC) return launch_generic(c.q, (hipStream_t)scr.stream);
+  if (c.variant == VT_VARIANT_PADDED) return launch_padded(c.q, scr);
+  return launch_vector(c.q, c.variant, c.k_split, scr);
+}
+
+// Dynamic LDS beyond the default for the kernels that need it.
+void set_kernel_attributes(DeviceState &st) {
+  const std::pair<const void *, int> need[] = {
+      {(const void *)skinny_kernel<kSkinnyNB, kSkinnyWaves, kSkinnyU, true>, kMaxSkinnyLds},
+      {(const void *)skinny_kernel<kSkinnyNB, kSkinnyWaves, kSkinnyU, false>, kMaxSkinnyLds},
+      {(const void *)replay_kernel, kMaxReplayLds + 256},
+  };
+  for (const auto &n : need) {
+    const hipError_t e =
+        hipFuncSetAttribute(n.first, hipFuncAttributeMaxDynamicSharedMemorySize, n.second);
+    if (e != hipSuccess && st.attr_err == hipSuccess) st.attr_err = e;
   }
 }
 
@@ -1927,14 +2133,6 @@ int vt_replay_i8(const int32_t *program, int64_t n_ops, const int8_t *A, const i
   DeviceState *st = nullptr;
   int rc = current_device(&dev, &st);
   if (rc) return rc;
-  static std::once_flag lds_attr_once;
-  static hipError_t attr_err = hipSuccess;
-  std::call_once(lds_attr_once, [&] {
-    attr_err = hipFuncSetAttribute((const void *)replay_kernel,
-                                   hipFuncAttributeMaxDynamicSharedMemorySize, kMaxReplayLds + 256);
-  });
-  if (attr_err != hipSuccess)
-    return fail(VT_EHIP, "hipFuncSetAttribute(replay LDS) failed: %s", hipGetErrorString(attr_err));
   ReplayArgs a;
   a.prog = program;
   a.n_ops = (int)n_ops;
@@ -1974,14 +2172,17 @@ int vt_variant_info(int32_t variant, int32_t *tile_m, int32_t *tile_n, int32_t *
 }
 
 int vt_gemm_select(int64_t M, int64_t N, int64_t K, int64_t batch, int64_t lda, int64_t ldb,
-                   int32_t aligned, int32_t *variant_out, int32_t *k_split_out) {
+                   int32_t flags, int32_t *variant_out, int32_t *k_split_out) {
   if (!variant_out || !k_split_out) return fail(VT_EINVAL, "null output pointer");
   if (M < 0 || N < 0 || K < 0 || batch < 0) return fail(VT_EINVAL, "negative size");
+  if (flags & ~(VT_SELECT_ALIGNED | VT_SELECT_B_SHARED))
+    return fail(VT_EINVAL, "unknown vt_gemm_select flags 0x%x", (unsigned)flags);
   Problem q = {};
   q.M = M; q.N = N; q.K = K; q.batch = batch; q.lda = lda; q.ldb = ldb;
-  q.sa = M * lda; q.sb = 0; q.sc = M * N; q.ldc = N;
-  const bool vec = aligned && q.N % 16 == 0 && q.K % 16 == 0 && q.K > 0 && lda % 16 == 0 &&
-                   ldb % 16 == 0;
+  q.sa = M * lda; q.sc = M * N; q.ldc = N;
+  q.sb = (flags & VT_SELECT_B_SHARED) || batch <= 1 ? 0 : K * ldb;
+  const bool vec = (flags & VT_SELECT_ALIGNED) && q.N % 16 == 0 && q.K % 16 == 0 && q.K > 0 &&
+                   lda % 16 == 0 && ldb % 16 == 0;
   return select_variant(q, vec, variant_out, k_split_out);
 }
 
@@ -2055,63 +2256,40 @@ int vt_gemm_i8(const int8_t *A, const int8_t *B, const int32_t *D, int32_t *C, i
                int64_t batch, int64_t stride_a, int64_t stride_b, int64_t stride_d,
                int64_t stride_c, int32_t variant, int32_t k_split, void *stream) {
   g_err.clear();
-  // ---- host-side validation (never reaches the device on failure) ----
-  if (M < 0 || N < 0 || K < 0 || batch < 0)
-    return fail(VT_EINVAL, "negative size (M=%lld N=%lld K=%lld batch=%lld)", (long long)M,
-                (long long)N, (long long)K, (long long)batch);
-  if (variant < 0 || variant >= VT_VARIANT_COUNT)
-    return fail(VT_EINVAL, "unknown variant %d", (int)variant);
-  if (k_split < 0 || k_split > 4096) return fail(VT_EINVAL, "k_split %d out of range", (int)k_split);
-  if (stride_a < 0 || stride_b < 0 || stride_d < 0 || stride_c < 0)
-    return fail(VT_EINVAL, "negative batch stride");
-  if (M > (1ll << 40) || N > (1ll << 40) || K > (1ll << 40) || batch > (1ll << 31))
-    return fail(VT_EINVAL, "size beyond 2^40 (batch beyond 2^31)");
-  if (lda > (1ll << 40) || ldb > (1ll << 40) || ldd > (1ll << 40) || ldc > (1ll << 40) ||
-      stride_a > (1ll << 56) || stride_b > (1ll << 56) || stride_d > (1ll << 56) ||
-      stride_c > (1ll << 56))
-    return fail(VT_EINVAL, "leading dimension beyond 2^40 or batch stride beyond 2^56");
-  if (M == 0 || N == 0 || batch == 0) return VT_OK;
-  if (!C) return fail(VT_EINVAL, "C is null");
-  if (K > 0 && (!A || !B)) return fail(VT_EINVAL, "A or B is null");
-  if (ldc < N) return fail(VT_EINVAL, "ldc=%lld < N=%lld", (long long)ldc, (long long)N);
-  if (K > 0 && lda < K) return fail(VT_EINVAL, "lda=%lld < K=%lld", (long long)lda, (long long)K);
-  if (K > 0 && ldb < N) return fail(VT_EINVAL, "ldb=%lld < N=%lld", (long long)ldb, (long long)N);
-  if (D && ldd < N) return fail(VT_EINVAL, "ldd=%lld < N=%lld", (long long)ldd, (long long)N);
-  if (batch > 1 && stride_c != 0 && (__int128)stride_c < (__int128)M * ldc)
-    return fail(VT_EINVAL, "stride_c=%lld overlaps batches (M=%lld rows of ldc=%lld)",
-                (long long)stride_c, (long long)M, (long long)ldc);
-  if (batch > 1 && stride_c == 0) return fail(VT_EINVAL, "stride_c must be nonzero for batch > 1");
-  if (int rc = check_operand_overlap(A, B, D, C, M, N, K, lda, K, ldb, N, ldd, ldc, batch,
-                                     stride_a, stride_b, stride_d, stride_c, "vt_gemm_i8"))
-    return rc;
-
-  Problem q = {A, B, D, C, M, N, K, lda, ldb, ldd, ldc, batch,
-               stride_a, stride_b, stride_d, stride_c};
-  const bool vec = vector_ok(q);
-  int32_t chosen = variant, ks = k_split;
-  if (variant == VT_VARIANT_AUTO) {
-    select_variant(q, vec, &chosen, &ks);
-    if (k_split > 0) ks = k_split;
-  } else if (variant != VT_VARIANT_GENERIC && variant != VT_VARIANT_PADDED) {
-    if (!vec)
-      return fail(VT_EUNSUPPORTED,
-                  "variant %s needs N%%16==0, K%%16==0 (K>0), lda/ldb/strides multiples of 16 "
-                  "and 16-byte aligned A, B",
-                  kVariants[variant].name);
-    if (variant == VT_VARIANT_SKINNY && M > 16)
-      return fail(VT_EUNSUPPORTED, "variant skinny needs M <= 16 (M=%lld)", (long long)M);
-  }
-  if (chosen != VT_VARIANT_GENERIC && chosen != VT_VARIANT_PADDED && !vec)
-    return fail(VT_EUNSUPPORTED, "internal: vector variant selected for an unaligned problem");
-  if (chosen == VT_VARIANT_PADDED && K == 0) chosen = VT_VARIANT_GENERIC;   // C = D (or 0)
-
+  GemmCall c;
+  int rc = prepare_gemm(A, B, D, C, D != nullptr, true, M, N, K, lda, ldb, ldd, ldc, batch,
+                        stride_a, stride_b, stride_d, stride_c, variant, k_split, "vt_gemm_i8",
+                        &c);
+  if (rc || c.empty) return rc;
   int dev = 0;
   DeviceState *st = nullptr;
-  int rc = current_device(&dev, &st);
+  rc = current_device(&dev, &st);
   if (rc) return rc;
-  if (chosen == VT_VARIANT_GENERIC) return launch_generic(q, (hipStream_t)stream);
-  if (chosen == VT_VARIANT_PADDED) return launch_padded(q, st, stream);
-  return launch_vector(q, chosen, ks, st, stream);
+  Scratch scr;
+  scr.st = st;
+  scr.stream = stream;
+  return launch_gemm(c, scr);
+}
+
+int vt_gemm_check(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldd,
+                  int64_t ldc, int64_t batch, int64_t stride_a, int64_t stride_b, int64_t stride_d,
+                  int64_t stride_c, int32_t has_d, int32_t variant, int32_t k_split,
+                  int32_t *variant_out, int32_t *k_split_out, int64_t *scratch_bytes_out) {
+  g_err.clear();
+  GemmCall c;
+  int rc = prepare_gemm(nullptr, nullptr, nullptr, nullptr, has_d != 0, false, M, N, K, lda, ldb,
+                        ldd, ldc, batch, stride_a, stride_b, stride_d, stride_c, variant, k_split,
+                        "vt_gemm_check", &c);
+  if (rc) return rc;
+  if (variant_out) *variant_out = c.empty ? VT_VARIANT_AUTO : c.variant;
+  // The K split that launches: the skinny kernel's slice count; the other
+  // variants take none (padded chooses its own for the padded shape).
+  int32_t ks = 0;
+  if (!c.empty && c.variant == VT_VARIANT_SKINNY)
+    ks = skinny_geometry<kSkinnyNB, kSkinnyWaves, kSkinnyU>(c.q, c.k_split).ks;
+  if (k_split_out) *k_split_out = ks;
+  if (scratch_bytes_out) *scratch_bytes_out = c.empty ? 0 : scratch_need(c.q, c.variant, c.k_split);
+  return VT_OK;
 }
 
 int64_t vt_packed_b_size(int64_t K, int64_t N) {
@@ -2206,6 +2384,9 @@ int vt_gemm_i8_packed(const int8_t *A, const int8_t *Bp, const int32_t *D, int32
   int rc = current_device(&dev, &st);
   if (rc) return rc;
   Problem q = {A, Bp, D, C, M, N, K, lda, 0, ldd, ldc, batch, stride_a, stride_bp, stride_d, stride_c};
+  Scratch scr;
+  scr.st = st;
+  scr.stream = stream;
   if (K == 0) return launch_generic(q, (hipStream_t)stream);   // C = D (or 0)
   // Rows in groups of 16: each group streams B once more.
   for (int64_t r0 = 0; r0 < M; r0 += 16) {
@@ -2214,7 +2395,7 @@ int vt_gemm_i8_packed(const int8_t *A, const int8_t *Bp, const int32_t *D, int32
     g.C = C + r0 * ldc;
     g.D = D ? D + r0 * ldd : nullptr;
     g.M = M - r0 < 16 ? M - r0 : 16;
-    rc = launch_packed_rows(g, k_split, st, stream);
+    rc = launch_packed_rows(g, k_split, scr);
     if (rc) return rc;
   }
   return VT_OK;

@@ -186,7 +186,8 @@ def padded_inner_plan(plan):
     shape (vt_gemm_select). D goes to the product when n is a multiple of 16
     (it writes C directly), else it is added while copying C out."""
     n_p, k_p = -(-plan["n"] // DIM) * DIM, -(-plan["k"] // DIM) * DIM
-    name, ks = _lib.select_variant(plan["m"], n_p, k_p, plan["batch"], k_p, n_p, True)
+    name, ks = _lib.select_variant(plan["m"], n_p, k_p, plan["batch"], k_p, n_p, True,
+                                   b_shared=plan["b_shared"])
     d = plan["has_d"] and n_p == plan["n"]
     return dict(plan, n=n_p, k=k_p, variant=name, k_split=ks, has_d=d,
                 d_max_abs=plan["d_max_abs"] if d else 0)
@@ -215,7 +216,7 @@ def make_plan(m, n, k, *, batch=1, b_shared=False, has_d=False, d_max_abs=0,
         if not ok:
             raise HipGemmError("cannot plan: " + reason)
         vec = n % DIM == 0 and k % DIM == 0
-        name, ks = _lib.select_variant(m, n, k, batch, k, n, vec)
+        name, ks = _lib.select_variant(m, n, k, batch, k, n, vec, b_shared=b_shared)
         plan["variant"] = name
         if name == "skinny" and k_split == 0:
             plan["k_split"] = ks
@@ -279,7 +280,11 @@ def validate_plan(plan):
             return False, "variant 'padded' needs m, n+15, k+15 < 2^30 and batch <= 65535"
     elif variant != "generic" and plan["k_split"] != 0:
         return False, "k_split applies to variants 'skinny' and %r only" % PACKED_VARIANT
-    lds, workgroups = required_resources(plan)
+    try:
+        lds, workgroups = required_resources(plan)
+    except HipGemmError as exc:
+        # the padded variant's inner plan comes from the native selection
+        return False, "cannot resolve the %r launch: %s (fail-closed)" % (variant, exc)
     if lds > LDS_PER_CU:
         return False, "LDS %d bytes > %d per CU" % (lds, LDS_PER_CU)
     if workgroups > 2**31 - 1:
@@ -406,6 +411,41 @@ def modeled_objective(plan, counts):
     return (launches * _LAUNCH_S + _ROUND_TRIP_S + t, wgs)
 
 
+def native_check(plan):
+    """The native library's verdict on a valid plan -> (accepted, reason).
+
+    Asks vt_gemm_check whether vt_gemm_i8 accepts the plan's call on
+    contiguous operands (the refusal reasons are the native ones). Fail-closed
+    like the reference's external checker (backend.py:164-196): a library
+    that is missing or cannot load, or a plan with no native counterpart,
+    is a rejection, never an acceptance.
+    """
+    m, n, k, b = plan["m"], plan["n"], plan["k"], plan["batch"]
+    if plan["variant"] == PACKED_VARIANT:
+        if n % DIM or k % DIM:
+            return False, "packed B needs n and k divisible by 16"
+        try:
+            _lib.packed_b_size(k, n)
+        except HipGemmError as exc:
+            return False, "%s (fail-closed)" % exc
+        return True, "accepted: vt_packed_b_size takes k=%d n=%d; runs skinny_packed" % (k, n)
+    sb = 0 if (plan["b_shared"] or b == 1) else k * n
+    multi = b > 1
+    try:
+        st, reason, variant, ks, ws = _lib.gemm_check(
+            m, n, k, k, n, n, n, b, m * k if multi else 0, sb, m * n if multi else 0,
+            m * n if multi else 0, plan["has_d"], plan["variant"], plan["k_split"])
+    except HipGemmError as exc:
+        return False, "native check unavailable: %s (fail-closed)" % exc
+    if st != _lib.VT_OK:
+        return False, "vt_gemm_check: %s (%s)" % (reason, _lib.STATUS_NAMES.get(st, st))
+    if variant != plan["variant"] and plan["variant"] != "auto":
+        return False, ("vt_gemm_check would run %r for a %r plan (fail-closed)"
+                       % (variant, plan["variant"]))
+    return True, "accepted by vt_gemm_check: runs %s (k_split %d, %d bytes of workspace)" % (
+        variant, ks, ws)
+
+
 def gen_candidates(m, n, k, *, batch=1, b_shared=False, has_d=False, d_max_abs=0):
     """One plan per variant (the reference's per-schedule plans, backend.py:1080-1082)."""
     return [make_plan(m, n, k, batch=batch, b_shared=b_shared, has_d=has_d,
@@ -417,29 +457,43 @@ def optimize(m, n, k, *, batch=1, b_shared=False, has_d=False, d_max_abs=0,
     """Validate every variant, score it, pick the least modeled (or measured) time.
 
     Mirrors backend.py:1072-1093: returns {"candidates": [...], "winner": plan}
-    with one entry per variant {plan, valid, invalid_reason, counts, objective}.
-    With measure=True the valid candidates are also timed on the GPU
-    (runner.benchmark_gemm) and the winner is the fastest measured one; the
-    modeled objective is kept alongside.
+    with one entry per variant {plan, valid, invalid_reason,
+    check{accepted, reason}, counts, objective} (plus measured_ms). `check`
+    is the native library's verdict (native_check, fail-closed); only
+    candidates that are valid and accepted are scored and eligible. With
+    measure=True the eligible candidates are also timed on the GPU
+    (runner.benchmark_gemm) and the winner is the fastest one whose measured
+    output was correct (measured_ms, measured_correct); the modeled
+    objective is kept alongside.
     """
     candidates = []
     for plan in gen_candidates(m, n, k, batch=batch, b_shared=b_shared, has_d=has_d,
                                d_max_abs=d_max_abs):
         ok, reason = validate_plan(plan)
-        entry = {"plan": plan, "valid": ok, "invalid_reason": None if ok else reason,
-                 "counts": None, "objective": None, "measured_ms": None}
         if ok:
+            accepted, chk_reason = native_check(plan)
+        else:
+            accepted, chk_reason = False, "not checked: plan invalid (%s)" % reason
+        entry = {"plan": plan, "valid": ok, "invalid_reason": None if ok else reason,
+                 "check": {"accepted": accepted, "reason": chk_reason},
+                 "counts": None, "objective": None, "measured_ms": None,
+                 "measured_correct": None}
+        if ok and accepted:
             counts = modeled_counts(plan)
             entry["counts"] = counts
             entry["objective"] = modeled_objective(plan, counts)
         candidates.append(entry)
-    eligible = [c for c in candidates if c["valid"]]
+    eligible = [c for c in candidates if c["valid"] and c["check"]["accepted"]]
     if measure and eligible:
         from . import runner
         for c in eligible:
-            res = runner.benchmark_gemm(c["plan"], num_runs=num_runs, warmup=2, rotate=False)
+            res = runner.benchmark_gemm(c["plan"], num_runs=num_runs, warmup=2, rotate=False,
+                                        cpu_budget_s=0.05)
             c["measured_ms"] = res["gpu_time_ms"]
-        winner = min(eligible, key=lambda c: c["measured_ms"])["plan"]
+            c["measured_correct"] = res["correct"]
+        # a candidate whose measured output was wrong never wins
+        correct = [c for c in eligible if c["measured_correct"]]
+        winner = min(correct, key=lambda c: c["measured_ms"])["plan"] if correct else None
     else:
         winner = min(eligible, key=lambda c: c["objective"])["plan"] if eligible else None
     return {"candidates": candidates, "winner": winner}

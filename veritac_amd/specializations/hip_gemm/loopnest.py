@@ -57,6 +57,14 @@ least that many elements) and integer division or modulo by zero yields 0;
 either event sets a bit in a status word (STATUS_RANGE, STATUS_DIV0) that
 the call returns, and the offending store is skipped or read is 0.
 
+Bounded work. Each GPU thread runs at most MAX_THREAD_ITERATIONS iterations
+of sequential loops. Where interval arithmetic over the loop bounds gives an
+upper bound on a thread's iterations, a nest above the cap is refused when
+it is emitted. Where it cannot (a bound that reads memory), every
+sequential loop counts its iterations, and a thread that reaches the cap
+stops and sets STATUS_ITERATIONS. A nest therefore cannot hold the GPU
+indefinitely, as an emitted C program on a CPU could run until killed.
+
 Errors raise LoopNestError (a HipGemmError): unknown tags, unknown buffers,
 unbound or shadowing loop variables, shapes that disagree with the index
 count. Nothing falls back to the CPU.
@@ -73,6 +81,11 @@ BLOCK = 256
 REFERENCE_STRIDE = 1000
 STATUS_RANGE = 1   # an index fell outside its buffer
 STATUS_DIV0 = 2    # an integer division or modulo by zero
+STATUS_ITERATIONS = 4   # a thread reached MAX_THREAD_ITERATIONS and stopped
+# Sequential loop iterations one GPU thread may run (about 0.1-1 s of one
+# thread's time); the reference's largest benchmark nest (1000^3, one
+# thread per output cell) runs 1000 per thread.
+MAX_THREAD_ITERATIONS = 1 << 26
 DTYPES = {"int8": "signed char", "int32": "int", "int64": "long long", "float32": "float",
           "float64": "double"}
 FLOAT_DTYPES = ("float32", "float64")
@@ -315,6 +328,38 @@ def _var_ranges(stmt, ranges):
     return ranges
 
 
+def thread_iterations(stmt, mapped_vars, ranges):
+    """Upper bound on the sequential loop iterations one thread runs (mapped
+    loops are the threads themselves), by interval arithmetic over the loop
+    bounds with `ranges` from _var_ranges; None when a bound is not affine or
+    its range is unknown."""
+    kind = stmt[0]
+    if kind == "loop":
+        var, lo, hi, body = stmt[1], stmt[2], stmt[3], stmt[5]
+        inner = thread_iterations(body, mapped_vars, ranges)
+        if inner is None:
+            return None
+        if var in mapped_vars:
+            return inner
+        flo, fhi = _affine(lo), _affine(hi)
+        ilo = None if flo is None else _interval(flo, ranges)
+        ihi = None if fhi is None else _interval(fhi, ranges)
+        if ilo is None or ihi is None:
+            return None
+        return max(0, ihi[1] - ilo[0]) * (1 + inner)
+    if kind == "seq":
+        total = 0
+        for sub in stmt[1]:
+            w = thread_iterations(sub, mapped_vars, ranges)
+            if w is None:
+                return None
+            total += w
+        return total
+    if kind == "alloc":
+        return thread_iterations(stmt[3], mapped_vars, ranges)
+    return 0
+
+
 def _flat_form(buf, idx, buffers, layout):
     """Affine form of the flat cell index of buf[idx], or None."""
     forms = [_affine(i) for i in idx]
@@ -441,6 +486,8 @@ def _walk_notes(stmt, mapped_vars, notes):
 # ---------------------------------------------------------------------------
 
 class _Emitter:
+    guard = None   # cap on each thread's sequential iterations, when counted at run time
+
     def __init__(self, buffers, layout):
         self.buffers = buffers
         self.layout = layout
@@ -520,6 +567,11 @@ class _Emitter:
                 raise LoopNestError("buffer %r is not declared" % b)
         return "double" if any(self.buf_dtype(b) in FLOAT_DTYPES for b in bufs) else "long long"
 
+    def count_iteration(self, depth):
+        if self.guard is not None:
+            self.lines.append("%sif (++vt_iters > %dULL) { atomicOr(vt_status, %d); return; }"
+                              % ("  " * depth, self.guard, STATUS_ITERATIONS))
+
     def stmt(self, s, depth):
         pad = "  " * depth
         kind = s[0]
@@ -543,6 +595,7 @@ class _Emitter:
                 self.lines.append(pad + "#pragma unroll")
             self.lines.append("%sfor (long long %s = %s; %s < %s; ++%s) {"
                               % (pad, var, self.expr_int(lo), var, self.expr_int(hi), var))
+            self.count_iteration(depth + 1)
             self.stmt(body, depth + 1)
             self.lines.append(pad + "}")
         elif kind == "seq":
@@ -641,17 +694,21 @@ def _used(stmt):
     return {buf for buf, _, _ in _accesses(stmt, frozenset(), [])}
 
 
-def emit_kernel(stmt, buffers, name="loopnest", layout="dense"):
+def emit_kernel(stmt, buffers, name="loopnest", layout="dense",
+                max_iterations=MAX_THREAD_ITERATIONS):
     """Lower a parsed (or JSON) loop nest to a HIP kernel.
 
     buffers: {name: {"dtype": one of DTYPES, "shape": (d0, ...)}} for every
     buffer the nest touches (shape is used by layout "dense" and for the
     parameter size checks). Returns a dict: source, kernel name, params (the
     buffer names in parameter order), mapped loops, threads, grid, block and
-    the suppression notes.
+    the suppression notes. `max_iterations` caps each thread's sequential
+    loop iterations (at most MAX_THREAD_ITERATIONS).
     """
     if isinstance(stmt, dict):
         stmt = parse_stmt(stmt)
+    if not (isinstance(max_iterations, int) and 0 < max_iterations <= MAX_THREAD_ITERATIONS):
+        raise LoopNestError("max_iterations must be an integer in [1, %d]" % MAX_THREAD_ITERATIONS)
     if layout not in ("dense", "reference"):
         raise LoopNestError("layout must be 'dense' or 'reference'")
     _name(name, "kernel name")
@@ -666,9 +723,17 @@ def emit_kernel(stmt, buffers, name="loopnest", layout="dense"):
         raise LoopNestError("buffers used but not declared: %s" % missing)
     mapped, notes = plan_mapping(stmt, buffers, layout)
     _walk_notes(stmt, {m[0] for m in mapped}, notes)
+    work = thread_iterations(stmt, {m[0] for m in mapped}, _var_ranges(stmt, {}))
+    if work is not None and work > max_iterations:
+        raise LoopNestError("each GPU thread would run up to %d sequential loop iterations, "
+                            "beyond the cap of %d" % (work, max_iterations))
+    if work is None:
+        notes.append("loop bounds that read memory: each thread's sequential iterations are "
+                     "counted and stop at %d (STATUS_ITERATIONS)" % max_iterations)
     written = _written(stmt)
     params = sorted(b for b in used if b in buffers)
     em = _Emitter(buffers, layout)
+    em.guard = max_iterations if work is None else None
     # peel the mapped loops off the perfect nest
     node, seq_chain = stmt, []
     mapped_vars = {m[0] for m in mapped}
@@ -684,6 +749,8 @@ def emit_kernel(stmt, buffers, name="loopnest", layout="dense"):
     em.lines.append('extern "C" __global__ __launch_bounds__(%d) void %s(%s) {' % (BLOCK, name, sig))
     em.lines.append("  const long long vt_t = (long long)blockIdx.x * %d + threadIdx.x;" % BLOCK)
     em.lines.append("  if (vt_t >= %dLL) return;" % total)
+    if em.guard is not None:
+        em.lines.append("  unsigned long long vt_iters = 0;")
     if mapped:
         em.lines.append("  long long vt_rest = vt_t;")
         for var, lo, ext in reversed(mapped):
@@ -701,6 +768,7 @@ def emit_kernel(stmt, buffers, name="loopnest", layout="dense"):
         em.lines.append("%sfor (long long %s = %s; %s < %s; ++%s) {"
                         % (pad, var, em.expr_int(lo), var, em.expr_int(hi), var))
         depth += 1
+        em.count_iteration(depth)
     em.stmt(inner, depth)
     for d in range(depth - 1, 0, -1):
         em.lines.append("  " * d + "}")
@@ -744,8 +812,10 @@ def _max_index(shape, layout):
 class LoopNestKernel:
     """An emitted loop nest, compiled for gfx950 by hipRTC."""
 
-    def __init__(self, stmt, buffers, name="loopnest", layout="dense"):
-        self.info = emit_kernel(stmt, buffers, name=name, layout=layout)
+    def __init__(self, stmt, buffers, name="loopnest", layout="dense",
+                 max_iterations=MAX_THREAD_ITERATIONS):
+        self.info = emit_kernel(stmt, buffers, name=name, layout=layout,
+                                max_iterations=max_iterations)
         self.buffers = {b: dict(v) for b, v in buffers.items()}
         self.program = _lib.RtcProgram(self.info["source"], self.info["kernel"])
 
@@ -762,7 +832,8 @@ class LoopNestKernel:
         is a raw hipStream_t handle, default torch's current stream; the
         call orders the status word's zeroing before the launch on it.
         Returns the int32 status tensor of the launch (0, or STATUS_RANGE |
-        STATUS_DIV0 bits; read it after the stream has synchronised)."""
+        STATUS_DIV0 | STATUS_ITERATIONS bits; read it after the stream has
+        synchronised)."""
         import torch
         for b in self.info["params"]:
             if b not in tensors:
