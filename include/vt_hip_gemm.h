@@ -121,6 +121,31 @@ int vt_gemm_i8(const int8_t *A, const int8_t *B, const int32_t *D, int32_t *C,
                int32_t variant, int32_t k_split, void *stream);
 
 /*
+ * vt_gemm_i8_noalloc -- vt_gemm_i8 without any allocation.
+ *
+ * No counterpart in the reference. For callers that cannot allocate device
+ * memory during the call: code under HIP graph capture (including a first
+ * call on a stream), tight serving loops, harnesses that forbid hipMalloc.
+ * Same arguments, checks and results as vt_gemm_i8, and it calls no
+ * hipMalloc, hipFree or other allocating routine: the K-split partial sums
+ * and padded copies that vt_gemm_i8 keeps in per-stream workspaces live in
+ * one static device array of VT_NOALLOC_SCRATCH_BYTES (32 MiB) per device,
+ * held until the process ends. A call that needs more (vt_gemm_check
+ * reports the bytes) returns VT_EUNSUPPORTED before anything is launched.
+ * Every call on a device shares that device's array and nothing in it needs
+ * clearing between calls (each call writes all the scratch it reads), so
+ * calls that overlap on one device -- on different streams, or from
+ * different threads without ordering -- race: order them on one stream.
+ */
+#define VT_NOALLOC_SCRATCH_BYTES (32 << 20)
+int vt_gemm_i8_noalloc(const int8_t *A, const int8_t *B, const int32_t *D,
+                       int32_t *C, int64_t M, int64_t N, int64_t K,
+                       int64_t lda, int64_t ldb, int64_t ldd, int64_t ldc,
+                       int64_t batch, int64_t stride_a, int64_t stride_b,
+                       int64_t stride_d, int64_t stride_c,
+                       int32_t variant, int32_t k_split, void *stream);
+
+/*
  * vt_gemm_check -- the host-side acceptance check of vt_gemm_i8, without
  * operands: returns VT_OK when vt_gemm_i8 would accept a call with these
  * sizes, strides, D present or not (has_d), variant and k_split on distinct

@@ -37,7 +37,7 @@ VARIANT_IDS = {
 VARIANTS = tuple(VARIANT_IDS)
 
 # Every function include/vt_hip_gemm.h declares.
-EXPORTS = ("vt_gemm_i8", "vt_gemm_check", "vt_gemm_select", "vt_variant_info", "vt_variant_name",
+EXPORTS = ("vt_gemm_i8", "vt_gemm_i8_noalloc", "vt_gemm_check", "vt_gemm_select", "vt_variant_info", "vt_variant_name",
            "vt_last_error", "vt_sync", "vt_device_count", "vt_abi_version", "vt_replay_i8",
            "vt_device_query", "vt_packed_b_size", "vt_pack_b_i8", "vt_gemm_i8_packed",
            "vt_rtc_compile", "vt_rtc_code_size", "vt_rtc_launch", "vt_rtc_release")
@@ -95,6 +95,8 @@ def _declare(lib):
     lib.vt_gemm_i8.argtypes = [p, p, p, p, i64, i64, i64, i64, i64, i64, i64,
                                i64, i64, i64, i64, i64, i32, i32, p]
     lib.vt_gemm_i8.restype = ctypes.c_int
+    lib.vt_gemm_i8_noalloc.argtypes = lib.vt_gemm_i8.argtypes
+    lib.vt_gemm_i8_noalloc.restype = ctypes.c_int
     lib.vt_gemm_check.argtypes = [i64] * 12 + [i32, i32, i32, pi32, pi32,
                                                 ctypes.POINTER(ctypes.c_int64)]
     lib.vt_gemm_check.restype = ctypes.c_int
@@ -229,6 +231,21 @@ def gemm_raw(A_ptr, B_ptr, D_ptr, C_ptr, M, N, K, lda, ldb, ldd, ldc, batch=1,
     st = lib.vt_gemm_i8(A_ptr, B_ptr, D_ptr, C_ptr, M, N, K, lda, ldb, ldd, ldc, batch,
                         stride_a, stride_b, stride_d, stride_c, vid, k_split, stream)
     return check(st)
+
+
+NOALLOC_SCRATCH_BYTES = 32 << 20   # VT_NOALLOC_SCRATCH_BYTES
+
+
+def gemm_noalloc_raw(A_ptr, B_ptr, D_ptr, C_ptr, M, N, K, lda, ldb, ldd, ldc, batch=1,
+                     stride_a=0, stride_b=0, stride_d=0, stride_c=0, variant="auto",
+                     k_split=0, stream=None):
+    """One vt_gemm_i8_noalloc call (scratch from the static array, no
+    allocation) on raw device pointers; raises on failure."""
+    lib = load_library()
+    vid = VARIANT_IDS[variant] if isinstance(variant, str) else int(variant)
+    st = lib.vt_gemm_i8_noalloc(A_ptr, B_ptr, D_ptr, C_ptr, M, N, K, lda, ldb, ldd, ldc, batch,
+                                stride_a, stride_b, stride_d, stride_c, vid, k_split, stream)
+    return check(st, "vt_gemm_i8_noalloc")
 
 
 def sync(stream=None):

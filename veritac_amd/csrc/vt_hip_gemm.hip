@@ -56,6 +56,13 @@
 
 #include "vt_hip_gemm.h"
 
+// Scratch memory of vt_gemm_i8_noalloc: K-split partial sums and padded
+// operand copies of one call, in consecutive 256-byte aligned pieces. Each
+// device holds its own copy for the life of the process; host code reaches
+// it only through the address hipGetSymbolAddress returns on that device
+// (DeviceState::scratch), never through this name.
+static __device__ __align__(256) int8_t scratch[32 << 20];
+
 typedef int v2i __attribute__((ext_vector_type(2)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
@@ -1298,6 +1305,7 @@ struct DeviceState {
   // still be launching with one.
   std::vector<void *> retired;
   int8_t *scratch = nullptr;   // this device's address of the static scratch array
+  hipError_t scratch_err = hipSuccess;
 };
 
 std::mutex g_mu;
@@ -1320,9 +1328,14 @@ int current_device(int *dev_out, DeviceState **st_out) {
     st.arch = prop.gcnArchName;
     st.num_cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
     st.ok = strncmp(prop.gcnArchName, "gfx950", 6) == 0;
-    // Kernel attributes belong to a device: set them here, once per device,
-    // with that device current.
-    if (st.ok) set_kernel_attributes(st);
+    // Kernel attributes and the address of the static scratch array belong
+    // to a device: set up here, once per device, with that device current.
+    if (st.ok) {
+      set_kernel_attributes(st);
+      void *ptr = nullptr;
+      st.scratch_err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+      st.scratch = st.scratch_err == hipSuccess ? (int8_t *)ptr : nullptr;
+    }
     st.probed = true;
   }
   if (!st.ok)
@@ -1368,6 +1381,7 @@ int get_workspace(DeviceState *st, void *stream, ScratchKind kind, size_t bytes,
 // or consecutive 256-byte aligned pieces of a fixed device buffer of
 // kScratchBytes.
 constexpr size_t kScratchBytes = (size_t)32 << 20;
+static_assert(sizeof(scratch) == kScratchBytes, "the fixed scratch buffer is the static array");
 
 struct Scratch {
   DeviceState *st = nullptr;
@@ -2268,6 +2282,40 @@ int vt_gemm_i8(const int8_t *A, const int8_t *B, const int32_t *D, int32_t *C, i
   Scratch scr;
   scr.st = st;
   scr.stream = stream;
+  return launch_gemm(c, scr);
+}
+
+int vt_gemm_i8_noalloc(const int8_t *A, const int8_t *B, const int32_t *D, int32_t *C,
+                       int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldd,
+                       int64_t ldc, int64_t batch, int64_t stride_a, int64_t stride_b,
+                       int64_t stride_d, int64_t stride_c, int32_t variant, int32_t k_split,
+                       void *stream) {
+  g_err.clear();
+  GemmCall c;
+  int rc = prepare_gemm(A, B, D, C, D != nullptr, true, M, N, K, lda, ldb, ldd, ldc, batch,
+                        stride_a, stride_b, stride_d, stride_c, variant, k_split,
+                        "vt_gemm_i8_noalloc", &c);
+  if (rc || c.empty) return rc;
+  // Refused before anything is launched when the scratch array is too small.
+  const int64_t need = scratch_need(c.q, c.variant, c.k_split);
+  if (need > (int64_t)kScratchBytes)
+    return fail(VT_EUNSUPPORTED,
+                "vt_gemm_i8_noalloc: this call needs %lld bytes of scratch; the static scratch "
+                "array holds %zu (use vt_gemm_i8)",
+                (long long)need, kScratchBytes);
+  int dev = 0;
+  DeviceState *st = nullptr;
+  rc = current_device(&dev, &st);
+  if (rc) return rc;
+  // This device's address of the array, looked up when the device was
+  // first used (each device has its own copy).
+  if (!st->scratch)
+    return fail(VT_EHIP, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                hipGetErrorString(st->scratch_err));
+  Scratch scr;
+  scr.st = st;
+  scr.stream = stream;
+  scr.fixed = st->scratch;
   return launch_gemm(c, scr);
 }
 
