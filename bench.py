@@ -35,6 +35,9 @@ METRIC = "int8 GEMM TOPS @8192³ (% INT8 MFMA peak); HBM GB/s @M=16 decode shape
 PEAK_TOPS = 256 * 2.4e9 * 8192 / 1e12      # dense INT8 MFMA, MI355X datasheet
 PEAK_GBPS = 8000.0                          # HBM3E, MI355X datasheet
 N_SETS = 5
+# Decode input sets: 10 x 58.7 MB = 587 MB, 2.3x the 256 MB Infinity Cache,
+# so each step's B comes from HBM.
+DECODE_SETS = 10
 # HBM bytes per launch from the rocprofv3 FETCH_SIZE / WRITE_SIZE runs kept under
 # profiles/ (FETCH_SIZE scaled by 2.00, WRITE_SIZE by 1.00: the factors a plain
 # 1 GiB copy gives). Update them with the kernels.
@@ -263,8 +266,8 @@ def _loopnest_f64(cref, M, K, N, runs=5):
 def bench_decode(dev, steps, warmup, packed=False, m=16):
     """Decode-shaped GEMM (config 4, M = m of 1 or 16): `steps` launches
     captured in one HIP graph (launch overhead would otherwise dominate a
-    ~10-15 us kernel) and replayed; the launches cycle through 6 buffer sets
-    (> 256 MB).
+    ~10-15 us kernel) and replayed; the launches cycle through DECODE_SETS
+    buffer sets (587 MB, more than twice the 256 MB Infinity Cache).
 
     packed=False: row-major B (vt_gemm_i8, skinny variant). packed=True: the
     same B packed once per set by pack_b (vt_pack_b_i8, timed separately and
@@ -276,7 +279,7 @@ def bench_decode(dev, steps, warmup, packed=False, m=16):
     c = inputs.config_inputs(4, seed=0, m=m)
     A = torch.from_numpy(c["A"]).to(dev)
     B = torch.from_numpy(c["B"]).to(dev)
-    sets = make_sets(dev, A, B, None, (m, 14336), N_SETS + 1)
+    sets = make_sets(dev, A, B, None, (m, 14336), DECODE_SETS)
     stream = torch.cuda.Stream(dev)
     pack_ms = None
     if packed:
