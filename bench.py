@@ -497,6 +497,102 @@ def bench_gemm_operands(dev, steps, warmup):
     return {"workload": "gemm 8192^3 by operand distribution", "steps": steps, "results": out}
 
 
+# Register-only MFMA loop: each wave multiplies 4 A and 4 B fragments of
+# config-5 bytes (16 per lane, straight from the 8192^3 operands) into the same
+# 4 x 4 block of v_mfma_i32_32x32x32_i8 accumulators the GEMM's waves hold,
+# rotating the A fragments every sweep so consecutive sweeps see different
+# data; no memory traffic in the loop. Wave 0 of each workgroup records the
+# core clock counter (s_memtime) and the 100 MHz real-time counter
+# (s_memrealtime) around the loop, which gives the effective clock.
+MFMA_CEILING_SRC = r"""
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+extern "C" __global__ __launch_bounds__(256, 1) void mfma_ceiling(
+    const v4i *a_frags, const v4i *b_frags, int iters, long long *clocks, int *sink) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int slot = (blockIdx.x * 4 + wave) & 255;
+  v4i fa[4], fb[4];
+  for (int i = 0; i < 4; ++i) {
+    fa[i] = a_frags[(slot * 4 + i) * 64 + lane];
+    fb[i] = b_frags[(slot * 4 + i) * 64 + lane];
+  }
+  v16i acc[4][4];
+  for (int a = 0; a < 4; ++a)
+    for (int b = 0; b < 4; ++b)
+      for (int e = 0; e < 16; ++e) acc[a][b][e] = 0;
+  const long long t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+        acc[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[a], fb[b], acc[a][b], 0, 0, 0);
+    const v4i t = fa[0];
+    fa[0] = fa[1]; fa[1] = fa[2]; fa[2] = fa[3]; fa[3] = t;
+  }
+  int sum = 0;
+  for (int a = 0; a < 4; ++a)
+    for (int b = 0; b < 4; ++b)
+      for (int e = 0; e < 16; ++e) sum += acc[a][b][e];
+  const long long t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+  if (wave == 0 && lane == 0) {
+    clocks[blockIdx.x * 2] = t1 - t0;
+    clocks[blockIdx.x * 2 + 1] = r1 - r0;
+  }
+  if (sum == 0x7eadbeef) sink[0] = sum;
+}
+"""
+
+
+def bench_mfma_ceiling(dev, steps, warmup, iters=20000):
+    """The power-limited ceiling of the MFMA pipes on config-5 data: TOPS of
+    a register-only v_mfma_i32_32x32x32_i8 loop (256 workgroups x 4 waves,
+    one per SIMD, the GEMM's 4 x 4 accumulator block per wave) and its
+    effective clock, so the GEMM's roofline fraction can be read against
+    what the board sustains on the same bytes."""
+    import ctypes
+    import numpy as np
+    import torch
+    from veritac_amd import _lib
+    from veritac_amd.specializations.hip_gemm import inputs
+    c = inputs.config_inputs(5, seed=0)
+    # 256 slots x 4 fragments x 64 lanes x 16 bytes from the operands' first rows
+    frag_bytes = 256 * 4 * 64 * 16
+    a_frags = torch.from_numpy(np.ascontiguousarray(c["A"].reshape(-1)[:frag_bytes])).to(dev)
+    b_frags = torch.from_numpy(np.ascontiguousarray(c["B"].reshape(-1)[:frag_bytes])).to(dev)
+    clocks = torch.zeros(256 * 2, dtype=torch.int64, device=dev)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    prog = _lib.RtcProgram(MFMA_CEILING_SRC, "mfma_ceiling")
+    stream = torch.cuda.current_stream(dev)
+    args = [ctypes.c_void_p(a_frags.data_ptr()), ctypes.c_void_p(b_frags.data_ptr()),
+            ctypes.c_int(iters), ctypes.c_void_p(clocks.data_ptr()),
+            ctypes.c_void_p(sink.data_ptr())]
+    for _ in range(warmup):
+        prog.launch((256,), (256,), args, stream.cuda_stream)
+    torch.cuda.synchronize(dev)
+    runs = []
+    for _ in range(steps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        prog.launch((256,), (256,), args, stream.cuda_stream)
+        e1.record(stream)
+        torch.cuda.synchronize(dev)
+        ck = clocks.view(256, 2).cpu().numpy().astype(np.float64)
+        ghz = float(np.median(ck[:, 0] / (ck[:, 1] / 100e6)) / 1e9)
+        runs.append((e0.elapsed_time(e1), ghz))
+    prog.close()
+    ops = 256.0 * 4 * iters * 16 * 2 * 32 * 32 * 32
+    ms = statistics.median(r[0] for r in runs)
+    ghz = statistics.median(r[1] for r in runs)
+    tops = ops / (ms / 1e3) / 1e12
+    return {"workload": "register-only v_mfma_i32_32x32x32_i8 loop on config-5 bytes",
+            "tops": tops, "frac_of_int8_peak": tops / PEAK_TOPS, "kernel_ms": ms,
+            "effective_clock_ghz": ghz,
+            "mfma_utilisation_at_that_clock": tops / (256 * ghz * 8192 / 1e3),
+            "runs": steps, "iters": iters,
+            "timing": "HIP events per launch; clock from s_memtime / s_memrealtime (100 MHz)"}
+
+
 def bench_copy(dev, steps, warmup):
     """A plain 1 GiB device-to-device copy (torch's copy kernel): the known
     byte count against which the profiler's FETCH_SIZE / WRITE_SIZE are scaled."""
@@ -531,11 +627,13 @@ def main():
     ap.add_argument("--provenance", default=None, metavar="PATH",
                     help="write a hash-bound report of the last timed step's result to PATH")
     ap.add_argument("--workload", choices=("all", "gemm", "gemm_d", "decode", "decode_packed",
-                                           "configs", "gemm_operands", "copy", "cpu_paths"),
+                                           "configs", "gemm_operands", "mfma_ceiling", "copy",
+                                           "cpu_paths"),
                     default="all",
                     help="all: the JSON line below; gemm / decode / decode_packed: only that "
                          "kernel (for profiler runs); gemm_d: 8192^3 with an initial partial "
-                         "sum D; copy: a plain 1 GiB device copy "
+                         "sum D; mfma_ceiling: register-only MFMA loop on config-5 bytes "
+                         "(TOPS and effective clock); copy: a plain 1 GiB device copy "
                          "(counter calibration); cpu_paths: the reference's CPU paths on "
                          "every configuration, on this host (no GPU needed)")
     args = ap.parse_args()
@@ -564,6 +662,9 @@ def main():
         res = bench_gemm_d(dev, args.steps, args.warmup)
         print(json.dumps(res), flush=True)
         sys.exit(0 if res["parity"].startswith("exact") else 1)
+    if args.workload == "mfma_ceiling":
+        print(json.dumps(bench_mfma_ceiling(dev, max(3, min(args.steps, 10)), 2)), flush=True)
+        return
     if args.workload == "gemm_operands":
         print(json.dumps(bench_gemm_operands(dev, args.steps, args.warmup)), flush=True)
         return

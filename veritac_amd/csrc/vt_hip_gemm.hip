@@ -773,6 +773,7 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(SkinnyArgs p) {
   constexpr int STAGE_BYTES = R * NB;
   static_assert(KB * NBLK == WAVES && R % 64 == 0, "one MFMA per wave per stage");
   static_assert(NBLK == 16, "skinny_b_swz assumes 256-byte stage rows");
+  static_assert(U % 2 == 0, "stages alternate between two LDS buffers by u & 1");
 
   extern __shared__ __attribute__((aligned(16))) int8_t dsmem[];
   const int a_stride = skinny_a_stride(p.k_chunk);
