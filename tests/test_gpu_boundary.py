@@ -262,3 +262,70 @@ def test_mfma_variants_address_a_beyond_4gib(dev, variant, m):
     del A, C
     torch.cuda.empty_cache()
 
+
+
+# ---------------------------------------------------------------------------
+# Decode K splits: the slices' partial sums and the reduction kernel
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("m,n,k,k_split,with_d,batch", [
+    (1, 14336, 4096, 0, False, 1), (2, 14336, 4096, 0, True, 1), (1, 4112, 2048, 3, True, 1),
+    (2, 1024, 8192, 16, False, 1), (1, 272, 4096, 64, True, 2), (2, 2048, 1024, 7, True, 3)])
+def test_k_split_decode_in_place(dev, m, n, k, k_split, with_d, batch):
+    """C = D + A.B through the skinny kernel with K split across workgroups
+    (in place: C is D), for ragged N, batches and split counts from 3 to 64."""
+    rng = np.random.default_rng(m * 1000 + n + k_split)
+    A = rng.integers(-128, 128, (batch, m, k), dtype=np.int8)
+    B = rng.integers(-128, 128, (batch, k, n), dtype=np.int8)
+    D = rng.integers(-2**20, 2**20, (batch, m, n), dtype=np.int32) if with_d else None
+    plan = hg.make_plan(m, n, k, batch=batch, has_d=with_d, d_max_abs=(1 << 20) if with_d else 0,
+                        variant="skinny", k_split=k_split)
+    assert hg.skinny_split(plan)[0] > 1
+    # the plan's operand shapes: 2-D for one batch, 3-D (B per batch) otherwise
+    lead = (lambda x: x[0]) if batch == 1 else (lambda x: x)
+    At = torch.from_numpy(lead(A)).to(dev)
+    Bt = torch.from_numpy(lead(B)).to(dev)
+    if with_d:
+        C = torch.from_numpy(np.ascontiguousarray(lead(D))).to(dev)
+        out = hg.run(plan, At, Bt, C, out=C)
+    else:
+        out = hg.run(plan, At, Bt, out=torch.full(lead(np.zeros((batch, m, n))).shape, INT32_MIN,
+                                                    dtype=torch.int32, device=dev))
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().reshape(batch, m, n)
+    for b in range(batch):
+        assert np.array_equal(got[b], go.gemm_i8(A[b], B[b], None if D is None else D[b])), b
+
+
+def test_k_split_workspace_shared_by_calls_and_replays(dev):
+    """Two decode calls (different N and K split) share the stream's
+    partial-sum workspace: captured in one graph and replayed with an eager
+    call on the same stream between replays, every replay checked."""
+    s = torch.cuda.Stream(device=dev)
+    cases = []
+    for m, n, k, ks in ((1, 14336, 4096, 4), (2, 3072, 4096, 9)):
+        A, B = rand_i8(dev, (m, k), m + n), rand_i8(dev, (k, n), k + n)
+        plan = hg.make_plan(m, n, k, variant="skinny", k_split=ks)
+        C = torch.empty((m, n), dtype=torch.int32, device=dev)
+        cases.append((plan, A, B, C, go.gemm_i8(A.cpu().numpy(), B.cpu().numpy())))
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        for plan, A, B, C, _ in cases:
+            hg.run(plan, A, B, out=C, stream=s.cuda_stream)
+    s.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for plan, A, B, C, _ in cases:
+            hg.run(plan, A, B, out=C, stream=s.cuda_stream)
+    for i in range(4):
+        for _, _, _, C, _ in cases:
+            C.fill_(INT32_MIN)
+        with torch.cuda.stream(s):
+            g.replay()
+            # an eager call between replays on the same stream and workspace
+            plan, A, B, C, _ = cases[i % 2]
+            hg.run(plan, A, B, out=C, stream=s.cuda_stream)
+            g.replay()
+        s.synchronize()
+        for plan, A, B, C, want in cases:
+            assert np.array_equal(C.cpu().numpy(), want), (i, plan["n"])
