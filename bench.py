@@ -10,7 +10,9 @@ synthetic input already resident in HBM. The timed steps cycle through
 256 MB Infinity Cache. Secondary figures: the M=16 x K=4096 x N=14336 decode
 GEMM (configuration 4) in GB/s of algorithmic traffic, once with row-major B
 and once with B prepacked by vt_pack_b_i8 (the pack is timed on its own and
-is not part of the steps), and the same two at M=1 (secondary_m1).
+is not part of the steps), and the same two at M=1 (secondary_m1). After the
+GEMM, a register-only MFMA loop on the same bytes gives the board's power-limited
+ceiling in that run (mfma_ceiling, roofline.frac_of_measured_ceiling).
 
 Prints ONE JSON line with the metric, the roofline of the dominant kernel
 (average launch duration from HIP events recorded on the launch stream), a
@@ -41,9 +43,9 @@ DECODE_SETS = 10
 # HBM bytes per launch from the rocprofv3 FETCH_SIZE / WRITE_SIZE runs kept under
 # profiles/ (FETCH_SIZE scaled by 2.00, WRITE_SIZE by 1.00: the factors a plain
 # 1 GiB copy gives). Update them with the kernels.
-TRAFFIC_GEMM_8192 = {"read": 805.6e6, "written": 269.9e6}
+TRAFFIC_GEMM_8192 = {"read": 805.6e6, "written": 269.2e6}
 TRAFFIC_DECODE = {  # (packed B, M) -> bytes per step
-    (False, 16): {"read": 58.9e6 + 3.7e6, "written": 3.7e6 + 0.92e6},
+    (False, 16): {"read": 58.9e6 + 3.7e6, "written": 3.95e6 + 0.92e6},
     (True, 16): {"read": 59.3e6, "written": 0.92e6},
     (False, 1): {"read": 58.78e6 + 0.27e6, "written": 0.26e6 + 0.06e6},
     (True, 1): {"read": 58.80e6, "written": 0.06e6},
@@ -753,6 +755,13 @@ def main():
     if args.workload == "gemm":
         print(json.dumps(result), flush=True)
         sys.exit(0 if parity_ok else 1)
+    # The board's own ceiling on the same bytes, measured right after the GEMM
+    # in the same power state: the GEMM's fraction of it separates schedule
+    # losses from the power limit, which moves both by up to 10% between boxes.
+    log("register-only MFMA ceiling")
+    ceiling = bench_mfma_ceiling(dev, 5, 2)
+    result["mfma_ceiling"] = ceiling
+    result["roofline"]["frac_of_measured_ceiling"] = achieved / ceiling["tops"]
     if decode:
         result["secondary"] = decode[(16, False)]
         result["secondary_packed_b"] = decode[(16, True)]
