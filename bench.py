@@ -469,6 +469,76 @@ def bench_gemm_d(dev, steps, warmup):
             "parity": "exact (mod 2^32) on the GPU" if check["passed"] else "MISMATCH"}
 
 
+def bench_gemm_packed(dev, steps, warmup):
+    """Configuration 5 with B prepacked by vt_pack_b_i8: the same 256x256 DMA
+    kernel reading B fragments with ds_read_b128 instead of the transposing
+    ds_read_b64_tr_b8 pair. The pack runs once per set, timed on its own (not
+    part of the steps). Launches alternate in rounds of 5 between row-major and
+    packed B on the same 5 rotated sets, so both see the same power state; HIP
+    events per launch; exact check of both outputs on the GPU."""
+    import torch
+    from veritac_amd.specializations.hip_gemm import backend as hg
+    from veritac_amd.specializations.hip_gemm import inputs
+    from veritac_amd.specializations.hip_gemm import verify
+    c = inputs.config_inputs(5, seed=0)
+    M = N = K = 8192
+    A = torch.from_numpy(c["A"]).to(dev)
+    B = torch.from_numpy(c["B"]).to(dev)
+    plan_r = hg.make_plan(M, N, K)
+    plan_p = hg.make_plan(M, N, K, variant=hg.PACKED_VARIANT)
+    sets = make_sets(dev, A, B, None, (M, N), N_SETS)
+    stream = torch.cuda.current_stream(dev)
+    raw = stream.cuda_stream
+    hg.pack_b(sets[0][1], stream=raw)   # first call loads the kernel; not timed
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    packed = [hg.pack_b(s[1], stream=raw) for s in sets]
+    e1.record(stream)
+    torch.cuda.synchronize()
+    pack_ms = e0.elapsed_time(e1) / len(sets)
+    outs_p = [torch.empty((M, N), dtype=torch.int32, device=dev) for _ in sets]
+    for i in range(warmup):
+        s = i % N_SETS
+        hg.run(plan_r, sets[s][0], sets[s][1], out=sets[s][3], stream=raw)
+        hg.run(plan_p, sets[s][0], packed[s], out=outs_p[s], stream=raw)
+    durs = {"row_major": [], "packed": []}
+    rounds = max(1, steps // 5)
+    for r in range(rounds):
+        for kind in ("row_major", "packed"):
+            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                  for _ in range(5)]
+            for i in range(5):
+                s = (r * 5 + i) % N_SETS
+                ev[i][0].record(stream)
+                if kind == "packed":
+                    hg.run(plan_p, sets[s][0], packed[s], out=outs_p[s], stream=raw)
+                else:
+                    hg.run(plan_r, sets[s][0], sets[s][1], out=sets[s][3], stream=raw)
+                ev[i][1].record(stream)
+            torch.cuda.synchronize()
+            durs[kind] += [a.elapsed_time(b) for a, b in ev]
+    ops = 2.0 * M * N * K
+    res = {"workload": "int8 GEMM M=N=K=8192 (config 5), B prepacked by vt_pack_b_i8 against "
+                       "row-major B, alternating rounds of 5 launches",
+           "pack_ms_per_matrix": pack_ms, "launches_each": len(durs["packed"])}
+    parity = True
+    for kind in ("row_major", "packed"):
+        avg = statistics.mean(durs[kind])
+        res[kind] = {"kernel_avg_ms": avg, "kernel_min_ms": min(durs[kind]),
+                     "kernel_median_ms": statistics.median(durs[kind]),
+                     "tops": ops / (avg / 1e3) / 1e12,
+                     "mfma_frac": ops / (avg / 1e3) / 1e12 / PEAK_TOPS}
+    for s in range(N_SETS):
+        ok_r = verify.exact_check(sets[s][0], sets[s][1], sets[s][3])["passed"]
+        ok_p = verify.exact_check(sets[s][0], sets[s][1], outs_p[s])["passed"]
+        parity = parity and ok_r and ok_p and bool(torch.equal(sets[s][3], outs_p[s]))
+    res["packed_over_row_major"] = res["row_major"]["kernel_avg_ms"] / res["packed"]["kernel_avg_ms"]
+    res["parity"] = ("exact (mod 2^32) on the GPU, both layouts, every set; outputs equal"
+                     if parity else "MISMATCH")
+    return res
+
+
 def bench_gemm_operands(dev, steps, warmup):
     """The 8192^3 kernel over operand distributions that toggle the MFMA
     multipliers less and less: config 5, uniform in [-2, 2), all ones, all
@@ -628,13 +698,15 @@ def main():
     ap.add_argument("--variant", default="auto", help="kernel variant for the headline GEMM")
     ap.add_argument("--provenance", default=None, metavar="PATH",
                     help="write a hash-bound report of the last timed step's result to PATH")
-    ap.add_argument("--workload", choices=("all", "gemm", "gemm_d", "decode", "decode_packed",
+    ap.add_argument("--workload", choices=("all", "gemm", "gemm_d", "gemm_packed", "decode",
+                                           "decode_packed",
                                            "configs", "gemm_operands", "mfma_ceiling", "copy",
                                            "cpu_paths"),
                     default="all",
                     help="all: the JSON line below; gemm / decode / decode_packed: only that "
                          "kernel (for profiler runs); gemm_d: 8192^3 with an initial partial "
-                         "sum D; mfma_ceiling: register-only MFMA loop on config-5 bytes "
+                         "sum D; gemm_packed: 8192^3 with B prepacked against row-major B, "
+                         "alternating; mfma_ceiling: register-only MFMA loop on config-5 bytes "
                          "(TOPS and effective clock); copy: a plain 1 GiB device copy "
                          "(counter calibration); cpu_paths: the reference's CPU paths on "
                          "every configuration, on this host (no GPU needed)")
@@ -662,6 +734,10 @@ def main():
         return
     if args.workload == "gemm_d":
         res = bench_gemm_d(dev, args.steps, args.warmup)
+        print(json.dumps(res), flush=True)
+        sys.exit(0 if res["parity"].startswith("exact") else 1)
+    if args.workload == "gemm_packed":
+        res = bench_gemm_packed(dev, args.steps, args.warmup)
         print(json.dumps(res), flush=True)
         sys.exit(0 if res["parity"].startswith("exact") else 1)
     if args.workload == "mfma_ceiling":

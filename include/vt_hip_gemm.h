@@ -340,12 +340,16 @@ int vt_pack_b_i8(const int8_t *B, int8_t *Bp, int64_t K, int64_t N, int64_t ldb,
  * K % 16 == 0, lda and strides multiples of 16, 16-byte aligned A and Bp.
  * Same extent bounds and overlap refusals as vt_gemm_i8 (Bp counts as
  * batch blocks of vt_packed_b_size bytes; vt_pack_b_i8 likewise refuses a Bp
- * that overlaps B). Any M: rows run in groups of 16, each group streaming B once (the kernel
- * is built for M <= 16). Columns go to workgroups in groups of 8-column
- * half blocks: whole groups of four 16-column blocks when N gives 192 or
- * more of them, else smaller groups, about one per CU. k_split: workgroups
- * along K (0 = automatic: 1 unless even half-block groups are too few, else a
- * split whose partial sums a second kernel adds).
+ * that overlaps B). Any M. When N % 256 == 0, K % 64 == 0 and M >= 256, the
+ * rows in whole 256-row tiles run on the 256x256 MFMA kernel of vt_gemm_i8,
+ * which then reads each 32 x 32 B operand with one ds_read_b128 (a 1 KiB tile
+ * holds 16 consecutive k per lane, the k order of its A operand); the other
+ * rows run in groups of 16, each group streaming B once (that kernel is built
+ * for M <= 16). Columns go to workgroups in groups of 8-column half blocks:
+ * whole groups of four 16-column blocks when N gives 192 or more of them,
+ * else smaller groups, about one per CU. k_split: workgroups along K for the
+ * groups of 16 rows (0 = automatic: 1 unless even half-block groups are too
+ * few, else a split whose partial sums a second kernel adds).
  */
 int vt_gemm_i8_packed(const int8_t *A, const int8_t *Bp, const int32_t *D, int32_t *C,
                       int64_t M, int64_t N, int64_t K,

@@ -18,8 +18,12 @@ import pytest
 
 from veritac_amd import build as vb
 
-KERNELS = ("_ZN12_GLOBAL__N_115gemm_dma_kernelILi4ELb0EEEvNS_8GemmArgsE",
-           "_ZN12_GLOBAL__N_115gemm_dma_kernelILi4ELb1EEEvNS_8GemmArgsE")
+# (mangled name, fragment reads of one 32-deep k step): 4 A blocks plus the
+# lo/hi halves of 4 row-major B blocks, or 4 whole packed B blocks
+KERNELS = {"no_d": ("_ZN12_GLOBAL__N_115gemm_dma_kernelILi4ELb0ELb0EEEvNS_8GemmArgsE", 12),
+           "with_d": ("_ZN12_GLOBAL__N_115gemm_dma_kernelILi4ELb1ELb0EEEvNS_8GemmArgsE", 12),
+           "packed_b": ("_ZN12_GLOBAL__N_115gemm_dma_kernelILi4ELb0ELb1EEEvNS_8GemmArgsE", 8),
+           "packed_b_with_d": ("_ZN12_GLOBAL__N_115gemm_dma_kernelILi4ELb1ELb1EEEvNS_8GemmArgsE", 8)}
 
 
 @pytest.fixture(scope="module")
@@ -41,9 +45,9 @@ def kernel_body(asm, name):
     return asm[start:asm.index("s_endpgm", start)].split("\n")
 
 
-@pytest.mark.parametrize("name", KERNELS, ids=["no_d", "with_d"])
-def test_m0_is_only_written_by_the_dma_sequences(asm, name):
-    body = [l.strip() for l in kernel_body(asm, name)]
+@pytest.mark.parametrize("kind", sorted(KERNELS))
+def test_m0_is_only_written_by_the_dma_sequences(asm, kind):
+    body = [l.strip() for l in kernel_body(asm, KERNELS[kind][0])]
     dmas = 0
     for i, line in enumerate(body):
         if re.search(r"\bm0\b", line):
@@ -57,8 +61,9 @@ def test_m0_is_only_written_by_the_dma_sequences(asm, name):
     assert sum(l.startswith("global_load_lds_dwordx4") for l in body) == dmas
 
 
-@pytest.mark.parametrize("name", KERNELS, ids=["no_d", "with_d"])
-def test_k_loop_waits_are_the_kernels_own(asm, name):
+@pytest.mark.parametrize("kind", sorted(KERNELS))
+def test_k_loop_waits_are_the_kernels_own(asm, kind):
+    name, nunit = KERNELS[kind]
     body = [l.strip() for l in kernel_body(asm, name)]
     first_mfma = next(i for i, l in enumerate(body) if l.startswith("v_mfma"))
     last_mfma = max(i for i, l in enumerate(body) if l.startswith("v_mfma"))
@@ -66,6 +71,6 @@ def test_k_loop_waits_are_the_kernels_own(asm, name):
     end = next(i for i in range(last_mfma, len(body)) if body[i].startswith("s_barrier"))
     loop = body[first_mfma:end + 1]
     # the slice barrier: only slice g+3's 8 DMAs may be in flight, and only
-    # the next step's 12 early fragment reads
-    assert loop[-2:] == ["s_waitcnt vmcnt(8) lgkmcnt(12)", "s_barrier"]
+    # the next step's early fragment reads
+    assert loop[-2:] == ["s_waitcnt vmcnt(8) lgkmcnt(%d)" % nunit, "s_barrier"]
     assert not [l for l in loop if re.match(r"s_waitcnt .*vmcnt\(0\)", l)]

@@ -247,3 +247,66 @@ def test_half_block_groups_across_batches(dev):
     C = hg.run(plan, to_dev(dev, A), hg.pack_b(to_dev(dev, B)), out=out).cpu().numpy()
     for b in range(batch):
         assert np.array_equal(C[b], go.gemm_i8(A[b], B[b])), b
+
+
+# Rows in whole 256-row tiles run on the persistent 256x256 DMA kernel with
+# packed B (N % 256 == 0, K % 64 == 0); the rest in groups of 16 rows.
+@pytest.mark.parametrize("m,k,n", [(256, 64, 256), (512, 192, 768), (300, 128, 512),
+                                   (1024, 1024, 1024), (768, 4160, 256)])
+def test_dma_rows_with_packed_b(dev, m, k, n):
+    say("packed dma", m, k, n)
+    rng = np.random.default_rng(m + 7 * k + n)
+    A = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    B = rng.integers(-128, 128, (k, n), dtype=np.int8)
+    assert np.array_equal(gpu_gemm_packed(dev, A, B), go.gemm_i8_f64(A, B))
+
+
+def test_dma_rows_with_packed_b_d_in_place(dev):
+    m, k, n = 768, 512, 512
+    rng = np.random.default_rng(31)
+    A = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    B = rng.integers(-128, 128, (k, n), dtype=np.int8)
+    D = rng.integers(-2**30, 2**30, (m, n), dtype=np.int32)
+    want = go.gemm_i8(A, B, D)
+    assert np.array_equal(gpu_gemm_packed(dev, A, B, D), want)
+    assert np.array_equal(gpu_gemm_packed(dev, A, B, D, in_place=True), want)
+
+
+def test_dma_rows_with_packed_b_extremes(dev):
+    m, k, n = 256, 8192, 256
+    A = np.full((m, k), -128, np.int8)
+    B = np.full((k, n), -128, np.int8)
+    assert np.all(gpu_gemm_packed(dev, A, B) == 134217728)
+    A = np.tile(np.array([-128, 127], np.int8), (m, k // 2))
+    B = np.tile(np.array([[127], [-128]], np.int8), (k // 2, n))
+    assert np.array_equal(gpu_gemm_packed(dev, A, B), go.gemm_i8_f64(A, B))
+
+
+@pytest.mark.parametrize("shared", [True, False])
+def test_dma_rows_with_packed_b_batches(dev, shared):
+    rng = np.random.default_rng(41 + shared)
+    batch, m, k, n = 3, 272, 256, 512        # 256 rows per batch on the DMA kernel, 16 in a group
+    A = rng.integers(-128, 128, (batch, m, k), dtype=np.int8)
+    B = rng.integers(-128, 128, (k, n) if shared else (batch, k, n), dtype=np.int8)
+    D = rng.integers(-1000, 1000, (batch, m, n), dtype=np.int32)
+    At, Bt, Dt = to_dev(dev, A), to_dev(dev, B), to_dev(dev, D)
+    plan = hg.make_plan(m, n, k, batch=batch, b_shared=shared, has_d=True, d_max_abs=1000,
+                        variant=hg.PACKED_VARIANT)
+    C = hg.run(plan, At, hg.pack_b(Bt), Dt).cpu().numpy()
+    for b in range(batch):
+        Bb = B if shared else B[b]
+        assert np.array_equal(C[b], go.gemm_i8(A[b], Bb, D[b])), b
+
+
+def test_dma_rows_with_packed_b_equal_row_major_config5_shape(dev):
+    """2048^3 on config-5-like data: packed B and row-major B give the same
+    full output, which equals the exact float64 product."""
+    n = 2048
+    c = inputs.config_inputs(5, seed=4)
+    A, B = c["A"][:n, :n].copy(), c["B"][:n, :n].copy()
+    At, Bt = to_dev(dev, A), to_dev(dev, B)
+    plan_p = hg.make_plan(n, n, n, variant=hg.PACKED_VARIANT)
+    Cp = hg.run(plan_p, At, hg.pack_b(Bt)).cpu().numpy()
+    Cr = hg.run(hg.make_plan(n, n, n, variant="mfma_256x256"), At, Bt).cpu().numpy()
+    assert np.array_equal(Cp, Cr)
+    assert np.array_equal(Cp, go.gemm_i8_f64(A, B))

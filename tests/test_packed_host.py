@@ -107,6 +107,29 @@ def test_packed_plans_validate():
                for c in hg.optimize(16, 14336, 4096)["candidates"])
 
 
+def test_packed_rows_in_whole_tiles_go_to_the_256_kernel():
+    """Rows in whole 256-row tiles run on the 256x256 kernel when n % 256 == 0
+    and k % 64 == 0; the rest in groups of 16 (the split packed_dma_fits makes
+    in the library)."""
+    plan = lambda m, n, k, **kw: hg.make_plan(m, n, k, variant=hg.PACKED_VARIANT, **kw)
+    assert hg.packed_dma_rows(plan(8192, 8192, 8192)) == 8192
+    assert hg.packed_dma_rows(plan(300, 512, 128)) == 256
+    assert hg.packed_dma_rows(plan(255, 512, 128)) == 0
+    assert hg.packed_dma_rows(plan(512, 272, 128)) == 0      # n not whole 256 tiles
+    assert hg.packed_dma_rows(plan(512, 512, 80)) == 0       # k not whole 64 slices
+    # 16 column blocks of kbt 1 KiB tiles must stay within 32-bit lane offsets
+    assert hg.packed_dma_rows(plan(256, 256, 64 * 262143)) == 256
+    assert hg.packed_dma_rows(plan(256, 256, 64 * 262144)) == 0
+    p = plan(300, 512, 128)
+    assert hg.required_resources(p) == (hg.DMA_LDS, 2 + hg.packed_columns(dict(p, m=44))[1] * 3)
+    assert "256 rows on the 256x256 kernel, 44 in groups of 16" in hg.native_check(p)[1]
+    # 8192^3 packed is modeled as the 256x256 kernel, not as 512 row groups
+    big = plan(8192, 8192, 8192)
+    t_packed = hg.modeled_objective(big, hg.modeled_counts(big))[0]
+    row = hg.make_plan(8192, 8192, 8192, variant="mfma_256x256")
+    assert t_packed == pytest.approx(hg.modeled_objective(row, hg.modeled_counts(row))[0])
+
+
 def test_run_refuses_mismatched_packed_operands():
     calls = []
 

@@ -516,7 +516,16 @@ __device__ __forceinline__ void dma_b128(const int8_t *base, uint32_t voff, uint
 // columns of waves), so while one wave of a SIMD waits (a DMA the memory
 // pipeline cannot take yet, a C store burst) the other keeps its MFMA pipe
 // busy; fragment reads per MFMA rise by a third.
-template <int WAVES, bool HAS_D>
+//
+// PACKED_B: B is in the packed layout of vt_pack_b_i8 (p.B = Bp, p.ldb = kbt,
+// the 64-row blocks per 16-column block, p.sb = the packed batch stride). A
+// slice's B is then 16 whole 1 KB tiles, one per 16-column block, each a
+// single DMA of contiguous bytes, and each tile holds lane l's 16 consecutive
+// k of column l % 16 at byte 16 * l. A lane's B operand of the 32x32x32 MFMA
+// (column l % 32, k 16 * (l / 32) .. +15 of the 32-deep step, the same k as
+// its A operand) is one ds_read_b128: two fragment reads per B block fewer
+// than the transposing ds_read_b64_tr_b8 pair that row-major B needs.
+template <int WAVES, bool HAS_D, bool PACKED_B = false>
 __global__ __launch_bounds__(64 * WAVES, 1) void gemm_dma_kernel(GemmArgs p) {
   static_assert(WAVES == 4 || WAVES == 8, "4 or 8 waves");
   constexpr int BM = 256, BN = 256, BK = 64;
@@ -565,20 +574,24 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_dma_kernel(GemmArgs p) {
   const int last_g = ntiles * KT - 1;
 
   // DMA sources. Wave w fills A blocks DPW*w .. DPW*w+DPW-1 (16 rows of 64
-  // bytes each) and the same B blocks (4 rows of 256 bytes each); lane L lands
-  // at byte 16*L of its block, so it fetches the logical chunk that the
-  // swizzle maps to that position (XOR swizzles are their own inverse). Lane
-  // offsets are relative to the tile's origin, which goes into the
-  // wave-uniform base.
+  // bytes each) and the same B blocks (4 rows of 256 bytes each; with packed
+  // B, the 1 KB tiles of 16-column blocks DPW*w ..); lane L lands at byte
+  // 16*L of its block, so it fetches the logical chunk that the swizzle maps
+  // to that position (XOR swizzles are their own inverse). Lane offsets are
+  // relative to the tile's origin, which goes into the wave-uniform base.
   uint32_t a_lane[DPW], b_lane[DPW];
 #pragma unroll
   for (int i = 0; i < DPW; ++i) {
     const int arow = (wave * DPW + i) * 16 + (lane >> 2);
     const int ac = (lane & 3) ^ a_swz(arow);
     a_lane[i] = (uint32_t)((int64_t)arow * lda + ac * 16);
-    const int brow = (wave * DPW + i) * 4 + (lane >> 4);
-    const int bc = (lane & 15) ^ b_swz<BCH>(brow);
-    b_lane[i] = (uint32_t)((int64_t)brow * ldb + bc * 16);
+    if constexpr (PACKED_B) {
+      b_lane[i] = (uint32_t)((int64_t)(wave * DPW + i) * ldb * 1024 + lane * 16);
+    } else {
+      const int brow = (wave * DPW + i) * 4 + (lane >> 4);
+      const int bc = (lane & 15) ^ b_swz<BCH>(brow);
+      b_lane[i] = (uint32_t)((int64_t)brow * ldb + bc * 16);
+    }
   }
   // The slice the next DMA fetches, as (tile iteration, k slice), advanced one
   // slice per DMA round; tile origins are recomputed only at tile changes.
@@ -589,12 +602,12 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_dma_kernel(GemmArgs p) {
     int bidx, m0, n0;
     tile_coords(it, bidx, m0, n0);
     a_tile = p.A + bidx * p.sa + (int64_t)m0 * lda;
-    b_tile = p.B + bidx * p.sb + n0;
+    b_tile = p.B + bidx * p.sb + (PACKED_B ? (int64_t)(n0 / 16) * ldb * 1024 : (int64_t)n0);
   };
   set_tile(0);
   auto next_bases = [&](const int8_t *&abase, const int8_t *&bbase) {
     abase = a_tile + d_kt * BK;
-    bbase = b_tile + (int64_t)(d_kt * BK) * ldb;
+    bbase = b_tile + (PACKED_B ? (int64_t)d_kt * 1024 : (int64_t)(d_kt * BK) * ldb);
     if (d_it * KT + d_kt < last_g) {
       if (++d_kt == KT) {
         d_kt = 0;
@@ -622,9 +635,14 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_dma_kernel(GemmArgs p) {
       a_frag[ks][mi] = a_off(wm * WTM + mi * 32 + (lane & 31), ks * 2 + (lane >> 5));
 #pragma unroll
     for (int ni = 0; ni < NI; ++ni) {
-      const int nc = (wn * WTN + ni * 32) / 16 + (g & 1);
-      const int r0 = ks * 32 + (g >> 1) * 16 + (j >> 1);
-      b_frag[ks][ni] = r0 * BN + ((nc ^ b_swz<BCH>(r0)) << 4) + (j & 1) * 8;
+      if constexpr (PACKED_B) {
+        const int t = (wn * WTN + ni * 32) / 16 + ((lane & 31) >> 4);
+        b_frag[ks][ni] = t * 1024 + (16 * (2 * ks + (lane >> 5)) + (lane & 15)) * 16;
+      } else {
+        const int nc = (wn * WTN + ni * 32) / 16 + (g & 1);
+        const int r0 = ks * 32 + (g >> 1) * 16 + (j >> 1);
+        b_frag[ks][ni] = r0 * BN + ((nc ^ b_swz<BCH>(r0)) << 4) + (j & 1) * 8;
+      }
     }
   }
   v16i acc[MI][NI];
@@ -635,26 +653,31 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_dma_kernel(GemmArgs p) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[mi][ni][e] = 0;
 
-  // Fragments of one 32-deep k step as MI + 2*NI LDS reads ("units"): units
+  // Fragments of one 32-deep k step as MI + BU LDS reads ("units"): units
   // 0..MI-1 are the A blocks (ds_read_b128), the rest the lo/hi halves of the
-  // B blocks (ds_read_b64_tr_b8).
-  constexpr int NUNIT = MI + 2 * NI;
+  // B blocks (ds_read_b64_tr_b8), or with packed B the whole B blocks
+  // (ds_read_b128).
+  constexpr int BU = PACKED_B ? NI : 2 * NI;
+  constexpr int NUNIT = MI + BU;
   static_assert(NUNIT <= 15, "the barrier's lgkmcnt counts one k step of reads");
   v4i fa0[MI], fa1[MI];
-  v2i fl0[NI], fh0[NI], fl1[NI], fh1[NI];
-  auto read_unit = [&](int stage, int ks, int u, v4i *fa, v2i *fl, v2i *fh) {
+  v2i fl0[NI], fh0[NI], fl1[NI], fh1[NI];   // row-major B
+  v4i fb0[NI], fb1[NI];                     // packed B
+  auto read_unit = [&](int stage, int ks, int u, v4i *fa, v2i *fl, v2i *fh, v4i *fb) {
     const int8_t *As = smem + stage * STAGE;
     const int8_t *Bs = As + A_BYTES;
     if (u < MI) {
       fa[u] = ld_lds_b128(As, a_frag[ks][u]);
+    } else if constexpr (PACKED_B) {
+      fb[u - MI] = ld_lds_b128(Bs, b_frag[ks][u - MI]);
     } else {
       const int ni = (u - MI) >> 1;
       if (((u - MI) & 1) == 0) fl[ni] = ld_lds_tr8(Bs, b_frag[ks][ni]);
       else fh[ni] = ld_lds_tr8(Bs, b_frag[ks][ni] + 8 * BN);
     }
   };
-  auto mfma = [&](int mi, int ni, const v4i *fa, const v2i *fl, const v2i *fh) {
-    const v4i b = v4i{fl[ni].x, fl[ni].y, fh[ni].x, fh[ni].y};
+  auto mfma = [&](int mi, int ni, const v4i *fa, const v2i *fl, const v2i *fh, const v4i *fb) {
+    const v4i b = PACKED_B ? fb[ni] : v4i{fl[ni].x, fl[ni].y, fh[ni].x, fh[ni].y};
     acc[mi][ni] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[mi], b, acc[mi][ni], 0, 0, 0);
   };
 
@@ -663,7 +686,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_dma_kernel(GemmArgs p) {
   issue_slice(2);
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" :: "n"(DMAS) : "memory");   // slices 0, 1 landed
 #pragma unroll
-  for (int u = 0; u < NUNIT; ++u) read_unit(0, 0, u, fa0, fl0, fh0);
+  for (int u = 0; u < NUNIT; ++u) read_unit(0, 0, u, fa0, fl0, fh0, fb0);
 
   int gs = 0;   // global slice index
   for (int it = 0; it < ntiles; ++it) {
@@ -691,12 +714,13 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_dma_kernel(GemmArgs p) {
 #pragma unroll
       for (int slot = 0; slot < 2 * MI * NI; ++slot) {
         const int i = slot % (MI * NI);
+        const int u = i == 0 ? 0 : i <= BU ? MI + i - 1 : i - BU;
         if (slot < MI * NI) {
-          mfma(i / NI, i % NI, fa0, fl0, fh0);
-          if (i < NUNIT) read_unit(s0, 1, i == 0 ? 0 : i <= 2 * NI ? MI + i - 1 : i - 2 * NI, fa1, fl1, fh1);
+          mfma(i / NI, i % NI, fa0, fl0, fh0, fb0);
+          if (i < NUNIT) read_unit(s0, 1, u, fa1, fl1, fh1, fb1);
         } else {
-          mfma(i / NI, i % NI, fa1, fl1, fh1);
-          if (i < NUNIT) read_unit(s1, 0, i == 0 ? 0 : i <= 2 * NI ? MI + i - 1 : i - 2 * NI, fa0, fl0, fh0);
+          mfma(i / NI, i % NI, fa1, fl1, fh1, fb1);
+          if (i < NUNIT) read_unit(s1, 0, u, fa0, fl0, fh0, fb0);
         }
         if ((slot & 3) == 2) {
           const int d = slot >> 2;
@@ -1716,6 +1740,36 @@ int packed_k_split(int64_t groups, int64_t K) {
   return (int)ks;
 }
 
+// Whether the rows of a packed-B GEMM in whole 256-row tiles can run on the
+// 256x256 DMA kernel: N in whole 256-column tiles, K in whole 64-deep slices,
+// and every lane offset from a tile's base within 32 bits (A: 256 rows of
+// lda; packed B: 16 column blocks of kbt 1 KB tiles).
+bool packed_dma_fits(const Problem &q) {
+  return q.M >= 256 && q.N % 256 == 0 && q.K % 64 == 0 && q.K > 0 &&
+         256 * q.lda < (1ll << 32) - 4096 && 16 * 1024 * packed_kbt(q.K) < (1ll << 32) - 4096;
+}
+
+// Rows [0, 256 * (M / 256)) of a packed-B GEMM on the persistent 256x256 DMA
+// kernel, every batch in one launch.
+int launch_packed_dma(const Problem &q, hipStream_t stream, int num_cus) {
+  GemmArgs a;
+  a.A = q.A; a.B = q.B; a.D = q.D; a.C = q.C;
+  a.lda = q.lda; a.ldb = packed_kbt(q.K); a.ldd = q.ldd; a.ldc = q.ldc;
+  a.sa = q.sa; a.sb = q.sb; a.sd = q.sd; a.sc = q.sc;
+  a.M = (int)(q.M / 256 * 256); a.N = (int)q.N; a.K = (int)q.K;
+  a.tiles_m = a.M / 256;
+  a.tiles_n = a.N / 256;
+  a.group_m = 4;
+  a.batch_count = (int)q.batch;
+  const int64_t blocks = (int64_t)a.tiles_m * a.tiles_n * q.batch;
+  if (blocks > 0x7fffffff) return fail(VT_EUNSUPPORTED, "grid of %lld tiles too large", (long long)blocks);
+  dim3 pgrid((unsigned)(blocks < num_cus ? blocks : num_cus));
+  if (q.D) hipLaunchKernelGGL((gemm_dma_kernel<kDmaWaves, true, true>), pgrid, dim3(64 * kDmaWaves), 0, stream, a);
+  else hipLaunchKernelGGL((gemm_dma_kernel<kDmaWaves, false, true>), pgrid, dim3(64 * kDmaWaves), 0, stream, a);
+  VT_HIP_CHECK(hipGetLastError());
+  return VT_OK;
+}
+
 // One launch (plus the partial-sum reduction when K is split) over at most
 // 16 rows of A / C / D.
 int launch_packed_rows(const Problem &q, int k_split, Scratch &scr) {
@@ -2437,8 +2491,15 @@ int vt_gemm_i8_packed(const int8_t *A, const int8_t *Bp, const int32_t *D, int32
   scr.st = st;
   scr.stream = stream;
   if (K == 0) return launch_generic(q, (hipStream_t)stream);   // C = D (or 0)
-  // Rows in groups of 16: each group streams B once more.
-  for (int64_t r0 = 0; r0 < M; r0 += 16) {
+  // Whole 256-row tiles on the DMA kernel; the rest in groups of 16 rows, each
+  // of which streams B once more.
+  int64_t r_first = 0;
+  if (packed_dma_fits(q)) {
+    rc = launch_packed_dma(q, (hipStream_t)stream, st->num_cus);
+    if (rc) return rc;
+    r_first = M / 256 * 256;
+  }
+  for (int64_t r0 = r_first; r0 < M; r0 += 16) {
     Problem g = q;
     g.A = A + r0 * lda;
     g.C = C + r0 * ldc;

@@ -66,6 +66,7 @@ TILES = {
     "skinny_packed": (16, 64, 64, 512, 8 * 4 * 1024),
 }
 PACKED_WAVES = 8
+DMA_LDS = 4 * (256 * 64 + 64 * 256)   # LDS of the persistent 256x256 kernel (4 stages)
 SKINNY_MAX_M = 16
 SKINNY_PIPE_ROWS = 64 * 2   # stage rows x stages in flight (kSkinny* in the HIP source)
 LDS_PER_CU = 160 * 1024
@@ -155,6 +156,29 @@ def packed_split(plan):
     return -(-kbt // per), per
 
 
+def packed_dma_rows(plan):
+    """Rows of a skinny_packed plan that run on the 256x256 MFMA kernel: the
+    whole 256-row tiles, when n % 256 == 0, k % 64 == 0 and every lane offset
+    from a tile's base fits 32 bits (contiguous A: 256 * k; packed B: 16
+    column blocks of kbt 1 KiB tiles). The other rows run in groups of 16.
+    Mirrors packed_dma_fits in csrc/vt_hip_gemm.hip."""
+    m, n, k = plan["m"], plan["n"], plan["k"]
+    kbt = -(-k // 64)
+    if (m >= 256 and n % 256 == 0 and k % 64 == 0 and k > 0 and 256 * k < 2**32 - 4096
+            and 16 * 1024 * kbt < 2**32 - 4096):
+        return m // 256 * 256
+    return 0
+
+
+def _packed_parts(plan):
+    """(plan of the rows on the 256x256 kernel or None, plan of the rows in
+    groups of 16 or None) of a skinny_packed plan."""
+    rows = packed_dma_rows(plan)
+    dma = dict(plan, m=rows, variant="mfma_256x256", k_split=0) if rows else None
+    rest = dict(plan, m=plan["m"] - rows) if plan["m"] > rows else None
+    return dma, rest
+
+
 def required_resources(plan):
     """(lds_bytes per workgroup, workgroups) the plan's variant launches.
 
@@ -173,8 +197,15 @@ def required_resources(plan):
         ks, chunk = skinny_split(plan)
         return lds + 16 * skinny_a_stride(chunk), -(-n // tn) * ks * batch
     if variant == PACKED_VARIANT:
-        ks, _ = packed_split(plan)
-        return lds, packed_columns(plan)[1] * ks * batch * -(-m // tm)
+        dma, rest = _packed_parts(plan)
+        lds_out, wgs = 0, 0
+        if dma is not None:
+            lds_out, wgs = DMA_LDS, min(required_resources(dma)[1], NUM_CUS)
+        if rest is not None:
+            ks, _ = packed_split(rest)
+            lds_out = max(lds_out, lds)
+            wgs += packed_columns(rest)[1] * ks * batch * -(-rest["m"] // tm)
+        return lds_out, wgs
     if variant == "padded":
         return required_resources(padded_inner_plan(plan))
     return 0, -(-n // tn) * min(-(-m // tm), 65535) * min(batch, 65535)
@@ -330,12 +361,16 @@ def modeled_counts(plan):
         partial = 2 * 4 * b * m * n * ks if ks > 1 else 0
         l2_bytes = alg + partial + b * -(-n // tn) * 16 * k
     elif variant == PACKED_VARIANT:
-        ks, _ = packed_split(plan)
-        groups = -(-m // 16)
-        partial = 2 * 4 * b * m * n * ks if ks > 1 else 0
-        # B once per 16-row group; each column group reads its A rows once
-        l2_bytes = (groups * (b * -(-k // 64) * 64 * n) + b * m * k * packed_columns(plan)[1]
-                    + 4 * b * m * n * (2 if plan["has_d"] else 1) + partial)
+        dma, rest = _packed_parts(plan)
+        l2_bytes = modeled_counts(dma)["bytes_l2_modeled"] if dma is not None else 0
+        if rest is not None:
+            mr = rest["m"]
+            ks, _ = packed_split(rest)
+            groups = -(-mr // 16)
+            partial = 2 * 4 * b * mr * n * ks if ks > 1 else 0
+            # B once per 16-row group; each column group reads its A rows once
+            l2_bytes += (groups * (b * -(-k // 64) * 64 * n) + b * mr * k * packed_columns(rest)[1]
+                         + 4 * b * mr * n * (2 if plan["has_d"] else 1) + partial)
     elif variant == "padded":
         inner = padded_inner_plan(plan)
         l2_bytes = modeled_counts(inner)["bytes_l2_modeled"] + _padded_copy_bytes(plan, inner)
@@ -387,6 +422,14 @@ def modeled_objective(plan, counts):
         copy_a, copy_b, copy_c = _padded_copies(plan)
         launches = int(copy_a or copy_b) + int(copy_c)
         return (t_inner + _padded_copy_bytes(plan, inner) / PEAK_HBM_BYTES + launches * _LAUNCH_S, wgs)
+    if variant == PACKED_VARIANT and packed_dma_rows(plan):
+        # the 256-row tiles on the 256x256 kernel, then the rest in groups of 16
+        t, wgs = 0.0, 0
+        for part in _packed_parts(plan):
+            if part is not None:
+                tp, wp = modeled_objective(part, modeled_counts(part))
+                t, wgs = t + tp, wgs + wp
+        return t, wgs
     tm, tn = TILES[variant][:2]
     if variant.startswith("mfma") and plan["b_shared"] and b > 1:
         m, b = m * b, 1
@@ -428,7 +471,11 @@ def native_check(plan):
             _lib.packed_b_size(k, n)
         except HipGemmError as exc:
             return False, "%s (fail-closed)" % exc
-        return True, "accepted: vt_packed_b_size takes k=%d n=%d; runs skinny_packed" % (k, n)
+        rows = packed_dma_rows(plan)
+        how = ("%d rows on the 256x256 kernel, %d in groups of 16" % (rows, m - rows) if rows
+               else "rows in groups of 16")
+        return True, "accepted: vt_packed_b_size takes k=%d n=%d; runs skinny_packed (%s)" % (
+            k, n, how)
     sb = 0 if (plan["b_shared"] or b == 1) else k * n
     multi = b > 1
     try:
