@@ -30,6 +30,7 @@ k*16384 + d_max_abs <= 2^31-1 (Plan.lean:86-92 plus the initial partial sum).
 """
 from __future__ import annotations
 
+import hashlib
 import math
 
 from ... import _lib
@@ -452,6 +453,25 @@ def modeled_objective(plan, counts):
     else:
         t = max(t, -(-k // 64) * _SLICE_S)
     return (launches * _LAUNCH_S + _ROUND_TRIP_S + t, wgs)
+
+
+def sha256_file(path):
+    """Hex sha256 of a file's bytes (backend.py:605-610)."""
+    h = hashlib.sha256()
+    with open(path, "rb") as fh:
+        for chunk in iter(lambda: fh.read(65536), b""):
+            h.update(chunk)
+    return h.hexdigest()
+
+
+def emit_c(plan, out_path, *, seed=0x12345678, input_mode="lcg"):
+    """Emit a standalone self-checking C program for the plan (backend.py:817-846):
+    refuses invalid or natively rejected plans, returns {path, sha256, counts}.
+    The program runs the GEMM through the C ABI on the GPU and prints
+    VERITAC_HIP_GEMM_PASS only after every output matched its scalar loop
+    (program.emit_c)."""
+    from .program import emit_c as _emit_c
+    return _emit_c(plan, out_path, seed=seed, input_mode=input_mode)
 
 
 def native_check(plan):
