@@ -569,6 +569,66 @@ def bench_gemm_packed(dev, steps, warmup):
     return res
 
 
+SHAPE_SWEEP = [(m, 14336, 4096) for m in (1, 16, 32, 48, 64, 96, 128, 256)] + \
+    [(m, 4096, 4096) for m in (16, 32, 64, 96, 128, 256, 512)] + \
+    [(128, 1024, 16384), (256, 256, 8192), (2048, 2048, 2048)]
+
+
+def bench_shapes(dev, launches=40):
+    """Weight-shaped GEMMs across M (auto-selected plans; the packed-B path for
+    M <= 256 at N = 14336): per-call time from a HIP graph of `launches` calls
+    over 4 rotated B, median of 5 replays; every output checked exactly on
+    the GPU."""
+    import torch
+    from veritac_amd.specializations.hip_gemm import backend as hg
+    from veritac_amd.specializations.hip_gemm import verify
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    stream = torch.cuda.Stream(dev)
+    rows = []
+    cases = [(m, n, k, False) for m, n, k in SHAPE_SWEEP] + \
+        [(m, 14336, 4096, True) for m in (16, 32, 64, 128, 256)]
+    for m, n, k, packed in cases:
+        A = torch.randint(-128, 128, (m, k), dtype=torch.int8, device=dev, generator=g)
+        Bs = [torch.randint(-128, 128, (k, n), dtype=torch.int8, device=dev, generator=g)
+              for _ in range(4)]
+        plan = hg.make_plan(m, n, k, variant=hg.PACKED_VARIANT if packed else "auto")
+        ops = [hg.pack_b(b) for b in Bs] if packed else Bs
+        Cs = [torch.empty((m, n), dtype=torch.int32, device=dev) for _ in Bs]
+        with torch.cuda.stream(stream):
+            for b, C in zip(ops, Cs):
+                hg.run(plan, A, b, out=C, stream=stream.cuda_stream)
+        stream.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(launches):
+                hg.run(plan, A, ops[i % 4], out=Cs[i % 4], stream=stream.cuda_stream)
+        for _ in range(2):
+            graph.replay()
+        torch.cuda.synchronize()
+        reps = []
+        for _ in range(5):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            cur = torch.cuda.current_stream(dev)
+            e0.record(cur)
+            graph.replay()
+            e1.record(cur)
+            torch.cuda.synchronize()
+            reps.append(e0.elapsed_time(e1) / launches * 1e3)
+        us = statistics.median(reps)
+        exact = all(verify.exact_check(A, b, C)["passed"] for b, C in zip(Bs, Cs))
+        ks = hg.mfma_k_split(plan) if plan["variant"].startswith("mfma") else plan["k_split"]
+        alg = m * k + k * n + 4 * m * n
+        rows.append({"m": m, "n": n, "k": k, "variant": plan["variant"], "k_split": ks,
+                     "us_per_call": us, "tops": 2.0 * m * n * k / us / 1e6,
+                     "gbps_algorithmic": alg / us / 1e3,
+                     "parity": "exact (mod 2^32) on the GPU" if exact else "MISMATCH"})
+        log("shape %dx%dx%d %s: %.2f us" % (m, n, k, plan["variant"], us))
+        del graph
+    return {"workload": "weight-shaped GEMMs across M, HIP graph of %d calls over 4 B" % launches,
+            "shapes": rows}
+
+
 def bench_gemm_operands(dev, steps, warmup):
     """The 8192^3 kernel over operand distributions that toggle the MFMA
     multipliers less and less: config 5, uniform in [-2, 2), all ones, all
@@ -729,14 +789,15 @@ def main():
     ap.add_argument("--provenance", default=None, metavar="PATH",
                     help="write a hash-bound report of the last timed step's result to PATH")
     ap.add_argument("--workload", choices=("all", "gemm", "gemm_d", "gemm_packed", "decode",
-                                           "decode_packed",
+                                           "decode_packed", "shapes",
                                            "configs", "gemm_operands", "mfma_ceiling", "copy",
                                            "cpu_paths"),
                     default="all",
                     help="all: the JSON line below; gemm / decode / decode_packed: only that "
                          "kernel (for profiler runs); gemm_d: 8192^3 with an initial partial "
                          "sum D; gemm_packed: 8192^3 with B prepacked against row-major B, "
-                         "alternating; mfma_ceiling: register-only MFMA loop on config-5 bytes "
+                         "alternating; shapes: weight-shaped GEMMs across M (auto plans); "
+                         "mfma_ceiling: register-only MFMA loop on config-5 bytes "
                          "(TOPS and effective clock); copy: a plain 1 GiB device copy "
                          "(counter calibration); cpu_paths: the reference's CPU paths on "
                          "every configuration, on this host (no GPU needed)")
@@ -772,6 +833,10 @@ def main():
         res = bench_gemm_d(dev, args.steps, args.warmup)
         print(json.dumps(res), flush=True)
         sys.exit(0 if res["parity"].startswith("exact") else 1)
+    if args.workload == "shapes":
+        res = bench_shapes(dev)
+        print(json.dumps(res), flush=True)
+        sys.exit(0 if all(r["parity"].startswith("exact") for r in res["shapes"]) else 1)
     if args.workload == "gemm_packed":
         res = bench_gemm_packed(dev, args.steps, args.warmup)
         print(json.dumps(res), flush=True)

@@ -53,7 +53,7 @@ extern "C" {
 #define VT_VARIANT_MFMA_256x256 1  /* compute-bound: 256x256 tile, 4 waves,
                                       v_mfma_i32_32x32x32_i8                  */
 #define VT_VARIANT_MFMA_128x128 2  /* 128x128 tile, 4 waves, same MFMA        */
-#define VT_VARIANT_SKINNY 3        /* M <= 16 decode shapes: B streamed once,
+#define VT_VARIANT_SKINNY 3        /* M <= 64 decode shapes: B streamed once,
                                       v_mfma_i32_16x16x64_i8, K split         */
 #define VT_VARIANT_GENERIC 4       /* any shape/stride/alignment, VALU        */
 #define VT_VARIANT_MFMA_256x128 5  /* 256x128 tile, 4 waves                   */
@@ -90,9 +90,11 @@ extern "C" {
  * the operands the vector variants cannot read as they are, zero padded, to
  * a workspace the library allocates once per (device, stream) and grows as
  * needed; when N % 16 == 0 the product writes C directly. For aligned
- * shapes VT_VARIANT_AUTO picks VT_VARIANT_SKINNY for M <= 16,
- * VT_VARIANT_GENERIC when K <= 64 and M * N * K * batch <= 2^20 (faster than
- * any MFMA launch there), and an MFMA variant otherwise. The MFMA variants
+ * shapes VT_VARIANT_AUTO picks VT_VARIANT_SKINNY for M <= 16, and for
+ * M <= 64 when K >= 512 and ceil(N / 128) * batch < 256 (the skinny kernel
+ * runs 1, 2 or 4 row blocks of 16 over one stream of B), VT_VARIANT_GENERIC when K <= 64 and
+ * M * N * K * batch <= 2^20 (faster than any MFMA launch there), and an MFMA
+ * variant otherwise. The MFMA variants
  * address each tile from a 64-bit base with 32-bit offsets inside it, so
  * they need 256 * lda and 64 * ldb below 2^32 (K < 2^24 for contiguous A):
  * VT_VARIANT_AUTO picks VT_VARIANT_GENERIC beyond that, and an explicit MFMA
@@ -295,7 +297,7 @@ int vt_device_query(int32_t device, vt_device_info *info, int64_t info_size);
 /*
  * Packed-B decode path.
  *
- * A decode-shaped GEMM (M <= 16 rows of activations against K x N int8
+ * A decode-shaped GEMM (M <= 64 rows of activations against K x N int8
  * weights) is bound by streaming B from HBM once. Row-major B makes the
  * kernel transpose it through LDS and split K across workgroups to reach
  * enough memory parallelism, which costs a second reduction launch. When the
@@ -344,12 +346,12 @@ int vt_pack_b_i8(const int8_t *B, int8_t *Bp, int64_t K, int64_t N, int64_t ldb,
  * rows in whole 256-row tiles run on the 256x256 MFMA kernel of vt_gemm_i8,
  * which then reads each 32 x 32 B operand with one ds_read_b128 (a 1 KiB tile
  * holds 16 consecutive k per lane, the k order of its A operand); the other
- * rows run in groups of 16, each group streaming B once (that kernel is built
- * for M <= 16). Columns go to workgroups in groups of 8-column half blocks:
- * whole groups of four 16-column blocks when N gives 192 or more of them,
- * else smaller groups, about one per CU. k_split: workgroups along K for the
- * groups of 16 rows (0 = automatic: 1 unless even half-block groups are too
- * few, else a split whose partial sums a second kernel adds).
+ * rows run in groups of up to 64, each group streaming B once for its 1, 2 or
+ * 4 row blocks of 16. Columns go to workgroups in groups of 8-column half
+ * blocks: whole groups of four 16-column blocks when N gives 192 or more of
+ * them, else smaller groups, about one per CU. k_split: workgroups along K
+ * for the groups of up to 64 rows (0 = automatic: 1 unless even half-block
+ * groups are too few, else a split whose partial sums a second kernel adds).
  */
 int vt_gemm_i8_packed(const int8_t *A, const int8_t *Bp, const int32_t *D, int32_t *C,
                       int64_t M, int64_t N, int64_t K,

@@ -65,7 +65,8 @@ def test_overflow_bound_boundary():
 def test_variant_specific_rules():
     assert hg.validate_plan(plan(m=1, variant="skinny"))[0]
     assert hg.validate_plan(plan(m=16, variant="skinny", k_split=3))[0]
-    assert not hg.validate_plan(plan(m=17, variant="skinny"))[0]
+    assert hg.validate_plan(plan(m=64, variant="skinny"))[0]     # 4 row blocks of 16
+    assert not hg.validate_plan(plan(m=65, variant="skinny"))[0]
     assert hg.validate_plan(plan(m=5, n=7, k=9, variant="generic"))[0]
     assert not hg.validate_plan(plan(m=5, n=7, k=9, variant="mfma_256x256"))[0]
 
@@ -79,7 +80,7 @@ def test_make_plan_auto_and_optimize():
     names = [c["plan"]["variant"] for c in res["candidates"]]
     assert names == list(hg.VARIANTS)
     skinny = res["candidates"][names.index("skinny")]
-    assert not skinny["valid"] and "m <= 16" in skinny["invalid_reason"]
+    assert not skinny["valid"] and "m <= 64" in skinny["invalid_reason"]
     assert res["winner"]["variant"] == "mfma_256x256"
     res = hg.optimize(16, 14336, 4096)
     assert res["winner"]["variant"] == "skinny"
@@ -92,7 +93,9 @@ def test_modeled_counts_are_consistent():
     c = hg.modeled_counts(p)
     assert c["ops"] == 2 * 64 * 64 * 512 * 1024
     assert c["bytes_algorithmic"] == 64 * 64 * 1024 + 1024 * 512 + 4 * 64 * 64 * 512
-    assert c["workgroups"] == (64 * 64 // 256) * (512 // 256)
+    # 32 tiles of a K of 1024: two K slices of 512
+    assert hg.mfma_k_split(p) == 2
+    assert c["workgroups"] == (64 * 64 // 256) * (512 // 256) * 2
     p = hg.make_plan(256, 256, 256, has_d=True, d_max_abs=1 << 20, variant="mfma_128x128")
     assert hg.modeled_counts(p)["bytes_algorithmic"] == 2 * 65536 + 8 * 65536
 
@@ -209,3 +212,24 @@ def test_padded_plans_take_any_n_and_k():
     assert hg.optimize(1024, 1024, 1024)["winner"]["variant"].startswith("mfma")
     counts = hg.modeled_counts(hg.make_plan(1000, 1000, 1000, has_d=True, d_max_abs=7))
     assert counts["bytes_l2_modeled"] > counts["bytes_algorithmic"]
+
+
+def test_mfma_k_split_mirrors_the_native_choice():
+    """Few long MFMA tiles run as K slices plus a reduction; the plan mirror
+    reports the same split as vt_gemm_check and sizes workgroups with it."""
+    from veritac_amd import _lib
+    for m, n, k in [(128, 14336, 4096), (96, 14336, 4096), (128, 4096, 4096), (256, 4096, 4096),
+                    (512, 4096, 4096), (8192, 8192, 8192), (1024, 14336, 4096), (300, 208, 160),
+                    (128, 4096, 1024), (128, 4096, 1152), (100, 256, 65536)]:
+        plan = hg.make_plan(m, n, k)
+        _, _, variant, ks, ws = _lib.gemm_check(m, n, k, k, n, n, n)
+        assert plan["variant"] == variant
+        want = ks if ks > 1 else 1
+        assert hg.mfma_k_split(plan) == want, (m, n, k)
+        if variant.startswith("mfma"):
+            tm, tn = hg.TILES[variant][:2]
+            assert hg.required_resources(plan)[1] == -(-m // tm) * -(-n // tn) * want
+            assert ws == (want * m * n * 4 if want > 1 else 0)
+    assert hg.mfma_k_split(hg.make_plan(128, 4096, 4096)) == 8
+    assert hg.mfma_k_split(hg.make_plan(128, 4096, 1024)) == 2     # slices of 512
+    assert hg.mfma_k_split(hg.make_plan(128, 4096, 1152)) == 1     # 1152 = 9 x 128

@@ -52,6 +52,14 @@ def test_native_selection_for_benchmark_configs():
     assert _lib.select_variant(64, 272, 64)[0] == "mfma_128x128"
     assert _lib.select_variant(16, 256, 64)[0] == "skinny"
     assert _lib.select_variant(128, 128, 128)[0] == "mfma_128x128"
+    # 17..64 rows with K >= 512: one B stream on the skinny kernel's row blocks,
+    # unless 128-column tiles alone fill the chip
+    assert _lib.select_variant(64, 14336, 4096)[0] == "skinny"
+    assert _lib.select_variant(17, 4096, 4096)[0] == "skinny"
+    assert _lib.select_variant(64, 28672, 8192)[0] == "skinny"
+    assert _lib.select_variant(64, 32768, 1024)[0] == "mfma_128x128"     # 256 tiles
+    assert _lib.select_variant(64, 4096, 256)[0] == "mfma_128x128"       # short K
+    assert _lib.select_variant(65, 4096, 4096)[0] == "mfma_128x128"
     assert _lib.select_variant(64, 60, 64, aligned=False)[0] == "generic"
 
 
@@ -77,7 +85,7 @@ def test_invalid_arguments_rejected_before_device(kw):
 def test_explicit_vector_variant_refuses_unaligned_shapes():
     assert call(N=20, variant=1) == _lib.VT_EUNSUPPORTED
     assert call(K=20, lda=20, variant=3) == _lib.VT_EUNSUPPORTED
-    assert call(M=17, variant=3) == _lib.VT_EUNSUPPORTED
+    assert call(M=65, variant=3) == _lib.VT_EUNSUPPORTED
     assert call(A=(1 << 20) + 1, variant=2) == _lib.VT_EUNSUPPORTED
 
 
@@ -271,20 +279,22 @@ def test_gemm_check_refusals_carry_the_native_reason():
     assert st == _lib.VT_EINVAL and "stride_c" in reason
     st, reason, *_ = _lib.gemm_check(32, 16, 16, 16, 16, 8, 16, has_d=True)
     assert st == _lib.VT_EINVAL and "ldd" in reason
-    st, reason, *_ = _lib.gemm_check(32, 16, 16, 16, 16, 16, 16, variant="skinny")
-    assert st == _lib.VT_EUNSUPPORTED and "M <= 16" in reason
+    st, reason, *_ = _lib.gemm_check(65, 16, 16, 16, 16, 16, 16, variant="skinny")
+    assert st == _lib.VT_EUNSUPPORTED and "M <= 64" in reason
 
 
 def test_mfma_variant_refuses_rows_too_long_for_tile_offsets():
     """256 * lda >= 2^32: an explicit MFMA variant refuses (no silent VALU
-    run); auto picks the VALU kernel, and the check says which."""
+    run); auto picks the VALU kernel past the skinny kernel's 64 rows (that
+    kernel addresses A and B with 64-bit offsets), and the check says which."""
     k = 1 << 24
     for variant in ("mfma_256x256", "mfma_256x128", "mfma_128x128"):
-        st, reason, *_ = _lib.gemm_check(32, 64, k, k, 64, 64, 64, variant=variant)
+        st, reason, *_ = _lib.gemm_check(100, 64, k, k, 64, 64, 64, variant=variant)
         assert st == _lib.VT_EUNSUPPORTED and "256*lda" in reason, variant
-    st, _, chosen, _, _ = _lib.gemm_check(32, 64, k, k, 64, 64, 64)
+    st, _, chosen, _, _ = _lib.gemm_check(100, 64, k, k, 64, 64, 64)
     assert st == 0 and chosen == "generic"
-    assert _lib.select_variant(32, 64, k)[0] == "generic"
+    assert _lib.select_variant(100, 64, k)[0] == "generic"
+    assert _lib.select_variant(32, 64, k)[0] == "skinny"
     # below the limit the MFMA variants accept rows of any length
     k = (1 << 24) - 4096
     assert _lib.gemm_check(32, 64, k, k, 64, 64, 64, variant="mfma_128x128")[0] == 0

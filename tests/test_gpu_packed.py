@@ -310,3 +310,30 @@ def test_dma_rows_with_packed_b_equal_row_major_config5_shape(dev):
     Cr = hg.run(hg.make_plan(n, n, n, variant="mfma_256x256"), At, Bt).cpu().numpy()
     assert np.array_equal(Cp, Cr)
     assert np.array_equal(Cp, go.gemm_i8_f64(A, B))
+
+
+# Up to 64 rows run as 1, 2 or 4 row blocks of 16 over one stream of packed B;
+# more rows as groups of 64.
+@pytest.mark.parametrize("m", [17, 32, 33, 48, 64, 100, 130])
+@pytest.mark.parametrize("k_split", [0, 3])
+def test_row_blocks_with_packed_b(dev, m, k_split):
+    rng = np.random.default_rng(1000 + m + k_split)
+    k, n = 1088, 4800        # 4800 columns: half-block column groups (masked)
+    A = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    B = rng.integers(-128, 128, (k, n), dtype=np.int8)
+    D = rng.integers(-2**20, 2**20, (m, n), dtype=np.int32)
+    say("packed row blocks", m, "k_split", k_split)
+    assert np.array_equal(gpu_gemm_packed(dev, A, B, k_split=k_split), go.gemm_i8(A, B))
+    assert np.array_equal(gpu_gemm_packed(dev, A, B, D, k_split=k_split, in_place=True),
+                          go.gemm_i8(A, B, D))
+
+
+def test_row_blocks_with_packed_b_whole_groups(dev):
+    """N = 14336: whole column groups (unmasked), 64 rows, extremes at K = 4096."""
+    m, k, n = 64, 4096, 14336
+    A = np.tile(np.array([-128, 127], np.int8), (m, k // 2))
+    B = np.tile(np.array([[127], [-128]], np.int8), (k // 2, n))
+    assert np.array_equal(gpu_gemm_packed(dev, A, B), go.gemm_i8_f64(A, B))
+    c = inputs.config_inputs(4, seed=2, m=16)
+    A = np.concatenate([c["A"]] * 4)          # 64 rows
+    assert np.array_equal(gpu_gemm_packed(dev, A, c["B"]), go.gemm_i8_f64(A, c["B"]))

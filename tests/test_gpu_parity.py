@@ -67,7 +67,7 @@ def gpu_gemm(dev, A, B, D=None, variant="auto", k_split=0, batch_shared=False):
 def test_spike_golden_vectors(dev, golden, variant):
     for run in golden["runs"]:
         m, n, k = run["plan"]["m"], run["plan"]["n"], run["plan"]["k"]
-        if variant == "skinny" and m > 16:
+        if variant == "skinny" and m > 64:
             continue
         for mode in golden["modes"]:
             say("golden", run["name"], mode, variant)
@@ -191,7 +191,7 @@ def test_edge_shapes_all_variants(dev, shape):
     D = rng.integers(-(1 << 20), (1 << 20) + 1, (m, n), dtype=np.int32)
     want = go.gemm_i8(A, B)
     want_d = go.gemm_i8(A, B, D)
-    variants = ["auto", "generic"] + list(VEC_VARIANTS) + (["skinny"] if m <= 16 else [])
+    variants = ["auto", "generic"] + list(VEC_VARIANTS) + (["skinny"] if m <= 64 else [])
     for variant in variants:
         say("edge", shape, variant)
         assert np.array_equal(gpu_gemm(dev, A, B, variant=variant), want), variant
@@ -244,6 +244,36 @@ def test_batched_unshared_and_shared(dev):
     A16 = A[:, :16, :]
     assert np.array_equal(gpu_gemm(dev, np.ascontiguousarray(A16), Bs, variant="skinny", k_split=2),
                           go.gemm_i8(A16, Bs))
+
+
+@pytest.mark.parametrize("m", [17, 24, 31, 32, 33, 48, 63, 64])
+@pytest.mark.parametrize("k_split", [0, 1, 3])
+def test_skinny_row_blocks(dev, m, k_split):
+    """17..64 rows run as 2 or 4 row blocks of 16 over the same B stream:
+    rows past M are zero in the A slice and never stored; D added in place."""
+    rng = np.random.default_rng(m * 10 + k_split)
+    n, k = 1040, 4160
+    A = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    B = rng.integers(-128, 128, (k, n), dtype=np.int8)
+    D = rng.integers(-(1 << 20), (1 << 20) + 1, (m, n), dtype=np.int32)
+    say("skinny row blocks", m, "k_split", k_split)
+    assert np.array_equal(gpu_gemm(dev, A, B, variant="skinny", k_split=k_split), go.gemm_i8(A, B))
+    At, Bt = torch.from_numpy(A).to(dev), torch.from_numpy(B).to(dev)
+    C = torch.from_numpy(D).to(dev)          # C = D + A.B in place
+    _lib.gemm_raw(At.data_ptr(), Bt.data_ptr(), C.data_ptr(), C.data_ptr(), m, n, k, k, n, n, n,
+                  1, 0, 0, 0, 0, "skinny", k_split, None)
+    _lib.sync(None)
+    assert np.array_equal(C.cpu().numpy(), go.gemm_i8(A, B, D))
+
+
+def test_skinny_row_blocks_extremes(dev):
+    m, k, n = 64, 8192, 256
+    A = np.full((m, k), -128, np.int8)
+    B = np.full((k, n), -128, np.int8)
+    assert np.all(gpu_gemm(dev, A, B, variant="skinny") == 134217728)
+    A = np.tile(np.array([-128, 127], np.int8), (m, k // 2))
+    B = np.tile(np.array([[127], [-128]], np.int8), (k // 2, n))
+    assert np.array_equal(gpu_gemm(dev, A, B, variant="skinny", k_split=5), go.gemm_i8_f64(A, B))
 
 
 def test_skinny_repeated_calls_reset_counters(dev):
@@ -530,7 +560,7 @@ def _random_case(rng, variant):
     def dim(lo, hi, mult):
         return int(rng.integers(lo // mult, hi // mult + 1)) * mult
     mult = 1 if variant in ("generic", "padded") else 16
-    m = int(rng.integers(1, 17)) if variant == "skinny" else int(rng.integers(1, 600))
+    m = int(rng.integers(1, 65)) if variant == "skinny" else int(rng.integers(1, 600))
     n, k = dim(16, 640, mult), dim(16, 1024, mult)
     pad_a = int(rng.integers(0, 3)) * (1 if mult == 1 else 16)
     pad_b = int(rng.integers(0, 3)) * (1 if mult == 1 else 16)
@@ -563,3 +593,58 @@ def test_random_problems_match_the_oracle(dev, variant):
             want = cref.gemm_i8(A[b, :, :k], B[0 if shared_b else b, :, :n],
                                 D[b] if has_d else None, order="ikj")
             assert np.array_equal(got[b], want), (variant, case, b)
+
+
+# Few long MFMA tiles: K runs as slices (batches of the same kernel) into a
+# partial-sum workspace, added with D by the reduction kernel.
+SPLIT_CASES = [("mfma_128x128", 128, 4096, 4096), ("mfma_128x128", 96, 2048, 2048),
+               ("mfma_128x128", 100, 208, 2048), ("mfma_256x256", 256, 256, 8192),
+               ("mfma_256x128", 256, 384, 4096), ("auto", 256, 1024, 4096)]
+
+
+@pytest.mark.parametrize("variant,m,n,k", SPLIT_CASES)
+def test_mfma_k_split(dev, variant, m, n, k):
+    name = variant if variant != "auto" else _lib.select_variant(m, n, k)[0]
+    plan = hg.make_plan(m, n, k, variant=name)
+    ks = hg.mfma_k_split(plan)
+    say("mfma split", variant, m, n, k, "k slices", ks)
+    assert ks > 1
+    rng = np.random.default_rng(m + n + k)
+    A = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    B = rng.integers(-128, 128, (k, n), dtype=np.int8)
+    D = rng.integers(-(1 << 20), (1 << 20) + 1, (m, n), dtype=np.int32)
+    assert np.array_equal(gpu_gemm(dev, A, B, variant=variant), go.gemm_i8_f64(A, B))
+    At, Bt = torch.from_numpy(A).to(dev), torch.from_numpy(B).to(dev)
+    C = torch.from_numpy(D).to(dev)          # C = D + A.B in place
+    _lib.gemm_raw(At.data_ptr(), Bt.data_ptr(), C.data_ptr(), C.data_ptr(), m, n, k, k, n, n, n,
+                  1, 0, 0, 0, 0, variant, 0, None)
+    _lib.sync(None)
+    assert np.array_equal(C.cpu().numpy(), go.gemm_i8_f64(A, B, D))
+
+
+def test_mfma_k_split_extremes_and_graph_replays(dev):
+    m, n, k = 128, 256, 8192
+    A = np.tile(np.array([-128, 127], np.int8), (m, k // 2))
+    B = np.tile(np.array([[127], [-128]], np.int8), (k // 2, n))
+    want = go.gemm_i8_f64(A, B)
+    assert hg.mfma_k_split(hg.make_plan(m, n, k)) > 1
+    At, Bt = torch.from_numpy(A).to(dev), torch.from_numpy(B).to(dev)
+    plan = hg.make_plan(m, n, k)
+    s = torch.cuda.Stream(dev)
+    outs = [torch.full((m, n), INT32_MIN, dtype=torch.int32, device=dev) for _ in range(3)]
+    with torch.cuda.stream(s):
+        hg.run(plan, At, Bt, out=outs[0], stream=s.cuda_stream)   # sizes the workspace
+    s.synchronize()
+    assert np.array_equal(outs[0].cpu().numpy(), want)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for C in outs[1:]:
+            hg.run(plan, At, Bt, out=C, stream=s.cuda_stream)
+    for rep in range(3):
+        for C in outs[1:]:
+            C.fill_(INT32_MIN)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for C in outs[1:]:
+            assert np.array_equal(C.cpu().numpy(), want), rep

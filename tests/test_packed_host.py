@@ -82,12 +82,14 @@ def test_packed_plans_validate():
     # 2048 columns: 256 groups of one half block each, no K split
     p = hg.make_plan(40, 2048, 1024, variant=hg.PACKED_VARIANT)
     assert hg.packed_columns(p) == (1, 256) and hg.packed_split(p) == (1, 16)
-    # few column groups: split K; rows beyond 16 run as row groups
+    # few column groups: split K; up to 64 rows run in one group (row blocks
+    # of 16), more rows as groups of 64
     p = hg.make_plan(40, 64, 1024, variant=hg.PACKED_VARIANT)
     assert hg.validate_plan(p)[0]
     assert hg.packed_columns(p) == (1, 8)
     assert hg.packed_split(p) == (2, 8)
-    assert hg.required_resources(p)[1] == 8 * 2 * 3
+    assert hg.required_resources(p)[1] == 8 * 2 * 1
+    assert hg.required_resources(dict(p, m=100))[1] == 8 * 2 * 2
     # fewer than 192 whole groups: one group per CU, down to half a block;
     # at most 8 half blocks (4 tiles) per group; batches share the chip
     assert hg.packed_columns(dict(p, n=4800)) == (3, 200)
@@ -109,8 +111,8 @@ def test_packed_plans_validate():
 
 def test_packed_rows_in_whole_tiles_go_to_the_256_kernel():
     """Rows in whole 256-row tiles run on the 256x256 kernel when n % 256 == 0
-    and k % 64 == 0; the rest in groups of 16 (the split packed_dma_fits makes
-    in the library)."""
+    and k % 64 == 0; the rest in groups of up to 64 (the split packed_dma_fits
+    makes in the library)."""
     plan = lambda m, n, k, **kw: hg.make_plan(m, n, k, variant=hg.PACKED_VARIANT, **kw)
     assert hg.packed_dma_rows(plan(8192, 8192, 8192)) == 8192
     assert hg.packed_dma_rows(plan(300, 512, 128)) == 256
@@ -121,8 +123,8 @@ def test_packed_rows_in_whole_tiles_go_to_the_256_kernel():
     assert hg.packed_dma_rows(plan(256, 256, 64 * 262143)) == 256
     assert hg.packed_dma_rows(plan(256, 256, 64 * 262144)) == 0
     p = plan(300, 512, 128)
-    assert hg.required_resources(p) == (hg.DMA_LDS, 2 + hg.packed_columns(dict(p, m=44))[1] * 3)
-    assert "256 rows on the 256x256 kernel, 44 in groups of 16" in hg.native_check(p)[1]
+    assert hg.required_resources(p) == (hg.DMA_LDS, 2 + hg.packed_columns(dict(p, m=44))[1])
+    assert "256 rows on the 256x256 kernel, 44 in groups of up to 64" in hg.native_check(p)[1]
     # 8192^3 packed is modeled as the 256x256 kernel, not as 512 row groups
     big = plan(8192, 8192, 8192)
     t_packed = hg.modeled_objective(big, hg.modeled_counts(big))[0]

@@ -27,12 +27,13 @@
 //       are remapped so consecutive tiles share an XCD (and its L2), then
 //       grouped along M. A K of at most 128 runs the SHORT instantiation,
 //       which fetches its two slices in one round trip.
-//   skinny_kernel<NB>  M <= 16 (decode). Bandwidth-bound: each workgroup
-//       streams an NB-column slab of B exactly once over a K slice with
-//       non-temporal loads, U stages of 64 rows in flight in registers, LDS
-//       double buffer, the A slice resident in LDS, v_mfma_i32_16x16x64_i8
-//       with M padded to 16. K slices write int32 partials to a workspace and
-//       skinny_reduce_kernel, next on the same stream, adds them (and D).
+//   skinny_kernel<NB>  M <= 64 (decode and small batches). Bandwidth-bound:
+//       each workgroup streams an NB-column slab of B exactly once over a K
+//       slice with non-temporal loads, U stages of 64 rows in flight in
+//       registers, LDS double buffer, the A slice resident in LDS,
+//       v_mfma_i32_16x16x64_i8 over 1, 2 or 4 row blocks of 16 (M padded up).
+//       K slices write int32 partials to a workspace and skinny_reduce_kernel,
+//       next on the same stream, adds them (and D).
 //   generic_kernel  any shape, stride or alignment; one thread per output,
 //       int32 VALU. Used where the vector kernels' alignment rules fail.
 //
@@ -215,7 +216,11 @@ struct GemmArgs {
   int batch_count;   // batches (the persistent kernel walks all their tiles)
 };
 
-template <int BM, int BN, bool EDGE, bool HAS_D, bool SHORT, bool EARLY_D>
+// EDGE: 0 full tiles; 1 M or N not a multiple of the tile (clamped source
+// rows and columns, masked stores); 2 also K not a multiple of 128 (each load
+// checks the K tail). The K checks sit in the k loop, so a ragged M or N
+// alone does not pay for them.
+template <int BM, int BN, int EDGE, bool HAS_D, bool SHORT, bool EARLY_D>
 __global__ __launch_bounds__(256, 1) void gemm_mfma_kernel(GemmArgs p) {
   constexpr int BK = 64;
   constexpr int WTM = BM / 2, WTN = BN / 2;   // wave tile (2x2 waves)
@@ -296,7 +301,7 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma_kernel(GemmArgs p) {
     const int8_t *bbase = Bb + (int64_t)k0 * p.ldb;
 #pragma unroll
     for (int i = 0; i < CA; ++i) {
-      if (EDGE && kt * BK + a_k[i] >= K) {
+      if (EDGE == 2 && kt * BK + a_k[i] >= K) {
         ra[i] = v4i{0, 0, 0, 0};
       } else {
         ra[i] = *(const v4i *)(abase + a_goff[i]);
@@ -304,7 +309,7 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma_kernel(GemmArgs p) {
     }
 #pragma unroll
     for (int i = 0; i < CB; ++i) {
-      if (EDGE && k0 + b_row[i] >= K) {
+      if (EDGE == 2 && k0 + b_row[i] >= K) {
         // rows past K: re-read row K-1 (A is zero there)
         rb[i] = *(const v4i *)(Bb + (int64_t)(K - 1 - b_row[i]) * p.ldb + b_goff[i]);
       } else {
@@ -390,8 +395,8 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma_kernel(GemmArgs p) {
   constexpr bool D_EARLY = D_TILE && EARLY_D;
   int32_t d_pre[D_TILE ? MI : 1][D_TILE ? NI : 1][16];
   if constexpr (D_EARLY)
-    load_d_tile<MI, NI, EDGE>(d_pre, p.D + bidx * p.sd, p.ldd, m0 + wm * WTM, n0 + wn * WTN, M, N,
-                              lane);
+    load_d_tile<MI, NI, (EDGE > 0)>(d_pre, p.D + bidx * p.sd, p.ldd, m0 + wm * WTM, n0 + wn * WTN,
+                                    M, N, lane);
 
   // SHORT (K <= 128, one pair of steps; the host picks it): slices 0 and 1
   // are both in flight before the first wait and nothing more is fetched,
@@ -453,7 +458,7 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma_kernel(GemmArgs p) {
     b2 = bt;
   };
   // Two steps per iteration (one per staging set). An odd step count only
-  // occurs on the edge path (the host routes K % 128 != 0 there), where the
+  // occurs with EDGE == 2 (the host routes K % 128 != 0 there), where the
   // padding step multiplies zero A columns.
   if constexpr (SHORT) {
     step(0, ra0, rb0);
@@ -467,18 +472,18 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma_kernel(GemmArgs p) {
 
   if constexpr (D_TILE) {
     if constexpr (!D_EARLY)
-      load_d_tile<MI, NI, EDGE>(d_pre, p.D + bidx * p.sd, p.ldd, m0 + wm * WTM, n0 + wn * WTN, M,
-                                N, lane);
+      load_d_tile<MI, NI, (EDGE > 0)>(d_pre, p.D + bidx * p.sd, p.ldd, m0 + wm * WTM, n0 + wn * WTN,
+                                      M, N, lane);
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
       for (int ni = 0; ni < NI; ++ni)
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[mi][ni][e] = add_wrap(acc[mi][ni][e], d_pre[mi][ni][e]);
-    store_tile<MI, NI, EDGE, false>(acc, p.C + bidx * p.sc, nullptr, p.ldc, p.ldd,
+    store_tile<MI, NI, (EDGE > 0), false>(acc, p.C + bidx * p.sc, nullptr, p.ldc, p.ldd,
                                     m0 + wm * WTM, n0 + wn * WTN, M, N, lane);
   } else {
-    store_tile<MI, NI, EDGE, HAS_D>(acc, p.C + bidx * p.sc, HAS_D ? p.D + bidx * p.sd : nullptr,
+    store_tile<MI, NI, (EDGE > 0), HAS_D>(acc, p.C + bidx * p.sc, HAS_D ? p.D + bidx * p.sd : nullptr,
                                     p.ldc, p.ldd, m0 + wm * WTM, n0 + wn * WTN, M, N, lane);
   }
 }
@@ -496,7 +501,7 @@ __device__ __forceinline__ void dma_b128(const int8_t *base, uint32_t voff, uint
                :: "v"(voff), "s"(base), "s"(m0));
 }
 
-// Same contract as gemm_mfma_kernel<256, 256, false, HAS_D, false> (full tiles only:
+// Same contract as gemm_mfma_kernel<256, 256, 0, HAS_D, false> (full tiles only:
 // M % 256 == 0, N % 256 == 0, K % 64 == 0), but the k slices go global -> LDS
 // by DMA (no VGPR staging, no ds_write instructions) and the kernel is
 // persistent: one workgroup per CU walks its tiles in order and the slice
@@ -750,7 +755,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_dma_kernel(GemmArgs p) {
 }
 
 // ---------------------------------------------------------------------------
-// Skinny (decode) kernels: M <= 16
+// Skinny (decode) kernels: M <= 64
 // ---------------------------------------------------------------------------
 
 // Row pitch of the LDS-resident A slice in the skinny kernel: a multiple of
@@ -788,21 +793,25 @@ struct SkinnyArgs {
 // the 64-row k-block w / (NB/16) against n-block w % (NB/16) with one
 // v_mfma_i32_16x16x64_i8 (M padded to 16 by zero rows of the LDS-resident A
 // slice). At the end the R/64 waves that share an n-block are summed through LDS.
-template <int NB, int WAVES, int U, bool HAS_D>
+// MB row blocks of 16 (M <= 16 * MB): the A slice holds 16 * MB rows and each
+// wave reuses its B fragment for MB MFMAs, one per row block, so B is still
+// streamed once for up to 64 rows.
+template <int NB, int WAVES, int U, int MB, bool HAS_D>
 __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(SkinnyArgs p) {
   constexpr int THREADS = 64 * WAVES;
   constexpr int NBLK = NB / 16;               // 16-column blocks = chunks per row
   constexpr int R = THREADS * 16 / NB;        // rows per stage
   constexpr int KB = R / 64;                  // 64-row k-blocks per stage
   constexpr int STAGE_BYTES = R * NB;
-  static_assert(KB * NBLK == WAVES && R % 64 == 0, "one MFMA per wave per stage");
+  static_assert(KB * NBLK == WAVES && R % 64 == 0, "one n-block per wave per stage");
   static_assert(NBLK == 16, "skinny_b_swz assumes 256-byte stage rows");
   static_assert(U % 2 == 0, "stages alternate between two LDS buffers by u & 1");
+  static_assert(KB == 1 || MB == 1, "the cross-wave sum holds one row block");
 
   extern __shared__ __attribute__((aligned(16))) int8_t dsmem[];
   const int a_stride = skinny_a_stride(p.k_chunk);
   int8_t *const As = dsmem;
-  int8_t *const Bs0 = dsmem + 16 * a_stride;  // stage buffer b at Bs0 + b*STAGE_BYTES
+  int8_t *const Bs0 = dsmem + 16 * MB * a_stride;  // stage buffer b at Bs0 + b*STAGE_BYTES
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   // XCD-aware order: workgroup w runs on XCD w % 8; give each XCD a contiguous
@@ -841,10 +850,10 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(SkinnyArgs p) {
 #pragma unroll
   for (int u = 0; u < U; ++u) rb[u] = load_stage(u);
 
-  // A slice -> LDS, [16][k_chunk] with zero rows past M and zero k past K.
+  // A slice -> LDS, [16 * MB][k_chunk] with zero rows past M and zero k past K.
   {
     const int cpr = p.k_chunk / 16;
-    for (int i = tid; i < 16 * cpr; i += THREADS) {
+    for (int i = tid; i < 16 * MB * cpr; i += THREADS) {
       const int row = i / cpr, c = i - row * cpr;
       const int k = kbeg + c * 16;
       v4i v = v4i{0, 0, 0, 0};
@@ -859,7 +868,9 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(SkinnyArgs p) {
   const int b_frag = r0 * NB + ((nblk ^ skinny_b_swz(r0)) << 4) + (j & 1) * 8;
   const int a_frag = (lane & 15) * a_stride + kb * 64 + g * 16;
 
-  v4i acc = v4i{0, 0, 0, 0};
+  v4i acc[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) acc[mb] = v4i{0, 0, 0, 0};
   for (int t0 = 0; t0 < T; t0 += U) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -868,26 +879,32 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(SkinnyArgs p) {
       st_lds_b128(Bs, b_lds, rb[u]);
       rb[u] = load_stage(s + U);
       lds_barrier();
-      const v4i a = ld_lds_b128(As, a_frag + s * R);
       const v2i lo = ld_lds_tr8(Bs, b_frag);
       const v2i hi = ld_lds_tr8(Bs, b_frag + 8 * NB);
-      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, v4i{lo.x, lo.y, hi.x, hi.y}, acc, 0, 0, 0);
+      const v4i b = v4i{lo.x, lo.y, hi.x, hi.y};
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        const v4i a = ld_lds_b128(As, a_frag + mb * 16 * a_stride + s * R);
+        acc[mb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc[mb], 0, 0, 0);
+      }
     }
   }
 
   // Sum the KB partials of each n-block through LDS (stage buffers are free
   // after the barrier). 16x16 accumulator layout: element e of lane l is
   // row 4*(l/16) + e, column l%16.
-  int32_t *red = (int32_t *)Bs0;
-  lds_barrier();
-  *(LDS_AS v4i *)((LDS_AS int32_t *)red + (wave * 64 + lane) * 4) = acc;
-  lds_barrier();
-  if (kb != 0) return;
+  if constexpr (KB > 1) {
+    int32_t *red = (int32_t *)Bs0;
+    lds_barrier();
+    *(LDS_AS v4i *)((LDS_AS int32_t *)red + (wave * 64 + lane) * 4) = acc[0];
+    lds_barrier();
+    if (kb != 0) return;
 #pragma unroll
-  for (int q = 1; q < KB; ++q) {
-    const v4i o = *(const LDS_AS v4i *)((const LDS_AS int32_t *)red + ((wave + q * NBLK) * 64 + lane) * 4);
+    for (int q = 1; q < KB; ++q) {
+      const v4i o = *(const LDS_AS v4i *)((const LDS_AS int32_t *)red + ((wave + q * NBLK) * 64 + lane) * 4);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) acc[e] = add_wrap(acc[e], o[e]);
+      for (int e = 0; e < 4; ++e) acc[0][e] = add_wrap(acc[0][e], o[e]);
+    }
   }
   const int col = n0 + nblk * 16 + j;
   if (col >= N) return;
@@ -895,24 +912,28 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(SkinnyArgs p) {
     const int32_t *Db = HAS_D ? p.D + bidx * p.sd : nullptr;
     int32_t *Cb = p.C + bidx * p.sc;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int row = g * 4 + e;
-      if (row < M) {
-        int32_t v = acc[e];
-        if (HAS_D) v = add_wrap(v, Db[(int64_t)row * p.ldd + col]);
-        Cb[(int64_t)row * p.ldc + col] = v;
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = mb * 16 + g * 4 + e;
+        if (row < M) {
+          int32_t v = acc[mb][e];
+          if (HAS_D) v = add_wrap(v, Db[(int64_t)row * p.ldd + col]);
+          Cb[(int64_t)row * p.ldc + col] = v;
+        }
       }
-    }
   } else {
     int32_t *wsb = p.ws + ((int64_t)bidx * p.k_split + split) * M * N;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int row = g * 4 + e;
-      // Non-temporal: the partials are read once, by the next kernel, and
-      // kept out of L2 they need no writeback at the kernel boundary
-      // (measured 15.4 -> 15.1 us per decode step at K = 4096, N = 14336).
-      if (row < M) __builtin_nontemporal_store(acc[e], wsb + (int64_t)row * N + col);
-    }
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = mb * 16 + g * 4 + e;
+        // Non-temporal: the partials are read once, by the next kernel, and
+        // kept out of L2 they need no writeback at the kernel boundary
+        // (measured 15.4 -> 15.1 us per decode step at K = 4096, N = 14336).
+        if (row < M) __builtin_nontemporal_store(acc[mb][e], wsb + (int64_t)row * N + col);
+      }
   }
 }
 
@@ -1030,7 +1051,9 @@ struct PackedArgs {
   int32_t *ws;       // [batch][k_split][M][N] partials when k_split > 1
 };
 
-// M <= 16. One workgroup = WAVES waves over one column group and one K slice.
+// M <= 16 * MB (MB row blocks of 16, up to 64 rows): every B tile a wave loads
+// feeds MB MFMAs, so B is streamed once for all of them.
+// One workgroup = WAVES waves over one column group and one K slice.
 // A column group is hpw consecutive 8-column half blocks, so it touches at
 // most NBW 16-column blocks; tiles past its last block are dead and store
 // nothing. Whole groups (hpw = 2 * NBW, MASKED false) load every tile, a dead
@@ -1040,12 +1063,12 @@ struct PackedArgs {
 // neither load B (a packed tile's half is whole 128-byte lines) nor store C.
 // Small groups let a small N spread over every CU without splitting K.
 // Wave w takes the 64-row blocks kb_beg + w, kb_beg + w + WAVES, ...;
-// per block it loads its A fragment (16 bytes per lane, rows past M and k past
-// K zero) and the NBW packed B tiles, S blocks ahead of the MFMAs
+// per block it loads its MB A fragments (16 bytes per lane, rows past M and k
+// past K zero) and the NBW packed B tiles, S blocks ahead of the MFMAs
 // (non-temporal loads: B is streamed once). The WAVES partial sums of each
-// column block are added through LDS and written once (plus D), or go to the
-// workspace when K is split across workgroups.
-template <int NBW, int WAVES, int S, bool HAS_D, bool MASKED>
+// column block are added through LDS, one row block at a time, and written
+// once (plus D), or go to the workspace when K is split across workgroups.
+template <int NBW, int WAVES, int S, int MB, bool HAS_D, bool MASKED>
 __global__ __launch_bounds__(64 * WAVES) void packed_skinny_kernel(PackedArgs p) {
   __shared__ v4i red[WAVES * NBW * 64];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -1061,9 +1084,15 @@ __global__ __launch_bounds__(64 * WAVES) void packed_skinny_kernel(PackedArgs p)
   const int nb0 = h0 >> 1, nb_last = (h1 - 1) >> 1;
   const int kb_beg = split * p.kb_per_split;
   const int kb_end = min(kb_beg + p.kb_per_split, p.kbt);
-  const int arow = lane & 15, acol = (lane >> 4) * 16;
-  const bool arow_ok = arow < p.M;
-  const int8_t *a_src = p.A + bidx * p.sa + (int64_t)(arow_ok ? arow : 0) * p.lda + acol;
+  const int acol = (lane >> 4) * 16;
+  bool arow_ok[MB];
+  const int8_t *a_src[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    const int arow = mb * 16 + (lane & 15);
+    arow_ok[mb] = arow < p.M;
+    a_src[mb] = p.A + bidx * p.sa + (int64_t)(arow_ok[mb] ? arow : 0) * p.lda + acol;
+  }
   const int8_t *Bb = p.Bp + bidx * p.sbp;
   // Tiles 0 .. live-1 are blocks nb0 .. nb_last. Live columns of tile n within
   // its block: [col_lo(n), col_hi(n)); with MASKED a lane loads B only for a
@@ -1078,14 +1107,16 @@ __global__ __launch_bounds__(64 * WAVES) void packed_skinny_kernel(PackedArgs p)
     b_live[n] = (lane & 15) >= col_lo(n) && (lane & 15) < col_hi(n);
     b_off[n] = (int64_t)min(nb0 + n, nbt - 1) * p.kbt * 1024 + lane * 16;
   }
-  v4i acc[NBW];
+  v4i acc[MB][NBW];
 #pragma unroll
-  for (int n = 0; n < NBW; ++n) acc[n] = v4i{0, 0, 0, 0};
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int n = 0; n < NBW; ++n) acc[mb][n] = v4i{0, 0, 0, 0};
 
   const int first = kb_beg + wave;
   const int steps = first < kb_end ? (kb_end - first + WAVES - 1) / WAVES : 0;
-  v4i a[S], b[S][NBW];
-  auto load = [&](int s, v4i &av, v4i (&bv)[NBW]) {
+  v4i a[S][MB], b[S][NBW];
+  auto load = [&](int s, v4i (&av)[MB], v4i (&bv)[NBW]) {
     if (s < steps) {
       const int kb = first + s * WAVES;
 #pragma unroll
@@ -1093,11 +1124,15 @@ __global__ __launch_bounds__(64 * WAVES) void packed_skinny_kernel(PackedArgs p)
         bv[n] = (!MASKED || b_live[n])
                     ? __builtin_nontemporal_load((const v4i *)(Bb + b_off[n] + (int64_t)kb * 1024))
                     : v4i{0, 0, 0, 0};
-      av = (arow_ok && kb * 64 + acol < p.K) ? *(const v4i *)(a_src + kb * 64) : v4i{0, 0, 0, 0};
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+        av[mb] = (arow_ok[mb] && kb * 64 + acol < p.K) ? *(const v4i *)(a_src[mb] + kb * 64)
+                                                       : v4i{0, 0, 0, 0};
     } else {
 #pragma unroll
       for (int n = 0; n < NBW; ++n) bv[n] = v4i{0, 0, 0, 0};
-      av = v4i{0, 0, 0, 0};
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) av[mb] = v4i{0, 0, 0, 0};
     }
   };
 #pragma unroll
@@ -1106,8 +1141,10 @@ __global__ __launch_bounds__(64 * WAVES) void packed_skinny_kernel(PackedArgs p)
 #pragma unroll
     for (int s = 0; s < S; ++s) {
 #pragma unroll
-      for (int n = 0; n < NBW; ++n)
-        acc[n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[s], b[s][n], acc[n], 0, 0, 0);
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int n = 0; n < NBW; ++n)
+          acc[mb][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[s][mb], b[s][n], acc[mb][n], 0, 0, 0);
       load(s0 + s + S, a[s], b[s]);
     }
   }
@@ -1115,27 +1152,33 @@ __global__ __launch_bounds__(64 * WAVES) void packed_skinny_kernel(PackedArgs p)
   // 16x16 accumulator layout: element e of lane l is row 4*(l/16) + e,
   // column l%16. Thread t sums output (block t/256, row (t/16)%16, column t%16)
   // over the waves, so 16 consecutive threads write 64 contiguous bytes.
-#pragma unroll
-  for (int n = 0; n < NBW; ++n) red[(wave * NBW + n) * 64 + lane] = acc[n];
-  __syncthreads();
+  // One row block at a time through the same LDS buffer.
   const int32_t *Db = HAS_D ? p.D + bidx * p.sd : nullptr;
   int32_t *Cb = p.C + bidx * p.sc;
   int32_t *wsb = p.ws ? p.ws + ((int64_t)bidx * p.k_split + split) * p.M * p.N : nullptr;
-  for (int t = tid; t < NBW * 256; t += 64 * WAVES) {
-    const int n = t >> 8, row = (t >> 4) & 15, c = t & 15;
-    const int src = (row >> 2) * 16 + c, e = row & 3;
-    int32_t s = 0;
 #pragma unroll
-    for (int wv = 0; wv < WAVES; ++wv)
-      s = add_wrap(s, ((const int32_t *)&red[(wv * NBW + n) * 64 + src])[e]);
-    if (MASKED ? (c < col_lo(n) || c >= col_hi(n)) : n >= live) continue;
-    if (row >= p.M) continue;
-    const int col = (nb0 + n) * 16 + c;
-    if (p.k_split == 1) {
-      if (HAS_D) s = add_wrap(s, Db[(int64_t)row * p.ldd + col]);
-      Cb[(int64_t)row * p.ldc + col] = s;
-    } else {
-      __builtin_nontemporal_store(s, wsb + (int64_t)row * p.N + col);
+  for (int mb = 0; mb < MB; ++mb) {
+    if (mb > 0) __syncthreads();   // the previous row block's sums are read
+#pragma unroll
+    for (int n = 0; n < NBW; ++n) red[(wave * NBW + n) * 64 + lane] = acc[mb][n];
+    __syncthreads();
+    for (int t = tid; t < NBW * 256; t += 64 * WAVES) {
+      const int n = t >> 8, r16 = (t >> 4) & 15, c = t & 15;
+      const int src = (r16 >> 2) * 16 + c, e = r16 & 3;
+      int32_t s = 0;
+#pragma unroll
+      for (int wv = 0; wv < WAVES; ++wv)
+        s = add_wrap(s, ((const int32_t *)&red[(wv * NBW + n) * 64 + src])[e]);
+      const int row = mb * 16 + r16;
+      if (MASKED ? (c < col_lo(n) || c >= col_hi(n)) : n >= live) continue;
+      if (row >= p.M) continue;
+      const int col = (nb0 + n) * 16 + c;
+      if (p.k_split == 1) {
+        if (HAS_D) s = add_wrap(s, Db[(int64_t)row * p.ldd + col]);
+        Cb[(int64_t)row * p.ldc + col] = s;
+      } else {
+        __builtin_nontemporal_store(s, wsb + (int64_t)row * p.N + col);
+      }
     }
   }
 }
@@ -1305,6 +1348,10 @@ const VariantInfo kVariants[VT_VARIANT_COUNT] = {
 // Default skinny configuration: 256-column slabs (full 128-byte lines of B
 // per row), 16 waves, 2 stages in flight per thread.
 constexpr int kSkinnyNB = 256, kSkinnyWaves = 16, kSkinnyU = 2;
+// Rows the skinny kernel takes: up to 4 row blocks of 16.
+constexpr int kSkinnyMaxM = 64;
+// Row blocks of 16 the skinny kernel is instantiated with for M rows.
+int skinny_row_blocks(int64_t M) { return M <= 16 ? 1 : M <= 32 ? 2 : 4; }
 // LDS for the replay's scratchpad and accumulator (plus the latched B tile).
 constexpr int kMaxReplayLds = 152 * 1024;
 constexpr int kMaxSkinnyLds = 160 * 1024;
@@ -1542,6 +1589,16 @@ int select_variant(const Problem &q, bool vec, int32_t *variant, int32_t *k_spli
     *k_split = choose_k_split(q.N, q.K, q.batch);
     return VT_OK;
   }
+  // 17..64 rows: streaming B once on the skinny kernel (2 or 4 row blocks)
+  // beats the MFMA tiles' long K loop unless 128-column tiles alone fill the
+  // chip (measured at K = 4096: 1.5-3x faster for N = 4096 .. 28672, even at
+  // N = 57344 and 65536; 7x at N = 1024, K = 16384). Short K stays on the
+  // MFMA kernels, whose K loop is then a round trip or two.
+  if (q.M <= kSkinnyMaxM && q.K >= 512 && (q.N + 127) / 128 * q.batch < 256) {
+    *variant = VT_VARIANT_SKINNY;
+    *k_split = choose_k_split(q.N, q.K, q.batch);
+    return VT_OK;
+  }
   // Rows too long for the MFMA kernels' tile-relative 32-bit offsets
   // (lda >= 2^24 bytes) go to the VALU kernel.
   if (!mfma_addressable(q)) {
@@ -1568,7 +1625,7 @@ int select_variant(const Problem &q, bool vec, int32_t *variant, int32_t *k_spli
 // Waves per workgroup of the persistent full-tile kernel.
 constexpr int kDmaWaves = 4;
 
-template <int BM, int BN, bool EDGE, bool HAS_D>
+template <int BM, int BN, int EDGE, bool HAS_D>
 void launch_mfma_kernel(bool short_k, bool early_d, dim3 grid, dim3 block, hipStream_t stream,
                         const GemmArgs &a) {
   if constexpr (HAS_D) {
@@ -1582,19 +1639,97 @@ void launch_mfma_kernel(bool short_k, bool early_d, dim3 grid, dim3 block, hipSt
   else hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, EDGE, HAS_D, false, false>), grid, block, 0, stream, a);
 }
 
-template <int BM, int BN>
-int launch_mfma(const Problem &q, hipStream_t stream, int num_cus) {
-  // Fold contiguous shared-B batches into one stacked-M GEMM.
+// Contiguous shared-B batches as one GEMM with stacked M.
+Problem mfma_fold(const Problem &q) {
   Problem r = q;
   if (r.batch > 1 && r.sb == 0 && r.sa == r.M * r.lda && r.sc == r.M * r.ldc &&
       (!r.D || r.sd == r.M * r.ldd) && r.M * r.batch < (1ll << 30)) {
     r.M *= r.batch;
     r.batch = 1;
   }
+  return r;
+}
+
+// K slices for an MFMA launch whose tiles alone would leave most of the chip
+// idle: a K of at least 1024 over at most 64 tiles is cut into ks slices of
+// whole 128-deep steps, each at least 512 deep, for up to 256 workgroups. The
+// slices run as ks batches of the same kernel into a partial-sum workspace
+// and skinny_reduce_kernel adds them (and D). The partial sums cost
+// 8 * ks * M * N bytes of traffic, which a split of two over 65..128 tiles
+// does not earn back (M = 128, N = 14336, K = 4096: 22.6 -> 24.0 us); from
+// four slices on it does (N = K = 4096: M = 128 21.0 -> 13.2 us, M = 256
+// 21.2 -> 16.5 us; M = 128, N = 1024, K = 16384 in 13.2 us, M = N = 256,
+// K = 8192 in 10.0 us). Sized for the 256 CUs of an MI355X rather than the
+// device at hand, so launch, scratch sizing and the check agree. 1: no split.
+constexpr int64_t kSplitCus = 256;
+template <int BM, int BN>
+int mfma_k_split(const Problem &r) {
+  if (r.batch != 1 || r.K < 1024 || r.N % 16) return 1;
+  const int64_t tiles = (r.M + BM - 1) / BM * ((r.N + BN - 1) / BN);
+  if (tiles * 4 > kSplitCus) return 1;
+  int ks = 1;
+  while (ks < 16 && 2 * ks * tiles <= kSplitCus) ks *= 2;
+  while (ks > 1 && (r.K % (128 * ks) || r.K / ks < 512)) ks /= 2;
+  return ks;
+}
+
+// The K split vt_gemm_i8 launches for an MFMA variant (1 for the others).
+int mfma_split_for(const Problem &q, int32_t variant) {
+  const Problem r = mfma_fold(q);
+  switch (variant) {
+    case VT_VARIANT_MFMA_256x256: return mfma_k_split<256, 256>(r);
+    case VT_VARIANT_MFMA_128x128: return mfma_k_split<128, 128>(r);
+    case VT_VARIANT_MFMA_256x128: return mfma_k_split<256, 128>(r);
+    default: return 1;
+  }
+}
+
+template <int BM, int BN>
+int launch_mfma_tiles(const Problem &r, hipStream_t stream, int num_cus);
+
+template <int BM, int BN>
+int launch_mfma(const Problem &q, Scratch &scr) {
+  const Problem r = mfma_fold(q);
   if (!mfma_addressable(r))
     return fail(VT_EUNSUPPORTED,
                 "MFMA variants need 256*lda and 64*ldb below 2^32 (lda=%lld ldb=%lld)",
                 (long long)r.lda, (long long)r.ldb);
+  hipStream_t stream = (hipStream_t)scr.stream;
+  const int num_cus = scr.st->num_cus;
+  const int ks = mfma_k_split<BM, BN>(r);
+  if (ks == 1) return launch_mfma_tiles<BM, BN>(r, stream, num_cus);
+  // K slices as batches: slice i reads A columns and B rows [i*kc, (i+1)*kc)
+  // and writes its partial sums to slice i of the workspace.
+  void *w = nullptr;
+  int rc = scr.take(kPartials, (size_t)ks * r.M * r.N * sizeof(int32_t), &w);
+  if (rc) return rc;
+  const int64_t kc = r.K / ks;
+  Problem sl = r;
+  sl.K = kc;
+  sl.batch = ks;
+  sl.sa = kc;
+  sl.sb = kc * r.ldb;
+  sl.D = nullptr;
+  sl.sd = 0;
+  sl.C = (int32_t *)w;
+  sl.ldc = r.N;
+  sl.sc = r.M * r.N;
+  rc = launch_mfma_tiles<BM, BN>(sl, stream, num_cus);
+  if (rc) return rc;
+  ReduceArgs ra;
+  ra.ws = (const int32_t *)w; ra.D = r.D; ra.C = r.C;
+  ra.ldd = r.ldd; ra.ldc = r.ldc; ra.sd = 0; ra.sc = 0;
+  ra.M = (int)r.M; ra.N = (int)r.N; ra.k_split = ks;
+  const int64_t per = r.M * r.N / 4;
+  dim3 rgrid((unsigned)((per + 255) / 256), 1);
+  if (r.D) hipLaunchKernelGGL(skinny_reduce_kernel<true>, rgrid, dim3(256), 0, stream, ra);
+  else hipLaunchKernelGGL(skinny_reduce_kernel<false>, rgrid, dim3(256), 0, stream, ra);
+  VT_HIP_CHECK(hipGetLastError());
+  return VT_OK;
+}
+
+template <int BM, int BN>
+int launch_mfma_tiles(const Problem &r, hipStream_t stream, int num_cus) {
   GemmArgs a;
   a.A = r.A; a.B = r.B; a.D = r.D; a.C = r.C;
   a.lda = r.lda; a.ldb = r.ldb; a.ldd = r.ldd; a.ldc = r.ldc;
@@ -1617,15 +1752,18 @@ int launch_mfma(const Problem &q, hipStream_t stream, int num_cus) {
     VT_HIP_CHECK(hipGetLastError());
     return VT_OK;
   }
-  const bool edge = (r.M % BM) || (r.N % BN) || (r.K % 128);
+  const int edge = (r.K % 128) ? 2 : ((r.M % BM) || (r.N % BN)) ? 1 : 0;
   const bool short_k = r.K <= 128;
   const bool early_d = blocks <= num_cus;   // one workgroup per CU: occupancy costs nothing
-  if (edge) {
-    if (has_d) launch_mfma_kernel<BM, BN, true, true>(short_k, early_d, grid, block, stream, a);
-    else launch_mfma_kernel<BM, BN, true, false>(short_k, early_d, grid, block, stream, a);
+  if (edge == 2) {
+    if (has_d) launch_mfma_kernel<BM, BN, 2, true>(short_k, early_d, grid, block, stream, a);
+    else launch_mfma_kernel<BM, BN, 2, false>(short_k, early_d, grid, block, stream, a);
+  } else if (edge == 1) {
+    if (has_d) launch_mfma_kernel<BM, BN, 1, true>(short_k, early_d, grid, block, stream, a);
+    else launch_mfma_kernel<BM, BN, 1, false>(short_k, early_d, grid, block, stream, a);
   } else {
-    if (has_d) launch_mfma_kernel<BM, BN, false, true>(short_k, early_d, grid, block, stream, a);
-    else launch_mfma_kernel<BM, BN, false, false>(short_k, early_d, grid, block, stream, a);
+    if (has_d) launch_mfma_kernel<BM, BN, 0, true>(short_k, early_d, grid, block, stream, a);
+    else launch_mfma_kernel<BM, BN, 0, false>(short_k, early_d, grid, block, stream, a);
   }
   VT_HIP_CHECK(hipGetLastError());
   return VT_OK;
@@ -1644,20 +1782,30 @@ SkinnyGeom skinny_geometry(const Problem &q, int k_split) {
   constexpr int R = WAVES * 1024 / NB;           // rows per stage
   constexpr int64_t kAlign = (int64_t)R * U;     // rows per unrolled pipeline
   constexpr int64_t kStageLds = 2 * (int64_t)R * NB;
+  const int64_t a_rows = 16 * (int64_t)skinny_row_blocks(q.M);   // LDS rows of the A slice
   if (k_split <= 0) k_split = choose_k_split(q.N, q.K, q.batch);
   int64_t chunk = (q.K + k_split - 1) / k_split;
   chunk = (chunk + kAlign - 1) / kAlign * kAlign;
-  int64_t lds = 16 * (int64_t)skinny_a_stride((int)chunk) + kStageLds;
+  int64_t lds = a_rows * skinny_a_stride((int)chunk) + kStageLds;
   if (lds > kMaxSkinnyLds) {
-    chunk = ((kMaxSkinnyLds - kStageLds) / 16 - 48) / kAlign * kAlign;
-    lds = 16 * (int64_t)skinny_a_stride((int)chunk) + kStageLds;
+    // skinny_a_stride adds at most 48 bytes to a row
+    chunk = ((kMaxSkinnyLds - kStageLds) / a_rows - 48) / kAlign * kAlign;
+    lds = a_rows * skinny_a_stride((int)chunk) + kStageLds;
   }
   return SkinnyGeom{chunk, lds, (int)((q.K + chunk - 1) / chunk)};
 }
 
+template <int NB, int WAVES, int U, int MB>
+void launch_skinny_kernel(bool has_d, dim3 grid, dim3 block, size_t lds, hipStream_t s,
+                          const SkinnyArgs &a) {
+  if (has_d) hipLaunchKernelGGL((skinny_kernel<NB, WAVES, U, MB, true>), grid, block, lds, s, a);
+  else hipLaunchKernelGGL((skinny_kernel<NB, WAVES, U, MB, false>), grid, block, lds, s, a);
+}
+
 template <int NB, int WAVES, int U>
 int launch_skinny_cfg(const Problem &q, int k_split, Scratch &scr) {
-  if (q.M > 16) return fail(VT_EUNSUPPORTED, "skinny variant needs M <= 16 (M=%lld)", (long long)q.M);
+  if (q.M > kSkinnyMaxM)
+    return fail(VT_EUNSUPPORTED, "skinny variant needs M <= %d (M=%lld)", kSkinnyMaxM, (long long)q.M);
   const SkinnyGeom geo = skinny_geometry<NB, WAVES, U>(q, k_split);
   const int64_t chunk = geo.chunk, lds = geo.lds;
   const int ks = geo.ks;
@@ -1682,10 +1830,12 @@ int launch_skinny_cfg(const Problem &q, int k_split, Scratch &scr) {
   hipStream_t s = (hipStream_t)scr.stream;
   dim3 grid((unsigned)(a.tiles_n * ks), (unsigned)q.batch), block(64 * WAVES);
   // With a K split the slices write partials and the reduction applies D.
-  if (q.D && ks == 1)
-    hipLaunchKernelGGL((skinny_kernel<NB, WAVES, U, true>), grid, block, (size_t)lds, s, a);
-  else
-    hipLaunchKernelGGL((skinny_kernel<NB, WAVES, U, false>), grid, block, (size_t)lds, s, a);
+  const bool d_in = q.D && ks == 1;
+  switch (skinny_row_blocks(q.M)) {
+    case 1: launch_skinny_kernel<NB, WAVES, U, 1>(d_in, grid, block, (size_t)lds, s, a); break;
+    case 2: launch_skinny_kernel<NB, WAVES, U, 2>(d_in, grid, block, (size_t)lds, s, a); break;
+    default: launch_skinny_kernel<NB, WAVES, U, 4>(d_in, grid, block, (size_t)lds, s, a); break;
+  }
   VT_HIP_CHECK(hipGetLastError());
   if (ks > 1) {
     ReduceArgs r;
@@ -1770,8 +1920,21 @@ int launch_packed_dma(const Problem &q, hipStream_t stream, int num_cus) {
   return VT_OK;
 }
 
+template <int MB>
+void launch_packed_kernel(bool d_in, bool masked, dim3 grid, dim3 block, hipStream_t s,
+                          const PackedArgs &a) {
+  if (d_in && masked)
+    hipLaunchKernelGGL((packed_skinny_kernel<kPackedNBW, kPackedWaves, kPackedS, MB, true, true>), grid, block, 0, s, a);
+  else if (d_in)
+    hipLaunchKernelGGL((packed_skinny_kernel<kPackedNBW, kPackedWaves, kPackedS, MB, true, false>), grid, block, 0, s, a);
+  else if (masked)
+    hipLaunchKernelGGL((packed_skinny_kernel<kPackedNBW, kPackedWaves, kPackedS, MB, false, true>), grid, block, 0, s, a);
+  else
+    hipLaunchKernelGGL((packed_skinny_kernel<kPackedNBW, kPackedWaves, kPackedS, MB, false, false>), grid, block, 0, s, a);
+}
+
 // One launch (plus the partial-sum reduction when K is split) over at most
-// 16 rows of A / C / D.
+// kSkinnyMaxM (64) rows of A / C / D: 1, 2 or 4 row blocks of 16.
 int launch_packed_rows(const Problem &q, int k_split, Scratch &scr) {
   PackedArgs a;
   a.A = q.A; a.Bp = q.B; a.D = q.D; a.C = q.C;
@@ -1797,14 +1960,11 @@ int launch_packed_rows(const Problem &q, int k_split, Scratch &scr) {
   hipStream_t s = (hipStream_t)scr.stream;
   dim3 grid((unsigned)(a.groups * a.k_split), (unsigned)q.batch), block(64 * kPackedWaves);
   const bool d_in = q.D && a.k_split == 1, masked = a.hpw != 2 * kPackedNBW;
-  if (d_in && masked)
-    hipLaunchKernelGGL((packed_skinny_kernel<kPackedNBW, kPackedWaves, kPackedS, true, true>), grid, block, 0, s, a);
-  else if (d_in)
-    hipLaunchKernelGGL((packed_skinny_kernel<kPackedNBW, kPackedWaves, kPackedS, true, false>), grid, block, 0, s, a);
-  else if (masked)
-    hipLaunchKernelGGL((packed_skinny_kernel<kPackedNBW, kPackedWaves, kPackedS, false, true>), grid, block, 0, s, a);
-  else
-    hipLaunchKernelGGL((packed_skinny_kernel<kPackedNBW, kPackedWaves, kPackedS, false, false>), grid, block, 0, s, a);
+  switch (skinny_row_blocks(q.M)) {
+    case 1: launch_packed_kernel<1>(d_in, masked, grid, block, s, a); break;
+    case 2: launch_packed_kernel<2>(d_in, masked, grid, block, s, a); break;
+    default: launch_packed_kernel<4>(d_in, masked, grid, block, s, a); break;
+  }
   VT_HIP_CHECK(hipGetLastError());
   if (a.k_split > 1) {
     ReduceArgs r;
@@ -1984,6 +2144,12 @@ int64_t scratch_need(const Problem &q, int32_t variant, int32_t k_split) {
     const SkinnyGeom geo = skinny_geometry<kSkinnyNB, kSkinnyWaves, kSkinnyU>(q, k_split);
     return geo.ks > 1 ? round256(q.batch * geo.ks * q.M * q.N * 4) : 0;
   }
+  if (variant == VT_VARIANT_MFMA_256x256 || variant == VT_VARIANT_MFMA_128x128 ||
+      variant == VT_VARIANT_MFMA_256x128) {
+    const int ks = mfma_split_for(q, variant);
+    const Problem r = mfma_fold(q);
+    return ks > 1 ? round256(ks * r.M * r.N * 4) : 0;
+  }
   if (variant != VT_VARIANT_PADDED || !padded_fits(q)) return 0;
   const PaddedLayout L = padded_layout(q);
   // distinct dummy bases, 16-byte aligned like the copies
@@ -2060,12 +2226,10 @@ int launch_generic(const Problem &q, hipStream_t stream) {
 
 // The vector variants (operands already checked by vector_ok).
 int launch_vector(const Problem &q, int32_t variant, int32_t k_split, Scratch &scr) {
-  hipStream_t s = (hipStream_t)scr.stream;
-  const int cus = scr.st->num_cus;
   switch (variant) {
-    case VT_VARIANT_MFMA_256x256: return launch_mfma<256, 256>(q, s, cus);
-    case VT_VARIANT_MFMA_128x128: return launch_mfma<128, 128>(q, s, cus);
-    case VT_VARIANT_MFMA_256x128: return launch_mfma<256, 128>(q, s, cus);
+    case VT_VARIANT_MFMA_256x256: return launch_mfma<256, 256>(q, scr);
+    case VT_VARIANT_MFMA_128x128: return launch_mfma<128, 128>(q, scr);
+    case VT_VARIANT_MFMA_256x128: return launch_mfma<256, 128>(q, scr);
     case VT_VARIANT_SKINNY: return launch_skinny(q, k_split, scr);
     default: return fail(VT_EINVAL, "variant %d is not a vector variant", (int)variant);
   }
@@ -2133,8 +2297,9 @@ int prepare_gemm(const int8_t *A, const int8_t *B, const int32_t *D, int32_t *C,
                   "variant %s needs N%%16==0, K%%16==0 (K>0), lda/ldb/strides multiples of 16 "
                   "and 16-byte aligned A, B",
                   kVariants[variant].name);
-    if (variant == VT_VARIANT_SKINNY && M > 16)
-      return fail(VT_EUNSUPPORTED, "variant skinny needs M <= 16 (M=%lld)", (long long)M);
+    if (variant == VT_VARIANT_SKINNY && M > kSkinnyMaxM)
+      return fail(VT_EUNSUPPORTED, "variant skinny needs M <= %d (M=%lld)", kSkinnyMaxM,
+                  (long long)M);
     if (variant != VT_VARIANT_SKINNY && !mfma_addressable(q))
       return fail(VT_EUNSUPPORTED,
                   "variant %s needs 256*lda and 64*ldb below 2^32 (lda=%lld ldb=%lld)",
@@ -2160,8 +2325,12 @@ int launch_gemm(const GemmCall &c, Scratch &scr) {
 // Dynamic LDS beyond the default for the kernels that need it.
 void set_kernel_attributes(DeviceState &st) {
   const std::pair<const void *, int> need[] = {
-      {(const void *)skinny_kernel<kSkinnyNB, kSkinnyWaves, kSkinnyU, true>, kMaxSkinnyLds},
-      {(const void *)skinny_kernel<kSkinnyNB, kSkinnyWaves, kSkinnyU, false>, kMaxSkinnyLds},
+      {(const void *)skinny_kernel<kSkinnyNB, kSkinnyWaves, kSkinnyU, 1, true>, kMaxSkinnyLds},
+      {(const void *)skinny_kernel<kSkinnyNB, kSkinnyWaves, kSkinnyU, 1, false>, kMaxSkinnyLds},
+      {(const void *)skinny_kernel<kSkinnyNB, kSkinnyWaves, kSkinnyU, 2, true>, kMaxSkinnyLds},
+      {(const void *)skinny_kernel<kSkinnyNB, kSkinnyWaves, kSkinnyU, 2, false>, kMaxSkinnyLds},
+      {(const void *)skinny_kernel<kSkinnyNB, kSkinnyWaves, kSkinnyU, 4, true>, kMaxSkinnyLds},
+      {(const void *)skinny_kernel<kSkinnyNB, kSkinnyWaves, kSkinnyU, 4, false>, kMaxSkinnyLds},
       {(const void *)replay_kernel, kMaxReplayLds + 256},
   };
   for (const auto &n : need) {
@@ -2385,11 +2554,16 @@ int vt_gemm_check(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int
                         "vt_gemm_check", &c);
   if (rc) return rc;
   if (variant_out) *variant_out = c.empty ? VT_VARIANT_AUTO : c.variant;
-  // The K split that launches: the skinny kernel's slice count; the other
-  // variants take none (padded chooses its own for the padded shape).
+  // The K split that launches: the skinny kernel's slice count, or the MFMA
+  // kernels' (1 reported as 0: no split); padded chooses its own for the
+  // padded shape.
   int32_t ks = 0;
   if (!c.empty && c.variant == VT_VARIANT_SKINNY)
     ks = skinny_geometry<kSkinnyNB, kSkinnyWaves, kSkinnyU>(c.q, c.k_split).ks;
+  else if (!c.empty) {
+    const int mks = mfma_split_for(c.q, c.variant);
+    ks = mks > 1 ? mks : 0;
+  }
   if (k_split_out) *k_split_out = ks;
   if (scratch_bytes_out) *scratch_bytes_out = c.empty ? 0 : scratch_need(c.q, c.variant, c.k_split);
   return VT_OK;
@@ -2491,20 +2665,20 @@ int vt_gemm_i8_packed(const int8_t *A, const int8_t *Bp, const int32_t *D, int32
   scr.st = st;
   scr.stream = stream;
   if (K == 0) return launch_generic(q, (hipStream_t)stream);   // C = D (or 0)
-  // Whole 256-row tiles on the DMA kernel; the rest in groups of 16 rows, each
-  // of which streams B once more.
+  // Whole 256-row tiles on the DMA kernel; the rest in groups of up to 64
+  // rows, each of which streams B once more.
   int64_t r_first = 0;
   if (packed_dma_fits(q)) {
     rc = launch_packed_dma(q, (hipStream_t)stream, st->num_cus);
     if (rc) return rc;
     r_first = M / 256 * 256;
   }
-  for (int64_t r0 = r_first; r0 < M; r0 += 16) {
+  for (int64_t r0 = r_first; r0 < M; r0 += kSkinnyMaxM) {
     Problem g = q;
     g.A = A + r0 * lda;
     g.C = C + r0 * ldc;
     g.D = D ? D + r0 * ldd : nullptr;
-    g.M = M - r0 < 16 ? M - r0 : 16;
+    g.M = M - r0 < kSkinnyMaxM ? M - r0 : kSkinnyMaxM;
     rc = launch_packed_rows(g, k_split, scr);
     if (rc) return rc;
   }

@@ -62,13 +62,13 @@ TILES = {
     # padding granularity: A and B copied with k and n rounded up to 16, the
     # product run on the vector kernel the native selection picks for that shape
     "padded": (16, 16, 16, 256, 0),
-    # 16 rows (groups of 16 for larger m), 4 column blocks, 64-row blocks,
-    # 8 waves, LDS for the cross-wave sums (kPacked* in the HIP source)
-    "skinny_packed": (16, 64, 64, 512, 8 * 4 * 1024),
+    # up to 64 rows (groups of 64 for larger m), 4 column blocks, 64-row
+    # blocks, 8 waves, LDS for the cross-wave sums (kPacked* in the HIP source)
+    "skinny_packed": (64, 64, 64, 512, 8 * 4 * 1024),
 }
 PACKED_WAVES = 8
 DMA_LDS = 4 * (256 * 64 + 64 * 256)   # LDS of the persistent 256x256 kernel (4 stages)
-SKINNY_MAX_M = 16
+SKINNY_MAX_M = 64   # up to 4 row blocks of 16 (kSkinnyMaxM in the HIP source)
 SKINNY_PIPE_ROWS = 64 * 2   # stage rows x stages in flight (kSkinny* in the HIP source)
 LDS_PER_CU = 160 * 1024
 
@@ -101,11 +101,18 @@ def skinny_split(plan):
         ks = _auto_k_split(plan["n"], k, plan["batch"])
     align = SKINNY_PIPE_ROWS
     stage_lds = TILES["skinny"][4]
+    a_rows = 16 * skinny_row_blocks(plan["m"])
     chunk = -(-k // ks)
     chunk = -(-chunk // align) * align
-    if 16 * skinny_a_stride(chunk) + stage_lds > LDS_PER_CU:
-        chunk = ((LDS_PER_CU - stage_lds) // 16 - 48) // align * align
+    if a_rows * skinny_a_stride(chunk) + stage_lds > LDS_PER_CU:
+        chunk = ((LDS_PER_CU - stage_lds) // a_rows - 48) // align * align
     return -(-k // chunk), chunk
+
+
+def skinny_row_blocks(m):
+    """Row blocks of 16 the skinny kernel runs for m rows: 1, 2 or 4
+    (skinny_row_blocks in the HIP source)."""
+    return 1 if m <= 16 else 2 if m <= 32 else 4
 
 
 def skinny_a_stride(k_chunk):
@@ -157,6 +164,32 @@ def packed_split(plan):
     return -(-kbt // per), per
 
 
+def mfma_k_split(plan):
+    """K slices vt_gemm_i8 runs an MFMA plan in (mfma_k_split in the HIP
+    source): a k of at least 1024 over at most 64 tiles (contiguous shared-B
+    batches folded into m) is cut into up to 16 slices of whole 128-deep steps,
+    each at least 512 deep, for up to 256 workgroups; the partial sums are
+    added by a second kernel. 1: no split."""
+    variant = plan["variant"]
+    if not variant.startswith("mfma"):
+        return 1
+    tm, tn = TILES[variant][:2]
+    m, n, k, b = plan["m"], plan["n"], plan["k"], plan["batch"]
+    if plan["b_shared"] and b > 1:
+        m, b = m * b, 1
+    if b != 1 or k < 1024 or n % 16:
+        return 1
+    tiles = -(-m // tm) * -(-n // tn)
+    if tiles * 4 > NUM_CUS:
+        return 1
+    ks = 1
+    while ks < 16 and 2 * ks * tiles <= NUM_CUS:
+        ks *= 2
+    while ks > 1 and (k % (128 * ks) or k // ks < 512):
+        ks //= 2
+    return ks
+
+
 def packed_dma_rows(plan):
     """Rows of a skinny_packed plan that run on the 256x256 MFMA kernel: the
     whole 256-row tiles, when n % 256 == 0, k % 64 == 0 and every lane offset
@@ -193,10 +226,11 @@ def required_resources(plan):
     if variant.startswith("mfma"):
         if plan["b_shared"] and batch > 1:      # stacked-M fold
             m, batch = m * batch, 1
-        return lds, -(-m // tm) * -(-n // tn) * batch
+        return lds, -(-m // tm) * -(-n // tn) * batch * mfma_k_split(plan)
     if variant == "skinny":
         ks, chunk = skinny_split(plan)
-        return lds + 16 * skinny_a_stride(chunk), -(-n // tn) * ks * batch
+        return (lds + 16 * skinny_row_blocks(m) * skinny_a_stride(chunk),
+                -(-n // tn) * ks * batch)
     if variant == PACKED_VARIANT:
         dma, rest = _packed_parts(plan)
         lds_out, wgs = 0, 0
@@ -356,7 +390,9 @@ def modeled_counts(plan):
         tiles_m, tiles_n = -(-m_eff // tm), -(-n // tn)
         # every tile reads its A row-panel and B column-panel once
         c_and_d = 4 * b * m * n * (2 if plan["has_d"] else 1)
-        l2_bytes = b_eff * (tiles_n * m_eff * k + tiles_m * k * n) + c_and_d
+        ks = mfma_k_split(plan)
+        partial = 2 * 4 * ks * m_eff * n if ks > 1 else 0   # written, then read back
+        l2_bytes = b_eff * (tiles_n * m_eff * k + tiles_m * k * n) + c_and_d + partial
     elif variant == "skinny":
         ks, _ = skinny_split(plan)
         partial = 2 * 4 * b * m * n * ks if ks > 1 else 0
@@ -367,9 +403,9 @@ def modeled_counts(plan):
         if rest is not None:
             mr = rest["m"]
             ks, _ = packed_split(rest)
-            groups = -(-mr // 16)
+            groups = -(-mr // SKINNY_MAX_M)
             partial = 2 * 4 * b * mr * n * ks if ks > 1 else 0
-            # B once per 16-row group; each column group reads its A rows once
+            # B once per group of up to 64 rows; each column group reads its A rows once
             l2_bytes += (groups * (b * -(-k // 64) * 64 * n) + b * mr * k * packed_columns(rest)[1]
                          + 4 * b * mr * n * (2 if plan["has_d"] else 1) + partial)
     elif variant == "padded":
@@ -451,7 +487,9 @@ def modeled_objective(plan, counts):
     elif variant == PACKED_VARIANT:
         launches += packed_split(plan)[0] > 1
     else:
-        t = max(t, -(-k // 64) * _SLICE_S)
+        ks = mfma_k_split(plan)
+        launches += ks > 1
+        t = max(t, -(-(k // ks) // 64) * _SLICE_S)
     return (launches * _LAUNCH_S + _ROUND_TRIP_S + t, wgs)
 
 
@@ -492,8 +530,8 @@ def native_check(plan):
         except HipGemmError as exc:
             return False, "%s (fail-closed)" % exc
         rows = packed_dma_rows(plan)
-        how = ("%d rows on the 256x256 kernel, %d in groups of 16" % (rows, m - rows) if rows
-               else "rows in groups of 16")
+        how = ("%d rows on the 256x256 kernel, %d in groups of up to 64" % (rows, m - rows)
+               if rows else "rows in groups of up to 64")
         return True, "accepted: vt_packed_b_size takes k=%d n=%d; runs skinny_packed (%s)" % (
             k, n, how)
     sb = 0 if (plan["b_shared"] or b == 1) else k * n
