@@ -342,16 +342,23 @@ int vt_pack_b_i8(const int8_t *B, int8_t *Bp, int64_t K, int64_t N, int64_t ldb,
  * K % 16 == 0, lda and strides multiples of 16, 16-byte aligned A and Bp.
  * Same extent bounds and overlap refusals as vt_gemm_i8 (Bp counts as
  * batch blocks of vt_packed_b_size bytes; vt_pack_b_i8 likewise refuses a Bp
- * that overlaps B). Any M. When N % 256 == 0, K % 64 == 0 and M >= 256, the
- * rows in whole 256-row tiles run on the 256x256 MFMA kernel of vt_gemm_i8,
- * which then reads each 32 x 32 B operand with one ds_read_b128 (a 1 KiB tile
- * holds 16 consecutive k per lane, the k order of its A operand); the other
- * rows run in groups of up to 64, each group streaming B once for its 1, 2 or
- * 4 row blocks of 16. Columns go to workgroups in groups of 8-column half
- * blocks: whole groups of four 16-column blocks when N gives 192 or more of
- * them, else smaller groups, about one per CU. k_split: workgroups along K
- * for the groups of up to 64 rows (0 = automatic: 1 unless even half-block
- * groups are too few, else a split whose partial sums a second kernel adds).
+ * that overlaps B). Any M. The rows run on three kernels:
+ *   - whole 256-row tiles, when N % 256 == 0, K % 64 == 0 and there are at
+ *     least 128 such tiles over all batches: the persistent 256x256 MFMA
+ *     kernel of vt_gemm_i8, which reads each 32 x 32 B operand with one
+ *     ds_read_b128 (a 1 KiB tile holds 16 consecutive k per lane, the k
+ *     order of its A operand);
+ *   - more than 64 remaining rows: 128 x 128 MFMA tiles reading the packed
+ *     tiles the same way, K split into up to 16 slices (a second kernel adds
+ *     them) when fewer than 64 tiles would run, as vt_gemm_i8 does;
+ *   - up to 64 rows (or tiles whose offsets exceed 32 bits): groups of up to
+ *     64 rows, each group streaming B once for its 1, 2 or 4 row blocks of
+ *     16. Columns go to workgroups in groups of 8-column half blocks: whole
+ *     groups of four 16-column blocks when N gives 192 or more of them, else
+ *     smaller groups, about one per CU.
+ * k_split: workgroups along K for the groups of up to 64 rows (0 =
+ * automatic: 1 unless even half-block groups are too few, else a split whose
+ * partial sums a second kernel adds); the tile kernels choose their own.
  */
 int vt_gemm_i8_packed(const int8_t *A, const int8_t *Bp, const int32_t *D, int32_t *C,
                       int64_t M, int64_t N, int64_t K,

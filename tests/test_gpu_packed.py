@@ -249,19 +249,21 @@ def test_half_block_groups_across_batches(dev):
         assert np.array_equal(C[b], go.gemm_i8(A[b], B[b])), b
 
 
-# Rows in whole 256-row tiles run on the persistent 256x256 DMA kernel with
-# packed B (N % 256 == 0, K % 64 == 0); the rest in groups of 16 rows.
+# Packed rows take one of three kernels: whole 256-row tiles on the persistent
+# 256x256 DMA kernel when N % 256 == 0, K % 64 == 0 and there are at least
+# 128 of them; more than 64 other rows on 128x128 tiles (K split when the grid
+# is small); up to 64 rows in a group on the decode kernel.
 @pytest.mark.parametrize("m,k,n", [(256, 64, 256), (512, 192, 768), (300, 128, 512),
                                    (1024, 1024, 1024), (768, 4160, 256)])
-def test_dma_rows_with_packed_b(dev, m, k, n):
-    say("packed dma", m, k, n)
+def test_tile_rows_with_packed_b(dev, m, k, n):
+    say("packed tiles", m, k, n)
     rng = np.random.default_rng(m + 7 * k + n)
     A = rng.integers(-128, 128, (m, k), dtype=np.int8)
     B = rng.integers(-128, 128, (k, n), dtype=np.int8)
     assert np.array_equal(gpu_gemm_packed(dev, A, B), go.gemm_i8_f64(A, B))
 
 
-def test_dma_rows_with_packed_b_d_in_place(dev):
+def test_tile_rows_with_packed_b_d_in_place(dev):
     m, k, n = 768, 512, 512
     rng = np.random.default_rng(31)
     A = rng.integers(-128, 128, (m, k), dtype=np.int8)
@@ -272,7 +274,7 @@ def test_dma_rows_with_packed_b_d_in_place(dev):
     assert np.array_equal(gpu_gemm_packed(dev, A, B, D, in_place=True), want)
 
 
-def test_dma_rows_with_packed_b_extremes(dev):
+def test_tile_rows_with_packed_b_extremes(dev):
     m, k, n = 256, 8192, 256
     A = np.full((m, k), -128, np.int8)
     B = np.full((k, n), -128, np.int8)
@@ -283,9 +285,9 @@ def test_dma_rows_with_packed_b_extremes(dev):
 
 
 @pytest.mark.parametrize("shared", [True, False])
-def test_dma_rows_with_packed_b_batches(dev, shared):
+def test_tile_rows_with_packed_b_batches(dev, shared):
     rng = np.random.default_rng(41 + shared)
-    batch, m, k, n = 3, 272, 256, 512        # 256 rows per batch on the DMA kernel, 16 in a group
+    batch, m, k, n = 3, 272, 256, 512        # 128x128 tiles; shared B folds the batches
     A = rng.integers(-128, 128, (batch, m, k), dtype=np.int8)
     B = rng.integers(-128, 128, (k, n) if shared else (batch, k, n), dtype=np.int8)
     D = rng.integers(-1000, 1000, (batch, m, n), dtype=np.int32)
@@ -298,7 +300,7 @@ def test_dma_rows_with_packed_b_batches(dev, shared):
         assert np.array_equal(C[b], go.gemm_i8(A[b], Bb, D[b])), b
 
 
-def test_dma_rows_with_packed_b_equal_row_major_config5_shape(dev):
+def test_tile_rows_with_packed_b_equal_row_major_config5_shape(dev):
     """2048^3 on config-5-like data: packed B and row-major B give the same
     full output, which equals the exact float64 product."""
     n = 2048
@@ -337,3 +339,79 @@ def test_row_blocks_with_packed_b_whole_groups(dev):
     c = inputs.config_inputs(4, seed=2, m=16)
     A = np.concatenate([c["A"]] * 4)          # 64 rows
     assert np.array_equal(gpu_gemm_packed(dev, A, c["B"]), go.gemm_i8_f64(A, c["B"]))
+
+
+# 128x128 tiles with packed B: K tails (K % 128 == 64, K % 64 == 16), ragged
+# N (last 128-column tile half live), K split into 2 and 16 slices, D in place.
+@pytest.mark.parametrize("m,k,n", [(65, 4160, 272), (100, 1040, 400), (200, 1024, 64),
+                                   (128, 16384, 1024), (129, 2048, 4096)])
+def test_packed_tiles_edges_and_k_split(dev, m, k, n):
+    plan = hg.make_plan(m, n, k, variant=hg.PACKED_VARIANT)
+    say("packed tiles", m, k, n, hg.native_check(plan)[1])
+    rng = np.random.default_rng(7 * m + k + n)
+    A = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    B = rng.integers(-128, 128, (k, n), dtype=np.int8)
+    D = rng.integers(-2**30, 2**30, (m, n), dtype=np.int32)
+    assert np.array_equal(gpu_gemm_packed(dev, A, B), go.gemm_i8(A, B))
+    assert np.array_equal(gpu_gemm_packed(dev, A, B, D, in_place=True), go.gemm_i8(A, B, D))
+
+
+def test_packed_tiles_k_split_extremes(dev):
+    """128 x 1024 x 16384 (16 K slices) on constant extremes: every partial sum
+    and the reduction at their largest magnitudes."""
+    m, k, n = 128, 16384, 1024
+    A = np.full((m, k), -128, np.int8)
+    B = np.full((k, n), -128, np.int8)
+    assert np.all(gpu_gemm_packed(dev, A, B) == 268435456)
+    A = np.tile(np.array([-128, 127], np.int8), (m, k // 2))
+    B = np.tile(np.array([[127], [-128]], np.int8), (k // 2, n))
+    assert np.array_equal(gpu_gemm_packed(dev, A, B), go.gemm_i8_f64(A, B))
+
+
+@pytest.mark.parametrize("extra", [0, 44, 100])
+def test_dma_rows_with_packed_b(dev, extra):
+    """4096 rows x 2048 columns: 128 whole 256-row tiles on the DMA kernel,
+    then 44 rows in a decode group or 100 rows on 128x128 tiles."""
+    m, k, n = 4096 + extra, 192, 2048
+    plan = hg.make_plan(m, n, k, variant=hg.PACKED_VARIANT)
+    assert hg.packed_dma_rows(plan) == 4096
+    say("packed dma", m, k, n, hg.native_check(plan)[1])
+    rng = np.random.default_rng(300 + extra)
+    A = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    B = rng.integers(-128, 128, (k, n), dtype=np.int8)
+    D = rng.integers(-2**20, 2**20, (m, n), dtype=np.int32)
+    assert np.array_equal(gpu_gemm_packed(dev, A, B), go.gemm_i8_f64(A, B))
+    assert np.array_equal(gpu_gemm_packed(dev, A, B, D, in_place=True), go.gemm_i8(A, B, D))
+
+
+@pytest.mark.parametrize("shared", [True, False])
+def test_dma_rows_with_packed_b_batches(dev, shared):
+    """8 batches of 256 x 4096: 128 tiles over the batches on the DMA kernel."""
+    rng = np.random.default_rng(51 + shared)
+    batch, m, k, n = 8, 256, 128, 4096
+    A = rng.integers(-128, 128, (batch, m, k), dtype=np.int8)
+    B = rng.integers(-128, 128, (k, n) if shared else (batch, k, n), dtype=np.int8)
+    D = rng.integers(-1000, 1000, (batch, m, n), dtype=np.int32)
+    plan = hg.make_plan(m, n, k, batch=batch, b_shared=shared, has_d=True, d_max_abs=1000,
+                        variant=hg.PACKED_VARIANT)
+    assert hg.packed_dma_rows(plan) == 256
+    At, Bt, Dt = to_dev(dev, A), to_dev(dev, B), to_dev(dev, D)
+    C = hg.run(plan, At, hg.pack_b(Bt), Dt).cpu().numpy()
+    for b in range(batch):
+        Bb = B if shared else B[b]
+        assert np.array_equal(C[b], go.gemm_i8(A[b], Bb, D[b])), b
+
+
+def test_packed_tiles_after_dma_rows_in_batches(dev):
+    """2 batches of 4096 + 100 rows, shared packed B: the DMA kernel takes the
+    whole tiles of both batches, then 100 rows of each batch run on 128x128
+    tiles batch by batch (not folded: those rows are not contiguous)."""
+    rng = np.random.default_rng(61)
+    batch, m, k, n = 2, 4196, 128, 2048
+    A = rng.integers(-128, 128, (batch, m, k), dtype=np.int8)
+    B = rng.integers(-128, 128, (k, n), dtype=np.int8)
+    plan = hg.make_plan(m, n, k, batch=batch, b_shared=True, variant=hg.PACKED_VARIANT)
+    At, Bt = to_dev(dev, A), to_dev(dev, B)
+    C = hg.run(plan, At, hg.pack_b(Bt)).cpu().numpy()
+    for b in range(batch):
+        assert np.array_equal(C[b], go.gemm_i8_f64(A[b], B)), b

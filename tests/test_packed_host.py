@@ -83,13 +83,13 @@ def test_packed_plans_validate():
     p = hg.make_plan(40, 2048, 1024, variant=hg.PACKED_VARIANT)
     assert hg.packed_columns(p) == (1, 256) and hg.packed_split(p) == (1, 16)
     # few column groups: split K; up to 64 rows run in one group (row blocks
-    # of 16), more rows as groups of 64
+    # of 16); more rows on 128x128 tiles (one tile, K split in 2 slices of 512)
     p = hg.make_plan(40, 64, 1024, variant=hg.PACKED_VARIANT)
     assert hg.validate_plan(p)[0]
     assert hg.packed_columns(p) == (1, 8)
     assert hg.packed_split(p) == (2, 8)
     assert hg.required_resources(p)[1] == 8 * 2 * 1
-    assert hg.required_resources(dict(p, m=100))[1] == 8 * 2 * 2
+    assert hg.required_resources(dict(p, m=100)) == (hg.TILES["mfma_128x128"][4], 2)
     # fewer than 192 whole groups: one group per CU, down to half a block;
     # at most 8 half blocks (4 tiles) per group; batches share the chip
     assert hg.packed_columns(dict(p, n=4800)) == (3, 200)
@@ -110,26 +110,45 @@ def test_packed_plans_validate():
 
 
 def test_packed_rows_in_whole_tiles_go_to_the_256_kernel():
-    """Rows in whole 256-row tiles run on the 256x256 kernel when n % 256 == 0
-    and k % 64 == 0; the rest in groups of up to 64 (the split packed_dma_fits
-    makes in the library)."""
+    """Rows in whole 256-row tiles run on the 256x256 kernel when n % 256 == 0,
+    k % 64 == 0 and there are at least 128 such tiles; more than 64 other rows
+    on 128x128 tiles; up to 64 in one group on the decode kernel (the split
+    vt_gemm_i8_packed makes in the library)."""
     plan = lambda m, n, k, **kw: hg.make_plan(m, n, k, variant=hg.PACKED_VARIANT, **kw)
+    assert hg.PACKED_DMA_MIN_TILES == 128
     assert hg.packed_dma_rows(plan(8192, 8192, 8192)) == 8192
-    assert hg.packed_dma_rows(plan(300, 512, 128)) == 256
-    assert hg.packed_dma_rows(plan(255, 512, 128)) == 0
-    assert hg.packed_dma_rows(plan(512, 272, 128)) == 0      # n not whole 256 tiles
-    assert hg.packed_dma_rows(plan(512, 512, 80)) == 0       # k not whole 64 slices
+    assert hg.packed_dma_rows(plan(4096 + 44, 2048, 128)) == 4096     # 16 x 8 = 128 tiles
+    assert hg.packed_dma_rows(plan(4096 + 44, 1792, 128)) == 0        # 16 x 7 = 112 tiles
+    assert hg.packed_dma_rows(plan(768, 14336, 4096)) == 768          # 3 x 56 tiles
+    assert hg.packed_dma_rows(plan(512, 14336, 4096)) == 0            # 2 x 56 tiles
+    assert hg.packed_dma_rows(plan(256, 4096, 128, batch=8)) == 256   # 1 x 16 x 8 batches
+    assert hg.packed_dma_rows(plan(300, 512, 128)) == 0               # 2 tiles
+    assert hg.packed_dma_rows(plan(4096, 4352, 80)) == 0              # k not whole 64 slices
     # 16 column blocks of kbt 1 KiB tiles must stay within 32-bit lane offsets
-    assert hg.packed_dma_rows(plan(256, 256, 64 * 262143)) == 256
-    assert hg.packed_dma_rows(plan(256, 256, 64 * 262144)) == 0
+    assert hg.packed_dma_rows(plan(256 * 128, 256, 64 * 262143)) == 256 * 128
+    assert hg.packed_dma_rows(plan(256 * 128, 256, 64 * 262144)) == 0
+    p = plan(4096 + 44, 2048, 128)
+    assert hg.required_resources(p) == (hg.DMA_LDS, 128 + hg.packed_columns(dict(p, m=44))[1])
+    assert "4096 rows on the 256x256 kernel, 44 in a group of up to 64" in hg.native_check(p)[1]
+    p = plan(4096 + 100, 2048, 128)
+    assert hg.required_resources(p) == (hg.DMA_LDS, 128 + 16)
+    assert "4096 rows on the 256x256 kernel, 100 on 128x128 tiles" in hg.native_check(p)[1]
     p = plan(300, 512, 128)
-    assert hg.required_resources(p) == (hg.DMA_LDS, 2 + hg.packed_columns(dict(p, m=44))[1])
-    assert "256 rows on the 256x256 kernel, 44 in groups of up to 64" in hg.native_check(p)[1]
+    assert hg.required_resources(p) == (hg.TILES["mfma_128x128"][4], 3 * 4)
+    assert "300 on 128x128 tiles" in hg.native_check(p)[1]
+    # a batch of rows after the 256-row tiles is not folded into one GEMM
+    dma, rest = hg._packed_parts(plan(4096 + 100, 2048, 1024, batch=2, b_shared=True))
+    assert dma["m"] == 4096 and rest["variant"] == "mfma_128x128" and not rest["b_shared"]
     # 8192^3 packed is modeled as the 256x256 kernel, not as 512 row groups
     big = plan(8192, 8192, 8192)
     t_packed = hg.modeled_objective(big, hg.modeled_counts(big))[0]
     row = hg.make_plan(8192, 8192, 8192, variant="mfma_256x256")
     assert t_packed == pytest.approx(hg.modeled_objective(row, hg.modeled_counts(row))[0])
+    # 512 x 14336 x 4096 packed is modeled as the row-major 128x128 plan
+    mid = plan(512, 14336, 4096)
+    row = hg.make_plan(512, 14336, 4096, variant="mfma_128x128")
+    assert hg.modeled_objective(mid, hg.modeled_counts(mid)) == pytest.approx(
+        hg.modeled_objective(row, hg.modeled_counts(row)))
 
 
 def test_run_refuses_mismatched_packed_operands():

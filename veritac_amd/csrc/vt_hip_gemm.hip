@@ -220,7 +220,15 @@ struct GemmArgs {
 // rows and columns, masked stores); 2 also K not a multiple of 128 (each load
 // checks the K tail). The K checks sit in the k loop, so a ragged M or N
 // alone does not pay for them.
-template <int BM, int BN, int EDGE, bool HAS_D, bool SHORT, bool EARLY_D>
+//
+// PACKED_B: B is in the packed layout of vt_pack_b_i8 (p.B = Bp, p.ldb = kbt,
+// the 64-row blocks per 16-column block; p.sb = the packed batch stride). A
+// 64-deep slice of the tile's B is then BN/16 whole 1 KB tiles, staged into
+// LDS as they are, and each 32x32 B operand is one ds_read_b128 (lane l: the
+// 16 k of column l % 32 that its A operand also holds). Rows past K are zero
+// in the layout, so B needs no K-tail test; columns past N re-read the last
+// 16-column block and are masked at the store.
+template <int BM, int BN, int EDGE, bool HAS_D, bool SHORT, bool EARLY_D, bool PACKED_B = false>
 __global__ __launch_bounds__(256, 1) void gemm_mfma_kernel(GemmArgs p) {
   constexpr int BK = 64;
   constexpr int WTM = BM / 2, WTN = BN / 2;   // wave tile (2x2 waves)
@@ -263,7 +271,7 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma_kernel(GemmArgs p) {
   // offsets within one tile need 32 bits (the host checks BM*lda and
   // BK*ldb), whatever the size of the whole matrix.
   const int8_t *Ab = p.A + bidx * p.sa + (int64_t)m0 * p.lda;
-  const int8_t *Bb = p.B + bidx * p.sb + n0;
+  const int8_t *Bb = p.B + bidx * p.sb + (PACKED_B ? (int64_t)(n0 / 16) * p.ldb * 1024 : (int64_t)n0);
 
   // Per-thread global source offsets for one 64-deep k slice, relative to a
   // wave-uniform base that advances by one slice per step.
@@ -282,12 +290,22 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma_kernel(GemmArgs p) {
   uint32_t b_goff[CB];
 #pragma unroll
   for (int i = 0; i < CB; ++i) {
-    const int row = tid / BCH + (256 / BCH) * i, c = tid % BCH;
-    int tcol = c * 16;
-    if (EDGE) tcol = min(n0 + tcol, N - 16) - n0;
-    b_row[i] = row;
-    b_goff[i] = (uint32_t)((int64_t)row * p.ldb + tcol);
-    b_lds[i] = row * BN + ((c ^ b_swz<BCH>(row)) << 4);
+    if constexpr (PACKED_B) {
+      // chunk l of 1 KB tile t (16-column block n0/16 + t), kept in place
+      const int ch = tid + 256 * i, t = ch >> 6, l = ch & 63;
+      int tb = t;
+      if (EDGE) tb = min(n0 / 16 + t, N / 16 - 1) - n0 / 16;
+      b_row[i] = 0;
+      b_goff[i] = (uint32_t)((int64_t)tb * p.ldb * 1024 + l * 16);
+      b_lds[i] = t * 1024 + l * 16;
+    } else {
+      const int row = tid / BCH + (256 / BCH) * i, c = tid % BCH;
+      int tcol = c * 16;
+      if (EDGE) tcol = min(n0 + tcol, N - 16) - n0;
+      b_row[i] = row;
+      b_goff[i] = (uint32_t)((int64_t)row * p.ldb + tcol);
+      b_lds[i] = row * BN + ((c ^ b_swz<BCH>(row)) << 4);
+    }
   }
 
   const int KT = (K + BK - 1) / BK;
@@ -298,7 +316,7 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma_kernel(GemmArgs p) {
   auto load_slice = [&](int kt, v4i *ra, v4i *rb) {
     const int k0 = min(kt, KT - 1) * BK;
     const int8_t *abase = Ab + k0;
-    const int8_t *bbase = Bb + (int64_t)k0 * p.ldb;
+    const int8_t *bbase = Bb + (PACKED_B ? (int64_t)(k0 / BK) * 1024 : (int64_t)k0 * p.ldb);
 #pragma unroll
     for (int i = 0; i < CA; ++i) {
       if (EDGE == 2 && kt * BK + a_k[i] >= K) {
@@ -309,7 +327,7 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma_kernel(GemmArgs p) {
     }
 #pragma unroll
     for (int i = 0; i < CB; ++i) {
-      if (EDGE == 2 && k0 + b_row[i] >= K) {
+      if (!PACKED_B && EDGE == 2 && k0 + b_row[i] >= K) {
         // rows past K: re-read row K-1 (A is zero there)
         rb[i] = *(const v4i *)(Bb + (int64_t)(K - 1 - b_row[i]) * p.ldb + b_goff[i]);
       } else {
@@ -347,9 +365,14 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma_kernel(GemmArgs p) {
   for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
     for (int ni = 0; ni < NI; ++ni) {
-      const int nc = (wn * WTN + ni * 32) / 16 + (g & 1);
-      const int r0 = ks * 32 + (g >> 1) * 16 + (j >> 1);
-      b_frag[ks][ni] = r0 * BN + ((nc ^ b_swz<BCH>(r0)) << 4) + (j & 1) * 8;
+      if constexpr (PACKED_B) {
+        const int t = (wn * WTN + ni * 32) / 16 + ((lane & 31) >> 4);
+        b_frag[ks][ni] = t * 1024 + (16 * (2 * ks + (lane >> 5)) + (lane & 15)) * 16;
+      } else {
+        const int nc = (wn * WTN + ni * 32) / 16 + (g & 1);
+        const int r0 = ks * 32 + (g >> 1) * 16 + (j >> 1);
+        b_frag[ks][ni] = r0 * BN + ((nc ^ b_swz<BCH>(r0)) << 4) + (j & 1) * 8;
+      }
     }
 
   // Fragments of one 32-deep k step: MI A blocks and NI B blocks.
@@ -361,9 +384,13 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma_kernel(GemmArgs p) {
     for (int mi = 0; mi < MI; ++mi) fa[mi] = ld_lds_b128(As, a_frag[ks][mi]);
 #pragma unroll
     for (int ni = 0; ni < NI; ++ni) {
-      const v2i lo = ld_lds_tr8(Bs, b_frag[ks][ni]);
-      const v2i hi = ld_lds_tr8(Bs, b_frag[ks][ni] + 8 * BN);
-      fb[ni] = v4i{lo.x, lo.y, hi.x, hi.y};
+      if constexpr (PACKED_B) {
+        fb[ni] = ld_lds_b128(Bs, b_frag[ks][ni]);
+      } else {
+        const v2i lo = ld_lds_tr8(Bs, b_frag[ks][ni]);
+        const v2i hi = ld_lds_tr8(Bs, b_frag[ks][ni] + 8 * BN);
+        fb[ni] = v4i{lo.x, lo.y, hi.x, hi.y};
+      }
     }
   };
   auto mfma_block = [&](const v4i *fa, const v4i *fb) {
@@ -420,7 +447,7 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma_kernel(GemmArgs p) {
   lds_barrier();
   read_frags(0, 0, fa0, fb0);
   int b0 = 0, b1 = 1, b2 = 2;   // buffers of slices kt, kt+1, kt+2
-  constexpr int NMFMA = MI * NI, NREAD = MI + 2 * NI, NSTORE = CA + CB;
+  constexpr int NMFMA = MI * NI, NREAD = MI + (PACKED_B ? 1 : 2) * NI, NSTORE = CA + CB;
   auto step = [&](int kt, v4i *ra, v4i *rb) {
     // First half step: fragments of k 32..63 load under the MFMAs of k 0..31.
     read_frags(b0, 1, fa1, fb1);
@@ -1625,18 +1652,18 @@ int select_variant(const Problem &q, bool vec, int32_t *variant, int32_t *k_spli
 // Waves per workgroup of the persistent full-tile kernel.
 constexpr int kDmaWaves = 4;
 
-template <int BM, int BN, int EDGE, bool HAS_D>
+template <int BM, int BN, int EDGE, bool HAS_D, bool PACKED>
 void launch_mfma_kernel(bool short_k, bool early_d, dim3 grid, dim3 block, hipStream_t stream,
                         const GemmArgs &a) {
   if constexpr (HAS_D) {
     if (early_d) {
-      if (short_k) hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, EDGE, true, true, true>), grid, block, 0, stream, a);
-      else hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, EDGE, true, false, true>), grid, block, 0, stream, a);
+      if (short_k) hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, EDGE, true, true, true, PACKED>), grid, block, 0, stream, a);
+      else hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, EDGE, true, false, true, PACKED>), grid, block, 0, stream, a);
       return;
     }
   }
-  if (short_k) hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, EDGE, HAS_D, true, false>), grid, block, 0, stream, a);
-  else hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, EDGE, HAS_D, false, false>), grid, block, 0, stream, a);
+  if (short_k) hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, EDGE, HAS_D, true, false, PACKED>), grid, block, 0, stream, a);
+  else hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, EDGE, HAS_D, false, false, PACKED>), grid, block, 0, stream, a);
 }
 
 // Contiguous shared-B batches as one GEMM with stacked M.
@@ -1684,20 +1711,28 @@ int mfma_split_for(const Problem &q, int32_t variant) {
   }
 }
 
-template <int BM, int BN>
+// Packed B on 128x128 MFMA tiles: lane offsets from a tile's base within 32
+// bits (A: 256 rows of lda; packed B: 8 column blocks of kbt 1 KB tiles).
+bool packed_tiles_fit(const Problem &q) {
+  return (__int128)256 * q.lda < (1ll << 32) - 4096 &&
+         (__int128)8 * 1024 * ((q.K + 63) / 64) < (1ll << 32) - 4096;
+}
+
+template <int BM, int BN, bool PACKED = false>
 int launch_mfma_tiles(const Problem &r, hipStream_t stream, int num_cus);
 
-template <int BM, int BN>
+// PACKED: B is packed (r.B = Bp, r.ldb = kbt, r.sb = the packed batch stride).
+template <int BM, int BN, bool PACKED = false>
 int launch_mfma(const Problem &q, Scratch &scr) {
   const Problem r = mfma_fold(q);
-  if (!mfma_addressable(r))
+  if (PACKED ? !packed_tiles_fit(r) : !mfma_addressable(r))
     return fail(VT_EUNSUPPORTED,
                 "MFMA variants need 256*lda and 64*ldb below 2^32 (lda=%lld ldb=%lld)",
                 (long long)r.lda, (long long)r.ldb);
   hipStream_t stream = (hipStream_t)scr.stream;
   const int num_cus = scr.st->num_cus;
   const int ks = mfma_k_split<BM, BN>(r);
-  if (ks == 1) return launch_mfma_tiles<BM, BN>(r, stream, num_cus);
+  if (ks == 1) return launch_mfma_tiles<BM, BN, PACKED>(r, stream, num_cus);
   // K slices as batches: slice i reads A columns and B rows [i*kc, (i+1)*kc)
   // and writes its partial sums to slice i of the workspace.
   void *w = nullptr;
@@ -1708,13 +1743,13 @@ int launch_mfma(const Problem &q, Scratch &scr) {
   sl.K = kc;
   sl.batch = ks;
   sl.sa = kc;
-  sl.sb = kc * r.ldb;
+  sl.sb = PACKED ? kc / 64 * 1024 : kc * r.ldb;   // packed: the slice's first 64-row block
   sl.D = nullptr;
   sl.sd = 0;
   sl.C = (int32_t *)w;
   sl.ldc = r.N;
   sl.sc = r.M * r.N;
-  rc = launch_mfma_tiles<BM, BN>(sl, stream, num_cus);
+  rc = launch_mfma_tiles<BM, BN, PACKED>(sl, stream, num_cus);
   if (rc) return rc;
   ReduceArgs ra;
   ra.ws = (const int32_t *)w; ra.D = r.D; ra.C = r.C;
@@ -1728,7 +1763,7 @@ int launch_mfma(const Problem &q, Scratch &scr) {
   return VT_OK;
 }
 
-template <int BM, int BN>
+template <int BM, int BN, bool PACKED>
 int launch_mfma_tiles(const Problem &r, hipStream_t stream, int num_cus) {
   GemmArgs a;
   a.A = r.A; a.B = r.B; a.D = r.D; a.C = r.C;
@@ -1743,7 +1778,7 @@ int launch_mfma_tiles(const Problem &r, hipStream_t stream, int num_cus) {
   const bool has_d = r.D != nullptr;
   dim3 grid((unsigned)blocks), block(256);
   a.batch_count = (int)r.batch;
-  if (BM == 256 && BN == 256 && !(r.M % BM) && !(r.N % BN) && !(r.K % 64)) {
+  if (!PACKED && BM == 256 && BN == 256 && !(r.M % BM) && !(r.N % BN) && !(r.K % 64)) {
     // Persistent: one workgroup per CU (the kernel's LDS allows no more).
     const int64_t g = blocks < num_cus ? blocks : num_cus;
     dim3 pgrid((unsigned)g);
@@ -1756,14 +1791,14 @@ int launch_mfma_tiles(const Problem &r, hipStream_t stream, int num_cus) {
   const bool short_k = r.K <= 128;
   const bool early_d = blocks <= num_cus;   // one workgroup per CU: occupancy costs nothing
   if (edge == 2) {
-    if (has_d) launch_mfma_kernel<BM, BN, 2, true>(short_k, early_d, grid, block, stream, a);
-    else launch_mfma_kernel<BM, BN, 2, false>(short_k, early_d, grid, block, stream, a);
+    if (has_d) launch_mfma_kernel<BM, BN, 2, true, PACKED>(short_k, early_d, grid, block, stream, a);
+    else launch_mfma_kernel<BM, BN, 2, false, PACKED>(short_k, early_d, grid, block, stream, a);
   } else if (edge == 1) {
-    if (has_d) launch_mfma_kernel<BM, BN, 1, true>(short_k, early_d, grid, block, stream, a);
-    else launch_mfma_kernel<BM, BN, 1, false>(short_k, early_d, grid, block, stream, a);
+    if (has_d) launch_mfma_kernel<BM, BN, 1, true, PACKED>(short_k, early_d, grid, block, stream, a);
+    else launch_mfma_kernel<BM, BN, 1, false, PACKED>(short_k, early_d, grid, block, stream, a);
   } else {
-    if (has_d) launch_mfma_kernel<BM, BN, 0, true>(short_k, early_d, grid, block, stream, a);
-    else launch_mfma_kernel<BM, BN, 0, false>(short_k, early_d, grid, block, stream, a);
+    if (has_d) launch_mfma_kernel<BM, BN, 0, true, PACKED>(short_k, early_d, grid, block, stream, a);
+    else launch_mfma_kernel<BM, BN, 0, false, PACKED>(short_k, early_d, grid, block, stream, a);
   }
   VT_HIP_CHECK(hipGetLastError());
   return VT_OK;
@@ -1898,6 +1933,13 @@ bool packed_dma_fits(const Problem &q) {
   return q.M >= 256 && q.N % 256 == 0 && q.K % 64 == 0 && q.K > 0 &&
          256 * q.lda < (1ll << 32) - 4096 && 16 * 1024 * packed_kbt(q.K) < (1ll << 32) - 4096;
 }
+
+// Whole 256-row tiles of a packed-B GEMM go to the persistent 256x256 DMA
+// kernel when there are at least this many of them (over all batches); fewer
+// run faster as 128x128 tiles (N = 14336, K = 4096: 512 rows, 112 tiles,
+// 46.6 us on the DMA kernel against 43.2 us; 768 rows, 168 tiles, 55.1 us
+// against 63.4 us).
+constexpr int64_t kPackedDmaMinTiles = 128;
 
 // Rows [0, 256 * (M / 256)) of a packed-B GEMM on the persistent 256x256 DMA
 // kernel, every batch in one launch.
@@ -2665,13 +2707,24 @@ int vt_gemm_i8_packed(const int8_t *A, const int8_t *Bp, const int32_t *D, int32
   scr.st = st;
   scr.stream = stream;
   if (K == 0) return launch_generic(q, (hipStream_t)stream);   // C = D (or 0)
-  // Whole 256-row tiles on the DMA kernel; the rest in groups of up to 64
-  // rows, each of which streams B once more.
+  // Whole 256-row tiles on the persistent DMA kernel when there are enough of
+  // them; more than 64 remaining rows on 128x128 tiles; up to 64 rows, or
+  // tiles whose offsets do not fit 32 bits, in groups of up to 64 rows on the
+  // decode kernel, each group streaming B once.
   int64_t r_first = 0;
-  if (packed_dma_fits(q)) {
+  if (packed_dma_fits(q) && M / 256 * (N / 256) * batch >= kPackedDmaMinTiles) {
     rc = launch_packed_dma(q, (hipStream_t)stream, st->num_cus);
     if (rc) return rc;
     r_first = M / 256 * 256;
+  }
+  if (M - r_first > kSkinnyMaxM && packed_tiles_fit(q)) {
+    Problem g = q;
+    g.A = A + r_first * lda;
+    g.C = C + r_first * ldc;
+    g.D = D ? D + r_first * ldd : nullptr;
+    g.M = M - r_first;
+    g.ldb = packed_kbt(K);
+    return launch_mfma<128, 128, true>(g, scr);
   }
   for (int64_t r0 = r_first; r0 < M; r0 += kSkinnyMaxM) {
     Problem g = q;

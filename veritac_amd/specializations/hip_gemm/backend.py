@@ -190,26 +190,48 @@ def mfma_k_split(plan):
     return ks
 
 
+PACKED_DMA_MIN_TILES = 128   # kPackedDmaMinTiles in the HIP source
+
+
 def packed_dma_rows(plan):
     """Rows of a skinny_packed plan that run on the 256x256 MFMA kernel: the
-    whole 256-row tiles, when n % 256 == 0, k % 64 == 0 and every lane offset
-    from a tile's base fits 32 bits (contiguous A: 256 * k; packed B: 16
-    column blocks of kbt 1 KiB tiles). The other rows run in groups of 16.
-    Mirrors packed_dma_fits in csrc/vt_hip_gemm.hip."""
-    m, n, k = plan["m"], plan["n"], plan["k"]
+    whole 256-row tiles, when n % 256 == 0, k % 64 == 0, there are at least
+    PACKED_DMA_MIN_TILES of them over all batches, and every lane offset from
+    a tile's base fits 32 bits (contiguous A: 256 * k; packed B: 16 column
+    blocks of kbt 1 KiB tiles). Mirrors packed_dma_fits and vt_gemm_i8_packed
+    in csrc/vt_hip_gemm.hip."""
+    m, n, k, batch = plan["m"], plan["n"], plan["k"], plan["batch"]
     kbt = -(-k // 64)
     if (m >= 256 and n % 256 == 0 and k % 64 == 0 and k > 0 and 256 * k < 2**32 - 4096
-            and 16 * 1024 * kbt < 2**32 - 4096):
+            and 16 * 1024 * kbt < 2**32 - 4096
+            and m // 256 * (n // 256) * batch >= PACKED_DMA_MIN_TILES):
         return m // 256 * 256
     return 0
 
 
+def packed_tiles_fit(plan):
+    """Whether packed rows can run on 128x128 MFMA tiles: lane offsets from a
+    tile's base within 32 bits (contiguous A: 256 * k; packed B: 8 column
+    blocks of kbt 1 KiB tiles). packed_tiles_fit in the HIP source."""
+    k = plan["k"]
+    return 256 * k < 2**32 - 4096 and 8 * 1024 * -(-k // 64) < 2**32 - 4096
+
+
 def _packed_parts(plan):
-    """(plan of the rows on the 256x256 kernel or None, plan of the rows in
-    groups of 16 or None) of a skinny_packed plan."""
+    """(plan of the rows on the 256x256 kernel or None, plan of the other
+    rows or None) of a skinny_packed plan. More than SKINNY_MAX_M other rows
+    run as 128x128 MFMA tiles (variant mfma_128x128); up to that many, in one
+    group on the packed decode kernel (variant skinny_packed)."""
     rows = packed_dma_rows(plan)
     dma = dict(plan, m=rows, variant="mfma_256x256", k_split=0) if rows else None
-    rest = dict(plan, m=plan["m"] - rows) if plan["m"] > rows else None
+    rest = None
+    if plan["m"] > rows:
+        rest = dict(plan, m=plan["m"] - rows)
+        if rest["m"] > SKINNY_MAX_M and packed_tiles_fit(plan):
+            # after the 256-row tiles the batches are no longer contiguous
+            # blocks of rows, so the library does not fold them into one GEMM
+            rest = dict(rest, variant="mfma_128x128", k_split=0,
+                        b_shared=plan["b_shared"] and not rows)
     return dma, rest
 
 
@@ -236,7 +258,10 @@ def required_resources(plan):
         lds_out, wgs = 0, 0
         if dma is not None:
             lds_out, wgs = DMA_LDS, min(required_resources(dma)[1], NUM_CUS)
-        if rest is not None:
+        if rest is not None and rest["variant"] != PACKED_VARIANT:
+            lds_r, wgs_r = required_resources(rest)
+            lds_out, wgs = max(lds_out, lds_r), wgs + wgs_r
+        elif rest is not None:
             ks, _ = packed_split(rest)
             lds_out = max(lds_out, lds)
             wgs += packed_columns(rest)[1] * ks * batch * -(-rest["m"] // tm)
@@ -400,7 +425,9 @@ def modeled_counts(plan):
     elif variant == PACKED_VARIANT:
         dma, rest = _packed_parts(plan)
         l2_bytes = modeled_counts(dma)["bytes_l2_modeled"] if dma is not None else 0
-        if rest is not None:
+        if rest is not None and rest["variant"] != PACKED_VARIANT:
+            l2_bytes += modeled_counts(rest)["bytes_l2_modeled"]
+        elif rest is not None:
             mr = rest["m"]
             ks, _ = packed_split(rest)
             groups = -(-mr // SKINNY_MAX_M)
@@ -459,14 +486,16 @@ def modeled_objective(plan, counts):
         copy_a, copy_b, copy_c = _padded_copies(plan)
         launches = int(copy_a or copy_b) + int(copy_c)
         return (t_inner + _padded_copy_bytes(plan, inner) / PEAK_HBM_BYTES + launches * _LAUNCH_S, wgs)
-    if variant == PACKED_VARIANT and packed_dma_rows(plan):
-        # the 256-row tiles on the 256x256 kernel, then the rest in groups of 16
-        t, wgs = 0.0, 0
-        for part in _packed_parts(plan):
-            if part is not None:
+    if variant == PACKED_VARIANT:
+        parts = [p for p in _packed_parts(plan) if p is not None]
+        if any(p["variant"] != PACKED_VARIANT for p in parts):
+            # 256-row tiles on the 256x256 kernel and / or 128x128 tiles, and
+            # at most one group on the decode kernel: launches in sequence
+            t, wgs = 0.0, 0
+            for part in parts:
                 tp, wp = modeled_objective(part, modeled_counts(part))
                 t, wgs = t + tp, wgs + wp
-        return t, wgs
+            return t, wgs
     tm, tn = TILES[variant][:2]
     if variant.startswith("mfma") and plan["b_shared"] and b > 1:
         m, b = m * b, 1
@@ -529,9 +558,15 @@ def native_check(plan):
             _lib.packed_b_size(k, n)
         except HipGemmError as exc:
             return False, "%s (fail-closed)" % exc
-        rows = packed_dma_rows(plan)
-        how = ("%d rows on the 256x256 kernel, %d in groups of up to 64" % (rows, m - rows)
-               if rows else "rows in groups of up to 64")
+        dma, rest = _packed_parts(plan)
+        how = []
+        if dma is not None:
+            how.append("%d rows on the 256x256 kernel" % dma["m"])
+        if rest is not None and rest["variant"] != PACKED_VARIANT:
+            how.append("%d on 128x128 tiles" % rest["m"])
+        elif rest is not None:
+            how.append("%d in a group of up to 64" % rest["m"])
+        how = ", ".join(how)
         return True, "accepted: vt_packed_b_size takes k=%d n=%d; runs skinny_packed (%s)" % (
             k, n, how)
     sb = 0 if (plan["b_shared"] or b == 1) else k * n
