@@ -42,7 +42,8 @@ N_SETS = 5
 DECODE_SETS = 10
 # HBM bytes per launch from the rocprofv3 FETCH_SIZE / WRITE_SIZE runs kept under
 # profiles/ (FETCH_SIZE scaled by 2.00, WRITE_SIZE by 1.00: the factors a plain
-# 1 GiB copy gives). Update them with the kernels.
+# 1 GiB copy gives). tests/test_traffic_profiles.py checks them against those
+# summaries, so a refreshed profile and these figures cannot drift apart.
 TRAFFIC_GEMM_8192 = {"read": 805.6e6, "written": 269.2e6}
 TRAFFIC_DECODE = {  # (packed B, M) -> bytes per step
     (False, 16): {"read": 58.9e6 + 3.7e6, "written": 3.95e6 + 0.92e6},
