@@ -44,7 +44,7 @@ DECODE_SETS = 10
 # profiles/ (FETCH_SIZE scaled by 2.00, WRITE_SIZE by 1.00: the factors a plain
 # 1 GiB copy gives). tests/test_traffic_profiles.py checks them against those
 # summaries, so a refreshed profile and these figures cannot drift apart.
-TRAFFIC_GEMM_8192 = {"read": 805.6e6, "written": 269.2e6}
+TRAFFIC_GEMM_8192 = {"read": 805.6e6, "written": 292.6e6}   # gemm_dma16_kernel
 TRAFFIC_DECODE = {  # (packed B, M) -> bytes per step
     (False, 16): {"read": 58.9e6 + 3.7e6, "written": 3.95e6 + 0.92e6},
     (True, 16): {"read": 59.3e6, "written": 0.92e6},
@@ -660,14 +660,55 @@ def bench_gemm_operands(dev, steps, warmup):
     return {"workload": "gemm 8192^3 by operand distribution", "steps": steps, "results": out}
 
 
-# Register-only MFMA loop: each wave multiplies 4 A and 4 B fragments of
-# config-5 bytes (16 per lane, straight from the 8192^3 operands) into the same
-# 4 x 4 block of v_mfma_i32_32x32x32_i8 accumulators the GEMM's waves hold,
-# rotating the A fragments every sweep so consecutive sweeps see different
-# data; no memory traffic in the loop. Wave 0 of each workgroup records the
-# core clock counter (s_memtime) and the 100 MHz real-time counter
-# (s_memrealtime) around the loop, which gives the effective clock.
-MFMA_CEILING_SRC = r"""
+# Register-only MFMA loops on config-5 bytes (16 per lane, straight from the
+# 8192^3 operands), no memory traffic in the loop, each wave holding the same
+# 128 x 128 block of accumulators the GEMM's waves hold:
+#   16x16x64: 8 x 8 v_mfma_i32_16x16x64_i8 accumulators (the headline kernel's
+#     instruction), A fragments rotated every sweep;
+#   32x32x32: 4 x 4 v_mfma_i32_32x32x32_i8 accumulators (the instruction of the
+#     kernel that takes K not a multiple of 256).
+# Wave 0 of each workgroup records the core clock counter (s_memtime) and the
+# 100 MHz real-time counter (s_memrealtime) around the loop, which gives the
+# effective clock.
+MFMA_CEILING_SRC = {
+    "16x16x64": (r"""
+typedef int v4i __attribute__((ext_vector_type(4)));
+extern "C" __global__ __launch_bounds__(256, 1) void mfma_ceiling(
+    const v4i *a_frags, const v4i *b_frags, int iters, long long *clocks, int *sink) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int slot = (blockIdx.x * 4 + wave) & 255;
+  v4i fa[8], fb[8];
+  for (int i = 0; i < 8; ++i) {
+    fa[i] = a_frags[(slot * 8 + i) * 64 + lane];
+    fb[i] = b_frags[(slot * 8 + i) * 64 + lane];
+  }
+  v4i acc[8][8];
+  for (int a = 0; a < 8; ++a)
+    for (int b = 0; b < 8; ++b) acc[a][b] = v4i{0, 0, 0, 0};
+  const long long t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int a = 0; a < 8; ++a)
+#pragma unroll
+      for (int b = 0; b < 8; ++b)
+        acc[a][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[a], fb[b], acc[a][b], 0, 0, 0);
+    const v4i t = fa[0];
+    for (int a = 0; a < 7; ++a) fa[a] = fa[a + 1];
+    fa[7] = t;
+  }
+  int sum = 0;
+  for (int a = 0; a < 8; ++a)
+    for (int b = 0; b < 8; ++b)
+      for (int e = 0; e < 4; ++e) sum += acc[a][b][e];
+  const long long t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+  if (wave == 0 && lane == 0) {
+    clocks[blockIdx.x * 2] = t1 - t0;
+    clocks[blockIdx.x * 2 + 1] = r1 - r0;
+  }
+  if (sum == 0x7eadbeef) sink[0] = sum;
+}
+""", 64 * 16 * 16 * 64 * 2),
+    "32x32x32": (r"""
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 extern "C" __global__ __launch_bounds__(256, 1) void mfma_ceiling(
@@ -676,8 +717,8 @@ extern "C" __global__ __launch_bounds__(256, 1) void mfma_ceiling(
   const int slot = (blockIdx.x * 4 + wave) & 255;
   v4i fa[4], fb[4];
   for (int i = 0; i < 4; ++i) {
-    fa[i] = a_frags[(slot * 4 + i) * 64 + lane];
-    fb[i] = b_frags[(slot * 4 + i) * 64 + lane];
+    fa[i] = a_frags[(slot * 8 + i) * 64 + lane];
+    fb[i] = b_frags[(slot * 8 + i) * 64 + lane];
   }
   v16i acc[4][4];
   for (int a = 0; a < 4; ++a)
@@ -704,28 +745,19 @@ extern "C" __global__ __launch_bounds__(256, 1) void mfma_ceiling(
   }
   if (sum == 0x7eadbeef) sink[0] = sum;
 }
-"""
+""", 16 * 32 * 32 * 32 * 2),
+}
 
 
-def bench_mfma_ceiling(dev, steps, warmup, iters=20000):
-    """The power-limited ceiling of the MFMA pipes on config-5 data: TOPS of
-    a register-only v_mfma_i32_32x32x32_i8 loop (256 workgroups x 4 waves,
-    one per SIMD, the GEMM's 4 x 4 accumulator block per wave) and its
-    effective clock, so the GEMM's roofline fraction can be read against
-    what the board sustains on the same bytes."""
+def _ceiling_run(dev, shape, a_frags, b_frags, steps, warmup, iters):
     import ctypes
     import numpy as np
     import torch
     from veritac_amd import _lib
-    from veritac_amd.specializations.hip_gemm import inputs
-    c = inputs.config_inputs(5, seed=0)
-    # 256 slots x 4 fragments x 64 lanes x 16 bytes from the operands' first rows
-    frag_bytes = 256 * 4 * 64 * 16
-    a_frags = torch.from_numpy(np.ascontiguousarray(c["A"].reshape(-1)[:frag_bytes])).to(dev)
-    b_frags = torch.from_numpy(np.ascontiguousarray(c["B"].reshape(-1)[:frag_bytes])).to(dev)
+    src, ops_per_iter = MFMA_CEILING_SRC[shape]
     clocks = torch.zeros(256 * 2, dtype=torch.int64, device=dev)
     sink = torch.zeros(1, dtype=torch.int32, device=dev)
-    prog = _lib.RtcProgram(MFMA_CEILING_SRC, "mfma_ceiling")
+    prog = _lib.RtcProgram(src, "mfma_ceiling")
     stream = torch.cuda.current_stream(dev)
     args = [ctypes.c_void_p(a_frags.data_ptr()), ctypes.c_void_p(b_frags.data_ptr()),
             ctypes.c_int(iters), ctypes.c_void_p(clocks.data_ptr()),
@@ -744,16 +776,37 @@ def bench_mfma_ceiling(dev, steps, warmup, iters=20000):
         ghz = float(np.median(ck[:, 0] / (ck[:, 1] / 100e6)) / 1e9)
         runs.append((e0.elapsed_time(e1), ghz))
     prog.close()
-    ops = 256.0 * 4 * iters * 16 * 2 * 32 * 32 * 32
     ms = statistics.median(r[0] for r in runs)
     ghz = statistics.median(r[1] for r in runs)
-    tops = ops / (ms / 1e3) / 1e12
-    return {"workload": "register-only v_mfma_i32_32x32x32_i8 loop on config-5 bytes",
-            "tops": tops, "frac_of_int8_peak": tops / PEAK_TOPS, "kernel_ms": ms,
+    tops = 256.0 * 4 * iters * ops_per_iter / (ms / 1e3) / 1e12
+    return {"tops": tops, "frac_of_int8_peak": tops / PEAK_TOPS, "kernel_ms": ms,
             "effective_clock_ghz": ghz,
-            "mfma_utilisation_at_that_clock": tops / (256 * ghz * 8192 / 1e3),
-            "runs": steps, "iters": iters,
-            "timing": "HIP events per launch; clock from s_memtime / s_memrealtime (100 MHz)"}
+            "mfma_utilisation_at_that_clock": tops / (256 * ghz * 8192 / 1e3)}
+
+
+def bench_mfma_ceiling(dev, steps, warmup, iters=10000):
+    """The power-limited ceiling of the MFMA pipes on config-5 data: TOPS of
+    a register-only v_mfma_i32_16x16x64_i8 loop (the headline kernel's
+    instruction; 256 workgroups x 4 waves, one per SIMD, the GEMM's 128 x 128
+    accumulator block per wave) and its effective clock, so the GEMM's
+    roofline fraction can be read against what the board sustains on the same
+    bytes; the same for v_mfma_i32_32x32x32_i8 beside it."""
+    import numpy as np
+    import torch
+    from veritac_amd.specializations.hip_gemm import inputs
+    c = inputs.config_inputs(5, seed=0)
+    # 256 slots x 8 fragments x 64 lanes x 16 bytes from the operands' first rows
+    frag_bytes = 256 * 8 * 64 * 16
+    a_frags = torch.from_numpy(np.ascontiguousarray(c["A"].reshape(-1)[:frag_bytes])).to(dev)
+    b_frags = torch.from_numpy(np.ascontiguousarray(c["B"].reshape(-1)[:frag_bytes])).to(dev)
+    main = _ceiling_run(dev, "16x16x64", a_frags, b_frags, steps, warmup, iters)
+    # a 32x32x32 sweep is half the work of a 16x16x64 sweep
+    other = _ceiling_run(dev, "32x32x32", a_frags, b_frags, steps, warmup, 2 * iters)
+    main.update({"workload": "register-only v_mfma_i32_16x16x64_i8 loop on config-5 bytes",
+                 "runs": steps, "iters": iters,
+                 "timing": "HIP events per launch; clock from s_memtime / s_memrealtime (100 MHz)",
+                 "v_mfma_i32_32x32x32_i8": other})
+    return main
 
 
 def bench_copy(dev, steps, warmup):
@@ -911,7 +964,7 @@ def main():
                      "frac": achieved / PEAK_TOPS,
                      "traffic": TRAFFIC_GEMM_8192["read"] + TRAFFIC_GEMM_8192["written"],
                      "traffic_split": TRAFFIC_GEMM_8192,
-                     "kernel": "gemm_dma_kernel (256x256, persistent)", "kernel_avg_ms": avg_ms,
+                     "kernel": "gemm_dma16_kernel (256x256, persistent, v_mfma_i32_16x16x64_i8)", "kernel_avg_ms": avg_ms,
                      "kernel_min_ms": min(durs), "kernel_median_ms": statistics.median(durs),
                      "kernel_p90_ms": sorted(durs)[min(len(durs) - 1, int(0.9 * len(durs)))],
                      "ops_per_launch": ops},

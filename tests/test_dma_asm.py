@@ -74,3 +74,87 @@ def test_k_loop_waits_are_the_kernels_own(asm, kind):
     # the next step's early fragment reads
     assert loop[-2:] == ["s_waitcnt vmcnt(8) lgkmcnt(%d)" % nunit, "s_barrier"]
     assert not [l for l in loop if re.match(r"s_waitcnt .*vmcnt\(0\)", l)]
+
+
+# gemm_dma16_kernel<HAS_D, PACKED_B>: the same DMA discipline, plus MFMAs
+# issued as inline asm (v_mfma_i32_16x16x64_i8 accumulating in place in
+# AGPRs), whose hazards the compiler does not check. The kernel fences them
+# itself: s_nop 7 pairs between the accumulators' zeroing (v_accvgpr_write)
+# and the next MFMA, and three s_nop 7 between the last MFMA of a tile and
+# the epilogue's reads of the AGPRs.
+KERNELS16 = {"no_d": "_ZN12_GLOBAL__N_117gemm_dma16_kernelILb0ELb0EEEvNS_8GemmArgsE",
+             "with_d": "_ZN12_GLOBAL__N_117gemm_dma16_kernelILb1ELb0EEEvNS_8GemmArgsE",
+             "packed_b": "_ZN12_GLOBAL__N_117gemm_dma16_kernelILb0ELb1EEEvNS_8GemmArgsE",
+             "packed_b_with_d": "_ZN12_GLOBAL__N_117gemm_dma16_kernelILb1ELb1EEEvNS_8GemmArgsE"}
+
+
+def instructions(asm, name):
+    return [l.strip() for l in kernel_body(asm, name)
+            if l.strip() and not l.strip().startswith((";", "."))]
+
+
+@pytest.mark.parametrize("kind", sorted(KERNELS16))
+def test_dma16_m0_is_only_written_by_the_dma_sequences(asm, kind):
+    body = instructions(asm, KERNELS16[kind])
+    dmas = 0
+    for i, line in enumerate(body):
+        if re.search(r"\bm0\b", line):
+            assert line.startswith("s_mov_b32 m0, s"), line
+            assert body[i + 1].startswith("s_nop 0"), body[i + 1]
+            assert body[i + 2].startswith("global_load_lds_dwordx4"), body[i + 2]
+            dmas += 1
+    # prologue (3 slices) and the k loop unrolled over the 4 stages, 8 DMAs
+    # per wave per slice
+    assert dmas == (3 + 4) * 8
+    assert sum(l.startswith("global_load_lds_dwordx4") for l in body) == dmas
+
+
+@pytest.mark.parametrize("kind", sorted(KERNELS16))
+def test_dma16_slice_barriers_and_no_full_waits_in_the_k_loop(asm, kind):
+    body = instructions(asm, KERNELS16[kind])
+    mfma = [i for i, l in enumerate(body) if l.startswith("v_mfma")]
+    assert len(mfma) == 4 * 64        # 4 unrolled steps of 8 x 8 MFMAs
+    assert all(body[i].startswith("v_mfma_i32_16x16x64_i8 a[") for i in mfma)
+    loop = body[mfma[0]:mfma[-1] + 1]
+    assert not [l for l in loop if re.match(r"s_waitcnt .*vmcnt\(0\)", l)]
+    barriers = [i for i in range(mfma[0], len(body)) if body[i] == "s_barrier"][:4]
+    assert len(barriers) == 4
+    for b in barriers:
+        assert body[b - 1] == "s_waitcnt vmcnt(8)", body[b - 1]
+
+
+def _reads_agpr(line):
+    return line.startswith("v_accvgpr_read") or (
+        line.startswith(("global_store", "buffer_store")) and re.search(r",\s*a\[?\d", line))
+
+
+def fence_violations(body):
+    """Accumulator writes without two s_nop 7 before the next MFMA, and AGPR
+    reads without three s_nop 7 since the last MFMA (in layout order)."""
+    bad = []
+    for i, line in enumerate(body):
+        if line.startswith("v_accvgpr_write"):
+            nxt = next((j for j in range(i, len(body)) if body[j].startswith("v_mfma")), len(body))
+            if sum(body[j] == "s_nop 7" for j in range(i, nxt)) < 2:
+                bad.append((i, line))
+        if _reads_agpr(line):
+            prev = [j for j in range(i) if body[j].startswith("v_mfma")]
+            start = prev[-1] if prev else 0
+            if sum(body[j] == "s_nop 7" for j in range(start, i)) < 3:
+                bad.append((i, line))
+    return bad
+
+
+@pytest.mark.parametrize("kind", sorted(KERNELS16))
+def test_dma16_mfma_hazards_are_fenced(asm, kind):
+    assert fence_violations(instructions(asm, KERNELS16[kind])) == []
+
+
+def test_fence_check_catches_missing_nops():
+    mf = "v_mfma_i32_16x16x64_i8 a[0:3], v[0:3], v[4:7], a[0:3]"
+    ok = ["v_accvgpr_write_b32 a0, 0", "s_nop 7", "s_nop 7", mf,
+          "s_nop 7", "s_nop 7", "s_nop 7", "global_store_dword v[0:1], a0, off nt"]
+    assert fence_violations(ok) == []
+    assert fence_violations(ok[:2] + ok[3:]) == [(0, ok[0])]                 # one nop short
+    assert fence_violations(ok[:5] + ok[6:]) == [(6, ok[7])]                 # store too early
+    assert fence_violations(ok[:4] + ["v_accvgpr_read_b32 v0, a0"]) != []

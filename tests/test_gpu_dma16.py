@@ -1,0 +1,120 @@
+"""gemm_dma16_kernel (full 256x256 tiles, K % 256 == 0 and K >= 5120, 8 x 8
+v_mfma_i32_16x16x64_i8 accumulators per wave) against the oracle, through the
+C ABI (needs a gfx950 GPU). The 8192^3 headline shape runs on it and is
+checked by its full-output hash in test_gpu_config_hashes.py; these cases
+cover D in place, the int8 extremes, batches, packed B and the K threshold.
+"""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from oracle import gemm_oracle as go
+from veritac_amd import _lib
+from veritac_amd.specializations.hip_gemm import backend as hg
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    assert _lib.load_library().vt_device_count() >= 1, "GPU visible but not gfx950"
+    return torch.device("cuda", 0)
+
+
+def say(*args):
+    print(*args, flush=True)
+
+
+def to_dev(dev, x):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+
+
+def run(dev, plan, A, B, D=None, in_place=False):
+    At, Bt = to_dev(dev, A), to_dev(dev, B)
+    if in_place:
+        C = to_dev(dev, D)
+        return hg.run(plan, At, Bt, C, out=C).cpu().numpy()
+    Dt = to_dev(dev, D) if D is not None else None
+    return hg.run(plan, At, Bt, Dt).cpu().numpy()
+
+
+@pytest.mark.parametrize("m,n,k", [(256, 256, 5120), (512, 256, 8192), (256, 768, 5376)])
+def test_row_major_full_tiles(dev, m, n, k):
+    say("dma16", m, n, k)
+    rng = np.random.default_rng(m + n + k)
+    A = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    B = rng.integers(-128, 128, (k, n), dtype=np.int8)
+    D = rng.integers(-2**30, 2**30, (m, n), dtype=np.int32)
+    plan = hg.make_plan(m, n, k, variant="mfma_256x256")
+    assert np.array_equal(run(dev, plan, A, B), go.gemm_i8_f64(A, B))
+    plan_d = hg.make_plan(m, n, k, has_d=True, d_max_abs=2**30, variant="mfma_256x256")
+    want = go.gemm_i8(A, B, D)
+    assert np.array_equal(run(dev, plan_d, A, B, D), want)
+    assert np.array_equal(run(dev, plan_d, A, B, D, in_place=True), want)
+
+
+def test_extremes_at_k8192(dev):
+    m = n = 256
+    k = 8192
+    plan = hg.make_plan(m, n, k, variant="mfma_256x256")
+    A = np.full((m, k), -128, np.int8)
+    assert np.all(run(dev, plan, A, np.full((k, n), -128, np.int8)) == 134217728)
+    assert np.all(run(dev, plan, A, np.full((k, n), 127, np.int8)) == -133169152)
+    A = np.tile(np.array([-128, 127], np.int8), (m, k // 2))
+    B = np.tile(np.array([[127], [-128]], np.int8), (k // 2, n))
+    assert np.array_equal(run(dev, plan, A, B), go.gemm_i8_f64(A, B))
+    # the largest partial sum a valid plan allows plus the largest product:
+    # exactly 2^31 - 1
+    dmax = 2**31 - 1 - 16384 * k
+    plan_d = hg.make_plan(m, n, k, has_d=True, d_max_abs=dmax, variant="mfma_256x256")
+    assert hg.validate_plan(plan_d)[0]
+    A = np.full((m, k), -128, np.int8)
+    C = run(dev, plan_d, A, np.full((k, n), -128, np.int8), np.full((m, n), dmax, np.int32))
+    assert np.all(C == 2**31 - 1)
+
+
+@pytest.mark.parametrize("shared", [True, False])
+def test_batches(dev, shared):
+    rng = np.random.default_rng(5 + shared)
+    batch, m, n, k = 3, 256, 256, 5120
+    A = rng.integers(-128, 128, (batch, m, k), dtype=np.int8)
+    B = rng.integers(-128, 128, (k, n) if shared else (batch, k, n), dtype=np.int8)
+    D = rng.integers(-1000, 1000, (batch, m, n), dtype=np.int32)
+    plan = hg.make_plan(m, n, k, batch=batch, b_shared=shared, has_d=True, d_max_abs=1000,
+                        variant="mfma_256x256")
+    C = hg.run(plan, to_dev(dev, A), to_dev(dev, B), to_dev(dev, D)).cpu().numpy()
+    for b in range(batch):
+        assert np.array_equal(C[b], go.gemm_i8(A[b], B if shared else B[b], D[b])), b
+
+
+def test_packed_dma_rows_equal_row_major_and_the_oracle(dev):
+    """4096 x 2048 x 5120: 128 whole 256-row tiles on the packed DMA path; the
+    full output equals the row-major kernel's and the 128x128 kernel's, and
+    sampled rows equal the oracle."""
+    m, n, k = 4096, 2048, 5120
+    rng = np.random.default_rng(77)
+    A = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    B = rng.integers(-128, 128, (k, n), dtype=np.int8)
+    At, Bt = to_dev(dev, A), to_dev(dev, B)
+    plan_p = hg.make_plan(m, n, k, variant=hg.PACKED_VARIANT)
+    assert hg.packed_dma_rows(plan_p) == m
+    Cp = hg.run(plan_p, At, hg.pack_b(Bt)).cpu().numpy()
+    Cr = hg.run(hg.make_plan(m, n, k, variant="mfma_256x256"), At, Bt).cpu().numpy()
+    C128 = hg.run(hg.make_plan(m, n, k, variant="mfma_128x128"), At, Bt).cpu().numpy()
+    assert np.array_equal(Cp, Cr) and np.array_equal(Cr, C128)
+    for rows in (slice(0, 256), slice(1792, 2048), slice(m - 256, m)):
+        assert np.array_equal(Cr[rows], go.gemm_i8_f64(A[rows], B)), rows
+
+
+def test_threshold_k(dev):
+    """K = 4096 and 4864, multiples of 256 below the 5120 threshold, stay on
+    the 32x32x32 kernel; both agree with the oracle."""
+    rng = np.random.default_rng(9)
+    for k in (4096, 4864):
+        A = rng.integers(-128, 128, (256, k), dtype=np.int8)
+        B = rng.integers(-128, 128, (k, 256), dtype=np.int8)
+        plan = hg.make_plan(256, 256, k, variant="mfma_256x256")
+        assert np.array_equal(run(dev, plan, A, B), go.gemm_i8_f64(A, B)), k

@@ -44,7 +44,8 @@ def test_copy_calibration_factors():
 
 
 def test_gemm_traffic_matches_its_profile():
-    text = read("gemm_dma_256x256_8192cube.md")
+    # the headline kernel (K = 8192: gemm_dma16_kernel)
+    text = read("gemm_dma16_256x256_8192cube.md")
     fetch = kib(re.search(r"\|\s*FETCH_SIZE\s*\|\s*([\d,]+) KiB", text).group(1))
     write = kib(re.search(r"\|\s*WRITE_SIZE\s*\|\s*([\d,]+) KiB", text).group(1))
     assert bench.TRAFFIC_GEMM_8192["read"] == pytest.approx(2.0 * fetch * 1024, rel=1e-3)

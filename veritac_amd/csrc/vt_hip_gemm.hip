@@ -9,12 +9,18 @@
 // kernel here relies on.
 //
 // Kernels
-//   gemm_dma_kernel  full 256x256 tiles, with or without D (the 8192^3 case).
-//       Persistent: one workgroup per CU walks its tiles in XCD-contiguous
-//       order; k slices go global -> LDS by direct-to-LDS DMA
-//       (global_load_lds_dwordx4) into four stages, three slices ahead, and
-//       the slice stream runs across tile boundaries. The MFMA, fragment-read
-//       and DMA instructions follow an explicit per-slot schedule.
+//   gemm_dma16_kernel  full 256x256 tiles with K % 256 == 0, with or without
+//       D, row-major or packed B (the 8192^3 case). Persistent: one workgroup
+//       per CU walks its tiles in XCD-contiguous order; k slices go global ->
+//       LDS by direct-to-LDS DMA (global_load_lds_dwordx4) into four stages,
+//       three slices ahead, and the slice stream runs across tile
+//       boundaries. Each wave's 128x128 block is 8 x 8 v_mfma_i32_16x16x64_i8
+//       accumulators (half the accumulator traffic per multiply-add of the
+//       32x32x32 form, so more work per joule under the board's power limit);
+//       the MFMA, fragment-read and DMA instructions follow an explicit
+//       per-slot schedule.
+//   gemm_dma_kernel  the same on 4 x 4 v_mfma_i32_32x32x32_i8 accumulators,
+//       for full tiles whose K is a multiple of 64 but not of 256.
 //   gemm_mfma_kernel<BM,BN>  every other compute-bound case. 256 threads = 4
 //       waves in a 2x2 grid, each wave owns a (BM/2)x(BN/2) block of 32x32
 //       accumulators fed by v_mfma_i32_32x32x32_i8. A/B k-slices of 64 bytes
@@ -777,6 +783,308 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_dma_kernel(GemmArgs p) {
       for (int ni = 0; ni < NI; ++ni)
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[mi][ni][e] = 0;
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
+// ---------------------------------------------------------------------------
+// Full-tile MFMA kernel on v_mfma_i32_16x16x64_i8
+// ---------------------------------------------------------------------------
+
+// Slice swizzles of gemm_dma16_kernel. A slice [256][64 B]: a 16x16x64 A
+// fragment read (lane l: row l % 16, chunk l / 16) puts rows r and r + 8 in one
+// ds_read_b128 lane group, so chunk c of row r is stored at c ^ (2 * bit 3 of
+// r). B slice [64][256 B]: the transposing reads of one 32-lane group take
+// rows r .. r + 7 and r + 16 .. r + 23 of one chunk, so chunk c of row r is
+// stored at c ^ (r % 8 + 8 * bit 4 of r). Both give every lane group distinct
+// banks under the measured grouping (helpers above).
+__device__ __forceinline__ int a16_swz(int row) { return ((row >> 3) & 1) << 1; }
+__device__ __forceinline__ int a16_off(int row, int c) { return row * 64 + ((c ^ a16_swz(row)) << 4); }
+__device__ __forceinline__ int b16_swz(int row) { return (row & 7) | (((row >> 4) & 1) << 3); }
+
+// Epilogue for 16x16 accumulator blocks: element e of lane l is row
+// 4 * (l / 16) + e and column l % 16 of its block, so one store writes 64
+// bytes of each of 4 rows. Blocks ni and ni + 1 hold the two halves of the
+// same 128-byte row segments: their stores go out back to back, so the L2
+// merges each line before it leaves (block by block, HBM saw 33 % more
+// writes than C). Full tiles only. With D, each 16-row block's D values are
+// all loaded before its stores (C may be D).
+template <int MI, int NI, bool HAS_D>
+__device__ __forceinline__ void store_tile16(const v4i (&acc)[MI][NI], int32_t *Cb,
+                                             const int32_t *Db, int64_t ldc, int64_t ldd,
+                                             int row0, int col0, int lane) {
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi) {
+    int32_t d[HAS_D ? NI : 1][4];
+    if constexpr (HAS_D) {
+#pragma unroll
+      for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          d[ni][e] = Db[(int64_t)(row0 + mi * 16 + 4 * (lane >> 4) + e) * ldd + col0 + ni * 16 + (lane & 15)];
+    }
+#pragma unroll
+    for (int np = 0; np < NI; np += 2)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int ni = np; ni < np + 2; ++ni) {
+          int32_t v = acc[mi][ni][e];
+          if constexpr (HAS_D) v = add_wrap(v, d[ni][e]);
+          __builtin_nontemporal_store(
+              v, Cb + (int64_t)(row0 + mi * 16 + 4 * (lane >> 4) + e) * ldc + col0 + ni * 16 + (lane & 15));
+        }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// v_mfma_i32_16x16x64_i8 accumulating in place in AGPRs. As a builtin, the
+// compiler gives each result a new register tuple and, with all 256 AGPRs
+// holding accumulators, stages them through VGPRs around every MFMA; the
+// tied asm operand keeps each accumulator in one AGPR tuple. Hazards: every
+// use in gemm_dma16_kernel reads an accumulator 64 MFMAs after its previous
+// write, its fragments come from LDS reads the compiler waits for, and the
+// kernel waits explicitly before its epilogue reads the results.
+__device__ __forceinline__ void mfma16_in_place(v4i &acc, const v4i &a, const v4i &b) {
+  asm volatile("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+
+// Same contract and structure as gemm_dma_kernel<4, HAS_D, PACKED_B> (full
+// 256x256 tiles, persistent, k slices by DMA into 4 LDS stages, 3 slices
+// ahead, one barrier per slice), with each wave's 128x128 block held as 8 x 8
+// v_mfma_i32_16x16x64_i8 accumulators instead of 4 x 4 of 32x32x32. The
+// 16x16x64 form does the same work per slice from the same 16 KB of fragment
+// reads per wave, and on config-5 data its register-only loop sustains about
+// 20 % more operations per second at the board's power limit (3945 against
+// 3262-3293 TOPS, at 1.98 against 1.67 GHz): it reads and writes half the
+// accumulator bytes per multiply-add.
+//
+// Step gs multiplies slice gs (its whole 64-deep fragment set, read during
+// step gs - 1) in 64 MFMA slots while reading slice gs + 1's fragments into
+// the other register set, one LDS read per slot in first-use order, and
+// issues slice gs + 3's DMAs one every 8 slots. The wait at the end of step gs
+// (vmcnt(DMAS): only slice gs + 3's DMAs may remain) plus the barrier publish
+// slice gs + 2, whose fragments step gs + 1 reads. Stage gs % 4 is refilled in
+// step gs + 1; its reads were issued in step gs - 1 and consumed by step gs's
+// MFMAs.
+template <bool HAS_D, bool PACKED_B>
+__global__ __launch_bounds__(256, 1) void gemm_dma16_kernel(GemmArgs p) {
+  constexpr int BM = 256, BN = 256, BK = 64;
+  constexpr int WTM = 128, WTN = 128, MI = WTM / 16, NI = WTN / 16;
+  constexpr int A_BYTES = BM * BK, B_BYTES = BK * BN;
+  constexpr int NSTAGE = 4;
+  // A stages at [0, 64 KB), B stages at [64 KB, 128 KB): with the stage a
+  // compile-time constant, every fragment read is its base register plus an
+  // immediate offset below 64 KB, with no address arithmetic per read.
+  constexpr int B_REGION = NSTAGE * A_BYTES;
+  static_assert(A_BYTES == B_BYTES && (NSTAGE - 1) * A_BYTES + 8 * BN < 65536, "16-bit read offsets");
+  constexpr int DPW = 4;                 // 1 KB DMA blocks of A (and of B) per wave per slice
+  constexpr int DMAS = 2 * DPW;
+  __shared__ __attribute__((aligned(1024))) int8_t smem[NSTAGE * (A_BYTES + B_BYTES)];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+
+  const int G = gridDim.x;
+  const int w = blockIdx.x;
+  const int q = G >> 3, r = G & 7, x = w & 7;
+  const int wl = x * q + (x < r ? x : r) + (w >> 3);
+  const int per_batch = p.tiles_m * p.tiles_n;
+  const int total_tiles = per_batch * p.batch_count;
+  if (wl >= total_tiles) return;
+  const int ntiles = (total_tiles - 1 - wl) / G + 1;
+  const int group = p.group_m * p.tiles_n;
+  auto tile_coords = [&](int it, int &bidx, int &m0, int &n0) {
+    const int lt = wl + it * G;
+    bidx = lt / per_batch;
+    const int t = lt - bidx * per_batch;
+    const int gid = t / group;
+    const int first_m = gid * p.group_m;
+    const int gm = min(p.tiles_m - first_m, p.group_m);
+    const int within = t - gid * group;
+    m0 = (first_m + within % gm) * BM;
+    n0 = (within / gm) * BN;
+  };
+
+  const int64_t lda = p.lda, ldb = p.ldb;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(LDS_AS int8_t *)smem;
+  const int KT = p.K / BK;
+  const int last_g = ntiles * KT - 1;
+
+  uint32_t a_lane[DPW], b_lane[DPW];
+#pragma unroll
+  for (int i = 0; i < DPW; ++i) {
+    const int arow = (wave * DPW + i) * 16 + (lane >> 2);
+    const int ac = (lane & 3) ^ a16_swz(arow);
+    a_lane[i] = (uint32_t)((int64_t)arow * lda + ac * 16);
+    if constexpr (PACKED_B) {
+      b_lane[i] = (uint32_t)((int64_t)(wave * DPW + i) * ldb * 1024 + lane * 16);
+    } else {
+      const int brow = (wave * DPW + i) * 4 + (lane >> 4);
+      const int bc = (lane & 15) ^ b16_swz(brow);
+      b_lane[i] = (uint32_t)((int64_t)brow * ldb + bc * 16);
+    }
+  }
+  // The slice the next DMA round fetches: running A and B pointers, the
+  // slices left in the current tile and in the whole walk (slices past the
+  // last one re-read it; their stages are never read).
+  int d_it = 0, d_left = KT, g_left = last_g;
+  const int8_t *a_next = nullptr, *b_next = nullptr;
+  const int64_t b_step = PACKED_B ? 1024 : (int64_t)BK * ldb;
+  auto set_tile = [&](int it) {
+    int bidx, m0, n0;
+    tile_coords(it, bidx, m0, n0);
+    a_next = p.A + bidx * p.sa + (int64_t)m0 * lda;
+    b_next = p.B + bidx * p.sb + (PACKED_B ? (int64_t)(n0 / 16) * ldb * 1024 : (int64_t)n0);
+  };
+  set_tile(0);
+  auto next_bases = [&](const int8_t *&abase, const int8_t *&bbase) {
+    abase = a_next;
+    bbase = b_next;
+    if (g_left > 0) {
+      --g_left;
+      if (--d_left == 0) {
+        d_left = KT;
+        set_tile(++d_it);
+      } else {
+        a_next += BK;
+        b_next += b_step;
+      }
+    }
+  };
+  auto issue_slice = [&](int stage) {
+    const int8_t *abase, *bbase;
+    next_bases(abase, bbase);
+    const uint32_t ma = lds0 + stage * A_BYTES + wave * DPW * 1024;
+    const uint32_t mb = ma + B_REGION;
+#pragma unroll
+    for (int i = 0; i < DPW; ++i) dma_b128(abase, a_lane[i], ma + i * 1024);
+#pragma unroll
+    for (int i = 0; i < DPW; ++i) dma_b128(bbase, b_lane[i], mb + i * 1024);
+  };
+
+  // Fragment offsets within a stage. A block mi: lane l reads row
+  // wm*128 + mi*16 + l%16, chunk l/16 (k 16*(l/16) .. +15). B block ni (columns
+  // wn*128 + ni*16 ..): lane l needs k 16*(l/16) .. +15 of column l%16, read as
+  // two transposed 8-row halves (rows 16*(l/16) + (l%16)/2 and + 8, the same
+  // swizzle), or with packed B as one 16-byte piece of the block's tile.
+  int a_frag[MI], b_frag[NI];
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi) a_frag[mi] = a16_off(wm * WTM + mi * 16 + (lane & 15), lane >> 4);
+#pragma unroll
+  for (int ni = 0; ni < NI; ++ni) {
+    const int cb = wn * (WTN / 16) + ni;
+    if constexpr (PACKED_B) {
+      b_frag[ni] = B_REGION + cb * 1024 + lane * 16;
+    } else {
+      const int row = 16 * (lane >> 4) + ((lane & 15) >> 1);
+      b_frag[ni] = B_REGION + row * BN + ((cb ^ b16_swz(row)) << 4) + (lane & 1) * 8;
+    }
+  }
+  // The accumulators, in AGPRs (mfma16_in_place). The MFMAs are asm, whose
+  // hazards the compiler does not check, so every write of the accumulators
+  // by ordinary code (zeroing) and every read (the epilogue) is separated from
+  // the MFMAs by volatile asm in program order: an empty "+a" statement per
+  // accumulator pins the value at that point, and s_nop gives the wait states
+  // (VALU write -> MFMA srcC read; MFMA write -> VALU / store read).
+  v4i acc[MI][NI];
+  auto fence_acc = [&]() {
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < NI; ++ni) asm volatile("" : "+a"(acc[mi][ni]));
+  };
+  auto zero_acc = [&]() {
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = v4i{0, 0, 0, 0};
+    fence_acc();
+    asm volatile("s_nop 7\n\ts_nop 7" ::: "memory");
+  };
+  zero_acc();
+
+  // B reads per slice: lo/hi transposed halves, or whole packed pieces.
+  constexpr int BU = PACKED_B ? NI : 2 * NI;
+  // One set of A fragments (block mi of the next slice is read right after
+  // its last MFMA in this step, 64 slots before it is needed) and two sets of
+  // B fragments (every row of MFMAs uses every B block). Row-major B: the two
+  // transposed halves land in the low and high pairs of the operand itself.
+  v4i fa[MI], fb0[NI], fb1[NI];
+  auto read_a = [&](int stage, int mi) {
+    fa[mi] = ld_lds_b128(smem + stage * A_BYTES, a_frag[mi]);
+  };
+  auto read_b = [&](int stage, int u, v4i *fb) {
+    const int8_t *Bs = smem + stage * A_BYTES;   // b_frag includes B_REGION
+    if constexpr (PACKED_B) {
+      fb[u] = ld_lds_b128(Bs, b_frag[u]);
+    } else {
+      if ((u & 1) == 0) fb[u >> 1].xy = ld_lds_tr8(Bs, b_frag[u >> 1]);
+      else fb[u >> 1].zw = ld_lds_tr8(Bs, b_frag[u >> 1] + 8 * BN);
+    }
+  };
+  // One step: MFMAs of slice gs, row by row, from fa and fb; slice gs + 1's B
+  // blocks go to gb in the first BU slots (block order = first use), its A
+  // blocks to fa as each row's last MFMA retires.
+  // stg = gs % 4, a compile-time constant at every call.
+  auto step = [&](int stg, v4i *fb, v4i *gb) {
+    const int s1 = (stg + 1) & 3, s3 = (stg + 3) & 3;
+    const int8_t *abase, *bbase;
+    next_bases(abase, bbase);   // slice gs + 3
+    const uint32_t ma = lds0 + s3 * A_BYTES + wave * DPW * 1024;
+    const uint32_t mb = ma + B_REGION;
+#pragma unroll
+    for (int slot = 0; slot < MI * NI; ++slot) {
+      const int mi = slot / NI, ni = slot % NI;
+      mfma16_in_place(acc[mi][ni], fa[mi], fb[ni]);
+      if (slot < BU) read_b(s1, slot, gb);
+      if (ni == NI - 1) read_a(s1, mi);
+      if ((slot & 7) == 2) {
+        const int d = slot >> 3;
+        if (d < DPW) dma_b128(abase, a_lane[d], ma + d * 1024);
+        else dma_b128(bbase, b_lane[d - DPW], mb + (d - DPW) * 1024);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // Slice gs + 2 has landed (only slice gs + 3's DMAs remain in flight;
+    // older stores are waited for as well); after the barrier every wave may
+    // read it, and stage gs % 4 (read in step gs - 1) may be refilled.
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" :: "n"(DMAS) : "memory");
+  };
+
+  issue_slice(0);
+  issue_slice(1);
+  issue_slice(2);
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" :: "n"(DMAS) : "memory");   // slices 0, 1 landed
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi) read_a(0, mi);
+#pragma unroll
+  for (int u = 0; u < BU; ++u) read_b(0, u, fb0);
+
+  int gs = 0;   // global slice index
+  for (int it = 0; it < ntiles; ++it) {
+    // Kernel-argument scalar loads hoisted by the compiler complete here, not
+    // inside the k loop (they retire out of order with LDS reads).
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0); vmcnt, expcnt untouched
+    // KT is a multiple of 4 (the host requires K % 256 == 0), so every tile
+    // starts at stage 0 with register set 0, and stages and sets rotate
+    // statically.
+    for (int kt = 0; kt < KT; kt += 4, gs += 4) {
+      step(0, fb0, fb1);
+      step(1, fb1, fb0);
+      step(2, fb0, fb1);
+      step(3, fb1, fb0);
+    }
+    // The last MFMAs' result latency before the epilogue reads any AGPR.
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+    fence_acc();
+    int bidx, m0, n0;
+    tile_coords(it, bidx, m0, n0);
+    store_tile16<MI, NI, HAS_D>(acc, p.C + bidx * p.sc, HAS_D ? p.D + bidx * p.sd : nullptr, p.ldc,
+                                p.ldd, m0 + wm * WTM, n0 + wn * WTN, lane);
+    zero_acc();
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
@@ -1652,6 +1960,17 @@ int select_variant(const Problem &q, bool vec, int32_t *variant, int32_t *k_spli
 // Waves per workgroup of the persistent full-tile kernel.
 constexpr int kDmaWaves = 4;
 
+// Full 256x256 tiles run on gemm_dma16_kernel (16x16x64) when K is a whole
+// number of 256-deep groups of four slices and at least 5120; shorter K stays
+// on gemm_dma_kernel (32x32x32). Measured per launch (HIP graphs): at
+// 8192 x 8192 x K, 16x16x64 against 32x32x32 is 255/248 against 249/248 us at
+// K = 4096, 299/293 against 300/300 at 5120, 342/335 against 354/354 at 6144,
+// 427 against 462 at 8192; K = 256 .. 2048 lose 8-21 % (config 3, K = 1024:
+// 57 against 51 us), where the 64-byte row segments of the 16x16 blocks' C
+// stores cost more than the cheaper MFMAs save.
+constexpr int64_t kDma16MinK = 5120;
+bool use_dma16(int64_t K) { return K % 256 == 0 && K >= kDma16MinK; }
+
 template <int BM, int BN, int EDGE, bool HAS_D, bool PACKED>
 void launch_mfma_kernel(bool short_k, bool early_d, dim3 grid, dim3 block, hipStream_t stream,
                         const GemmArgs &a) {
@@ -1782,7 +2101,10 @@ int launch_mfma_tiles(const Problem &r, hipStream_t stream, int num_cus) {
     // Persistent: one workgroup per CU (the kernel's LDS allows no more).
     const int64_t g = blocks < num_cus ? blocks : num_cus;
     dim3 pgrid((unsigned)g);
-    if (has_d) hipLaunchKernelGGL((gemm_dma_kernel<kDmaWaves, true>), pgrid, dim3(64 * kDmaWaves), 0, stream, a);
+    if (use_dma16(r.K)) {
+      if (has_d) hipLaunchKernelGGL((gemm_dma16_kernel<true, false>), pgrid, dim3(256), 0, stream, a);
+      else hipLaunchKernelGGL((gemm_dma16_kernel<false, false>), pgrid, dim3(256), 0, stream, a);
+    } else if (has_d) hipLaunchKernelGGL((gemm_dma_kernel<kDmaWaves, true>), pgrid, dim3(64 * kDmaWaves), 0, stream, a);
     else hipLaunchKernelGGL((gemm_dma_kernel<kDmaWaves, false>), pgrid, dim3(64 * kDmaWaves), 0, stream, a);
     VT_HIP_CHECK(hipGetLastError());
     return VT_OK;
@@ -1956,7 +2278,10 @@ int launch_packed_dma(const Problem &q, hipStream_t stream, int num_cus) {
   const int64_t blocks = (int64_t)a.tiles_m * a.tiles_n * q.batch;
   if (blocks > 0x7fffffff) return fail(VT_EUNSUPPORTED, "grid of %lld tiles too large", (long long)blocks);
   dim3 pgrid((unsigned)(blocks < num_cus ? blocks : num_cus));
-  if (q.D) hipLaunchKernelGGL((gemm_dma_kernel<kDmaWaves, true, true>), pgrid, dim3(64 * kDmaWaves), 0, stream, a);
+  if (use_dma16(q.K)) {
+    if (q.D) hipLaunchKernelGGL((gemm_dma16_kernel<true, true>), pgrid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((gemm_dma16_kernel<false, true>), pgrid, dim3(256), 0, stream, a);
+  } else if (q.D) hipLaunchKernelGGL((gemm_dma_kernel<kDmaWaves, true, true>), pgrid, dim3(64 * kDmaWaves), 0, stream, a);
   else hipLaunchKernelGGL((gemm_dma_kernel<kDmaWaves, false, true>), pgrid, dim3(64 * kDmaWaves), 0, stream, a);
   VT_HIP_CHECK(hipGetLastError());
   return VT_OK;
