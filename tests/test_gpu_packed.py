@@ -341,10 +341,12 @@ def test_row_blocks_with_packed_b_whole_groups(dev):
     assert np.array_equal(gpu_gemm_packed(dev, A, c["B"]), go.gemm_i8_f64(A, c["B"]))
 
 
-# 128x128 tiles with packed B: K tails (K % 128 == 64, K % 64 == 16), ragged
-# N (last 128-column tile half live), K split into 2 and 16 slices, D in place.
+# 128x128 tiles with packed B: K tails (K % 128 == 64, K % 64 == 16, K of one
+# zero-padded 64-row block), ragged N (last 128-column tile partly live), K
+# split into 2 and 16 slices, D in place.
 @pytest.mark.parametrize("m,k,n", [(65, 4160, 272), (100, 1040, 400), (200, 1024, 64),
-                                   (128, 16384, 1024), (129, 2048, 4096)])
+                                   (128, 16384, 1024), (129, 2048, 4096), (100, 16, 48),
+                                   (130, 48, 80)])
 def test_packed_tiles_edges_and_k_split(dev, m, k, n):
     plan = hg.make_plan(m, n, k, variant=hg.PACKED_VARIANT)
     say("packed tiles", m, k, n, hg.native_check(plan)[1])
