@@ -1,8 +1,10 @@
-"""gemm_dma16_kernel (full 256x256 tiles, K % 256 == 0 and K >= 5120, 8 x 8
-v_mfma_i32_16x16x64_i8 accumulators per wave) against the oracle, through the
-C ABI (needs a gfx950 GPU). The 8192^3 headline shape runs on it and is
-checked by its full-output hash in test_gpu_config_hashes.py; these cases
-cover D in place, the int8 extremes, batches, packed B and the K threshold.
+"""gemm_dma16_kernel (full 256x256 tiles, K % 256 == 0, 8 x 8
+v_mfma_i32_16x16x64_i8 accumulators per wave, C stored through an LDS strip as
+16-byte row segments) against the oracle, through the C ABI (needs a gfx950
+GPU). The 8192^3 headline shape and config 3 run on it and are checked by
+their full-output hashes in test_gpu_config_hashes.py; these cases cover short
+and long K, D in place, the int8 extremes, batches, packed B, and the C / D
+alignment gate that sends other full-tile problems to the 32x32x32 kernel.
 """
 import numpy as np
 import pytest
@@ -41,7 +43,8 @@ def run(dev, plan, A, B, D=None, in_place=False):
     return hg.run(plan, At, Bt, Dt).cpu().numpy()
 
 
-@pytest.mark.parametrize("m,n,k", [(256, 256, 5120), (512, 256, 8192), (256, 768, 5376)])
+@pytest.mark.parametrize("m,n,k", [(256, 256, 256), (512, 256, 1024), (256, 256, 5120),
+                                   (512, 256, 8192), (256, 768, 5376)])
 def test_row_major_full_tiles(dev, m, n, k):
     say("dma16", m, n, k)
     rng = np.random.default_rng(m + n + k)
@@ -109,12 +112,42 @@ def test_packed_dma_rows_equal_row_major_and_the_oracle(dev):
         assert np.array_equal(Cr[rows], go.gemm_i8_f64(A[rows], B)), rows
 
 
-def test_threshold_k(dev):
-    """K = 4096 and 4864, multiples of 256 below the 5120 threshold, stay on
-    the 32x32x32 kernel; both agree with the oracle."""
+def test_k_not_a_multiple_of_256(dev):
+    """K = 4160 and 320 (multiples of 64, not of 256) run on the 32x32x32
+    kernel; both agree with the oracle."""
     rng = np.random.default_rng(9)
-    for k in (4096, 4864):
+    for k in (4160, 320):
         A = rng.integers(-128, 128, (256, k), dtype=np.int8)
         B = rng.integers(-128, 128, (k, 256), dtype=np.int8)
         plan = hg.make_plan(256, 256, k, variant="mfma_256x256")
         assert np.array_equal(run(dev, plan, A, B), go.gemm_i8_f64(A, B)), k
+
+
+INT32_MIN = -2**31
+
+
+@pytest.mark.parametrize("ldc,c_off,ldd,d_off", [
+    (516, 0, 512, 0),      # 16-byte rows with padding: the 16x16x64 kernel
+    (513, 0, 512, 0),      # ldc not a multiple of 4: 32x32x32
+    (512, 1, 512, 0),      # C 4 bytes past a 16-byte boundary: 32x32x32
+    (512, 0, 514, 0),      # ldd not a multiple of 4: 32x32x32
+    (512, 0, 512, 3),      # D 12 bytes past a 16-byte boundary: 32x32x32
+])
+def test_c_and_d_alignment(dev, ldc, c_off, ldd, d_off):
+    m, n, k = 256, 512, 1024
+    say("dma16 alignment", ldc, c_off, ldd, d_off)
+    rng = np.random.default_rng(ldc + 7 * c_off + ldd + 11 * d_off)
+    A = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    B = rng.integers(-128, 128, (k, n), dtype=np.int8)
+    Dfull = rng.integers(-2**20, 2**20, m * ldd + d_off, dtype=np.int32)
+    D = Dfull[d_off:].reshape(m, ldd)
+    At, Bt = to_dev(dev, A), to_dev(dev, B)
+    Dt = to_dev(dev, Dfull)
+    Cbuf = torch.full((m * ldc + c_off,), INT32_MIN, dtype=torch.int32, device=dev)
+    _lib.gemm_raw(At.data_ptr(), Bt.data_ptr(), Dt.data_ptr() + 4 * d_off, Cbuf.data_ptr() + 4 * c_off,
+                  m, n, k, k, n, ldd, ldc, variant="mfma_256x256")
+    _lib.sync(None)
+    got = Cbuf.cpu().numpy()
+    C = got[c_off:].reshape(m, ldc)
+    assert np.array_equal(C[:, :n], go.gemm_i8(A, B, D[:, :n]))
+    assert (C[:, n:] == INT32_MIN).all() and (got[:c_off] == INT32_MIN).all()

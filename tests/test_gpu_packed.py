@@ -370,15 +370,16 @@ def test_packed_tiles_k_split_extremes(dev):
     assert np.array_equal(gpu_gemm_packed(dev, A, B), go.gemm_i8_f64(A, B))
 
 
-@pytest.mark.parametrize("extra", [0, 44, 100])
-def test_dma_rows_with_packed_b(dev, extra):
-    """4096 rows x 2048 columns: 128 whole 256-row tiles on the DMA kernel,
-    then 44 rows in a decode group or 100 rows on 128x128 tiles."""
-    m, k, n = 4096 + extra, 192, 2048
+@pytest.mark.parametrize("extra,k", [(0, 192), (44, 192), (100, 192), (0, 256), (100, 512)])
+def test_dma_rows_with_packed_b(dev, extra, k):
+    """4096 rows x 2048 columns: 128 whole 256-row tiles on the DMA kernel
+    (32x32x32 at K = 192, 16x16x64 at K = 256 and 512), then 44 rows in a
+    decode group or 100 rows on 128x128 tiles."""
+    m, n = 4096 + extra, 2048
     plan = hg.make_plan(m, n, k, variant=hg.PACKED_VARIANT)
     assert hg.packed_dma_rows(plan) == 4096
     say("packed dma", m, k, n, hg.native_check(plan)[1])
-    rng = np.random.default_rng(300 + extra)
+    rng = np.random.default_rng(300 + extra + k)
     A = rng.integers(-128, 128, (m, k), dtype=np.int8)
     B = rng.integers(-128, 128, (k, n), dtype=np.int8)
     D = rng.integers(-2**20, 2**20, (m, n), dtype=np.int32)

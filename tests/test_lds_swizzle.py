@@ -160,3 +160,77 @@ def test_skinny_b_stage_conflict_free():
                 assert conflicts(addrs, 8) == 0
     for row in range(64):
         assert sorted(c ^ skinny_b_swz(row) for c in range(16)) == list(range(16))
+
+
+def strip_off(row, chunk):
+    return row * 512 + ((chunk ^ (((row >> 2) & 3) << 2)) << 4)
+
+
+def conflicts_b32(addrs):
+    """Extra bank cycles of a wave-wide 4-byte access, all 64 lanes served
+    together (the epilogue profile reads SQ_LDS_BANK_CONFLICT = 0 for it)."""
+    banks = {}
+    for addr in addrs:
+        banks[(addr // 4) % 64] = banks.get((addr // 4) % 64, 0) + 1
+    return max(banks.values()) - 1
+
+
+def strip_write_addr(lane, ni, e):
+    """store_tile16_lds: element e of lane l of 16x16 block ni (row 4*(l/16)+e,
+    column l%16) goes to strip row 4*(l/16)+e, 4-byte word ni*16 + l%16."""
+    c, g = lane & 15, lane >> 4
+    return strip_off(4 * g + e, ni * 4 + (c >> 2)) + (c & 3) * 4
+
+
+def strip_read_addr(lane, j):
+    """Read j: lane l takes 16 bytes of strip row 2*j + l/32, chunk l%32."""
+    return strip_off(2 * j + (lane >> 5), lane & 31)
+
+
+def test_epilogue_strip_is_a_permutation():
+    offs = sorted(strip_off(r, c) for r in range(16) for c in range(32))
+    assert offs == [16 * i for i in range(512)]
+
+
+def test_epilogue_strip_conflict_free():
+    for ni in range(8):
+        for e in range(4):
+            assert conflicts_b32([strip_write_addr(l, ni, e) for l in range(64)]) == 0
+    for j in range(8):
+        assert conflicts([strip_read_addr(l, j) for l in range(64)], 16) == 0
+    # unswizzled, every write of one instruction hits 4 lanes per bank
+    assert conflicts_b32([(4 * (l >> 4) + e) * 512 + ni * 64 + (l & 15) * 4
+                          for l in range(64) for ni, e in [(0, 0)]]) == 3
+
+
+def simulate_epilogue(acc, write=strip_write_addr, read=strip_read_addr):
+    """acc[ni][lane][e] (one 16-row strip of a wave's 16 x 128 block) -> the
+    16 x 128 int32 rows the stores write: read j of lane l goes to row
+    2*j + l/32, columns 4*(l%32) .. +3."""
+    import numpy as np
+    lds = np.zeros(8192 // 4, np.int64)
+    for ni in range(8):
+        for lane in range(64):
+            for e in range(4):
+                lds[write(lane, ni, e) // 4] = acc[ni][lane][e]
+    out = np.zeros((16, 128), np.int64)
+    for j in range(8):
+        for lane in range(64):
+            a = read(lane, j) // 4
+            out[2 * j + (lane >> 5), 4 * (lane & 31):4 * (lane & 31) + 4] = lds[a:a + 4]
+    return out
+
+
+def test_epilogue_round_trip_matches_accumulator_layout():
+    """Values placed by the v_mfma_i32_16x16x64_i8 accumulator layout (element
+    e of lane l of block ni is row 4*(l/16)+e, column 16*ni + l%16) come back as
+    the row-major strip; planted index mistakes do not."""
+    import numpy as np
+    want = np.arange(16 * 128, dtype=np.int64).reshape(16, 128) * 7 - 5000
+    acc = [[[want[4 * (l >> 4) + e, 16 * ni + (l & 15)] for e in range(4)] for l in range(64)]
+           for ni in range(8)]
+    assert np.array_equal(simulate_epilogue(acc), want)
+    swapped = lambda lane, ni, e: strip_off(4 * e + (lane >> 4), ni * 4 + ((lane & 15) >> 2)) + (lane & 3) * 4
+    assert not np.array_equal(simulate_epilogue(acc, write=swapped), want)
+    unswizzled_read = lambda lane, j: (2 * j + (lane >> 5)) * 512 + (lane & 31) * 16
+    assert not np.array_equal(simulate_epilogue(acc, read=unswizzled_read), want)

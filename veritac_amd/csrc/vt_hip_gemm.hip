@@ -802,38 +802,54 @@ __device__ __forceinline__ int a16_swz(int row) { return ((row >> 3) & 1) << 1; 
 __device__ __forceinline__ int a16_off(int row, int c) { return row * 64 + ((c ^ a16_swz(row)) << 4); }
 __device__ __forceinline__ int b16_swz(int row) { return (row & 7) | (((row >> 4) & 1) << 3); }
 
-// Epilogue for 16x16 accumulator blocks: element e of lane l is row
-// 4 * (l / 16) + e and column l % 16 of its block, so one store writes 64
-// bytes of each of 4 rows. Blocks ni and ni + 1 hold the two halves of the
-// same 128-byte row segments: their stores go out back to back, so the L2
-// merges each line before it leaves (block by block, HBM saw 33 % more
-// writes than C). Full tiles only. With D, each 16-row block's D values are
-// all loaded before its stores (C may be D).
+// Epilogue of gemm_dma16_kernel through LDS: each 16-row strip of the wave's
+// 128-column block is written to the wave's 8 KB of LDS in the accumulator
+// layout and read back row-contiguous, so every global store is 16 bytes per
+// lane and one instruction writes two whole 512-byte row segments (the
+// accumulator layout gives 64-byte row segments). 16-byte chunk k of strip
+// row r is stored at chunk k ^ (4 * ((r / 4) % 4)): the 4-byte writes of one
+// instruction (rows 4 * (l / 16) + e, column l % 16 of a block) then fall on
+// 64 distinct banks, and each 16-lane read still covers 16 distinct chunks of
+// one row. With D, the strip's D values (the same row-contiguous 16 bytes each
+// lane then stores) are all loaded before its stores; each lane reads its own
+// D bytes before writing them, so C may be D.
+__device__ __forceinline__ int strip_off(int row, int chunk) {
+  return row * 512 + ((chunk ^ (((row >> 2) & 3) << 2)) << 4);
+}
+
 template <int MI, int NI, bool HAS_D>
-__device__ __forceinline__ void store_tile16(const v4i (&acc)[MI][NI], int32_t *Cb,
-                                             const int32_t *Db, int64_t ldc, int64_t ldd,
-                                             int row0, int col0, int lane) {
+__device__ __forceinline__ void store_tile16_lds(const v4i (&acc)[MI][NI], int32_t *Cb,
+                                                 const int32_t *Db, int64_t ldc, int64_t ldd,
+                                                 int row0, int col0, int lane,
+                                                 LDS_AS int8_t *strip) {
+  static_assert(NI * 16 == 128, "two 512-byte rows per wave instruction");
+  const int c = lane & 15, g = lane >> 4;
 #pragma unroll
   for (int mi = 0; mi < MI; ++mi) {
-    int32_t d[HAS_D ? NI : 1][4];
-    if constexpr (HAS_D) {
 #pragma unroll
-      for (int ni = 0; ni < NI; ++ni)
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          d[ni][e] = Db[(int64_t)(row0 + mi * 16 + 4 * (lane >> 4) + e) * ldd + col0 + ni * 16 + (lane & 15)];
-    }
-#pragma unroll
-    for (int np = 0; np < NI; np += 2)
+    for (int ni = 0; ni < NI; ++ni)
 #pragma unroll
       for (int e = 0; e < 4; ++e)
+        *(LDS_AS int32_t *)(strip + strip_off(4 * g + e, ni * 4 + (c >> 2)) + (c & 3) * 4) =
+            acc[mi][ni][e];
+    v4i v[8];
 #pragma unroll
-        for (int ni = np; ni < np + 2; ++ni) {
-          int32_t v = acc[mi][ni][e];
-          if constexpr (HAS_D) v = add_wrap(v, d[ni][e]);
-          __builtin_nontemporal_store(
-              v, Cb + (int64_t)(row0 + mi * 16 + 4 * (lane >> 4) + e) * ldc + col0 + ni * 16 + (lane & 15));
-        }
+    for (int j = 0; j < 8; ++j)
+      v[j] = *(LDS_AS v4i *)(strip + strip_off(2 * j + (lane >> 5), lane & 31));
+    const int64_t r0 = row0 + mi * 16 + (lane >> 5);
+    const int col = col0 + (lane & 31) * 4;
+    if constexpr (HAS_D) {
+      v4i d[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) d[j] = *(const v4i *)(Db + (r0 + 2 * j) * ldd + col);
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[j][q] = add_wrap(v[j][q], d[j][q]);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      __builtin_nontemporal_store(v[j], (v4i *)(Cb + (r0 + 2 * j) * ldc + col));
     __builtin_amdgcn_sched_barrier(0);
   }
 }
@@ -880,7 +896,8 @@ __global__ __launch_bounds__(256, 1) void gemm_dma16_kernel(GemmArgs p) {
   static_assert(A_BYTES == B_BYTES && (NSTAGE - 1) * A_BYTES + 8 * BN < 65536, "16-bit read offsets");
   constexpr int DPW = 4;                 // 1 KB DMA blocks of A (and of B) per wave per slice
   constexpr int DMAS = 2 * DPW;
-  __shared__ __attribute__((aligned(1024))) int8_t smem[NSTAGE * (A_BYTES + B_BYTES)];
+  // The 32 KB past the stages hold each wave's 8 KB epilogue strip.
+  __shared__ __attribute__((aligned(1024))) int8_t smem[NSTAGE * (A_BYTES + B_BYTES) + 4 * 8192];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1082,8 +1099,9 @@ __global__ __launch_bounds__(256, 1) void gemm_dma16_kernel(GemmArgs p) {
     fence_acc();
     int bidx, m0, n0;
     tile_coords(it, bidx, m0, n0);
-    store_tile16<MI, NI, HAS_D>(acc, p.C + bidx * p.sc, HAS_D ? p.D + bidx * p.sd : nullptr, p.ldc,
-                                p.ldd, m0 + wm * WTM, n0 + wn * WTN, lane);
+    store_tile16_lds<MI, NI, HAS_D>(acc, p.C + bidx * p.sc, HAS_D ? p.D + bidx * p.sd : nullptr,
+                                    p.ldc, p.ldd, m0 + wm * WTM, n0 + wn * WTN, lane,
+                                    (LDS_AS int8_t *)smem + NSTAGE * (A_BYTES + B_BYTES) + wave * 8192);
     zero_acc();
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -1961,15 +1979,19 @@ int select_variant(const Problem &q, bool vec, int32_t *variant, int32_t *k_spli
 constexpr int kDmaWaves = 4;
 
 // Full 256x256 tiles run on gemm_dma16_kernel (16x16x64) when K is a whole
-// number of 256-deep groups of four slices and at least 5120; shorter K stays
-// on gemm_dma_kernel (32x32x32). Measured per launch (HIP graphs): at
-// 8192 x 8192 x K, 16x16x64 against 32x32x32 is 255/248 against 249/248 us at
-// K = 4096, 299/293 against 300/300 at 5120, 342/335 against 354/354 at 6144,
-// 427 against 462 at 8192; K = 256 .. 2048 lose 8-21 % (config 3, K = 1024:
-// 57 against 51 us), where the 64-byte row segments of the 16x16 blocks' C
-// stores cost more than the cheaper MFMAs save.
-constexpr int64_t kDma16MinK = 5120;
-bool use_dma16(int64_t K) { return K % 256 == 0 && K >= kDma16MinK; }
+// number of 256-deep groups of four slices and its epilogue's 16-byte C and D
+// accesses are aligned (C, D 16-byte aligned; ldc, ldd and the batch strides
+// multiples of 4 elements); otherwise on gemm_dma_kernel (32x32x32, 4-byte
+// stores). Measured per launch (HIP graphs, two passes), 16x16x64 against
+// 32x32x32 at 8192 x 8192 x K: K = 256 58-61 against 62-63 us, 1024 91-99
+// against 99, 2048 139-145 against 149-150, 4096 226-229 against 245-249,
+// 8192 400 against 447, 8192 with D 459 against 518; config 3 (K = 1024) 46-49
+// against 49; 4096^3 60-69 against 66-67.
+bool use_dma16(const Problem &r) {
+  const bool c_ok = aligned16(r.C) && r.ldc % 4 == 0 && (r.batch == 1 || r.sc % 4 == 0);
+  const bool d_ok = !r.D || (aligned16(r.D) && r.ldd % 4 == 0 && (r.batch == 1 || r.sd % 4 == 0));
+  return r.K % 256 == 0 && c_ok && d_ok;
+}
 
 template <int BM, int BN, int EDGE, bool HAS_D, bool PACKED>
 void launch_mfma_kernel(bool short_k, bool early_d, dim3 grid, dim3 block, hipStream_t stream,
@@ -2101,7 +2123,7 @@ int launch_mfma_tiles(const Problem &r, hipStream_t stream, int num_cus) {
     // Persistent: one workgroup per CU (the kernel's LDS allows no more).
     const int64_t g = blocks < num_cus ? blocks : num_cus;
     dim3 pgrid((unsigned)g);
-    if (use_dma16(r.K)) {
+    if (use_dma16(r)) {
       if (has_d) hipLaunchKernelGGL((gemm_dma16_kernel<true, false>), pgrid, dim3(256), 0, stream, a);
       else hipLaunchKernelGGL((gemm_dma16_kernel<false, false>), pgrid, dim3(256), 0, stream, a);
     } else if (has_d) hipLaunchKernelGGL((gemm_dma_kernel<kDmaWaves, true>), pgrid, dim3(64 * kDmaWaves), 0, stream, a);
@@ -2278,7 +2300,7 @@ int launch_packed_dma(const Problem &q, hipStream_t stream, int num_cus) {
   const int64_t blocks = (int64_t)a.tiles_m * a.tiles_n * q.batch;
   if (blocks > 0x7fffffff) return fail(VT_EUNSUPPORTED, "grid of %lld tiles too large", (long long)blocks);
   dim3 pgrid((unsigned)(blocks < num_cus ? blocks : num_cus));
-  if (use_dma16(q.K)) {
+  if (use_dma16(q)) {
     if (q.D) hipLaunchKernelGGL((gemm_dma16_kernel<true, true>), pgrid, dim3(256), 0, stream, a);
     else hipLaunchKernelGGL((gemm_dma16_kernel<false, true>), pgrid, dim3(256), 0, stream, a);
   } else if (q.D) hipLaunchKernelGGL((gemm_dma_kernel<kDmaWaves, true, true>), pgrid, dim3(64 * kDmaWaves), 0, stream, a);
