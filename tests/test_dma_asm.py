@@ -82,10 +82,13 @@ def test_k_loop_waits_are_the_kernels_own(asm, kind):
 # itself: s_nop 7 pairs between the accumulators' zeroing (v_accvgpr_write)
 # and the next MFMA, and three s_nop 7 between the last MFMA of a tile and
 # the epilogue's reads of the AGPRs.
-KERNELS16 = {"no_d": "_ZN12_GLOBAL__N_117gemm_dma16_kernelILb0ELb0EEEvNS_8GemmArgsE",
-             "with_d": "_ZN12_GLOBAL__N_117gemm_dma16_kernelILb1ELb0EEEvNS_8GemmArgsE",
-             "packed_b": "_ZN12_GLOBAL__N_117gemm_dma16_kernelILb0ELb1EEEvNS_8GemmArgsE",
-             "packed_b_with_d": "_ZN12_GLOBAL__N_117gemm_dma16_kernelILb1ELb1EEEvNS_8GemmArgsE"}
+def _k16(has_d, packed):
+    return "_ZN12_GLOBAL__N_117gemm_dma16_kernelILb%dELb%dEEEvNS_8GemmArgsE" % (has_d, packed)
+
+
+# gemm_dma16_kernel<HAS_D, PACKED_B>
+KERNELS16 = {"no_d": _k16(0, 0), "with_d": _k16(1, 0), "packed_b": _k16(0, 1),
+             "packed_b_with_d": _k16(1, 1)}
 
 
 def instructions(asm, name):
@@ -113,34 +116,60 @@ def test_dma16_m0_is_only_written_by_the_dma_sequences(asm, kind):
 def test_dma16_slice_barriers_and_no_full_waits_in_the_k_loop(asm, kind):
     body = instructions(asm, KERNELS16[kind])
     mfma = [i for i, l in enumerate(body) if l.startswith("v_mfma")]
-    assert len(mfma) == 4 * 64        # 4 unrolled steps of 8 x 8 MFMAs
-    assert all(body[i].startswith("v_mfma_i32_16x16x64_i8 a[") for i in mfma)
-    loop = body[mfma[0]:mfma[-1] + 1]
+    # 4 unrolled steps of 8 x 8 MFMAs accumulating in place
+    loop_mfma = [i for i in mfma if re.match(r"v_mfma_i32_16x16x64_i8 (a\[\d+:\d+\]), v.*, \1$", body[i])]
+    assert len(loop_mfma) == len(mfma) == 4 * 64
+    loop = body[loop_mfma[0]:loop_mfma[-1] + 1]
     assert not [l for l in loop if re.match(r"s_waitcnt .*vmcnt\(0\)", l)]
-    barriers = [i for i in range(mfma[0], len(body)) if body[i] == "s_barrier"][:4]
-    assert len(barriers) == 4
-    for b in barriers:
-        assert body[b - 1] == "s_waitcnt vmcnt(8)", body[b - 1]
+    # every slice barrier waits for all but the slice's own 8 DMAs
+    waits = [body[i - 1] for i in range(loop_mfma[0], loop_mfma[-1] + 8) if body[i] == "s_barrier"]
+    assert len(waits) == 4 and set(waits) == {"s_waitcnt vmcnt(8)"}, waits
 
 
-def _reads_agpr(line):
-    return line.startswith("v_accvgpr_read") or (
-        line.startswith(("global_store", "buffer_store")) and re.search(r",\s*a\[?\d", line))
+def _agprs(text):
+    """AGPR numbers named in an operand list (a7, a[4:7])."""
+    regs = set()
+    for lo, hi, one in re.findall(r"\ba\[(\d+):(\d+)\]|\ba(\d+)\b", text):
+        regs.update(range(int(lo), int(hi) + 1) if lo else {int(one)})
+    return regs
 
 
-def fence_violations(body):
-    """Accumulator writes without two s_nop 7 before the next MFMA, and AGPR
-    reads without three s_nop 7 since the last MFMA (in layout order)."""
+def _mfma_regs(line):
+    """(accumulator written, accumulator read as srcC) of an MFMA line."""
+    ops = line.split(None, 1)[1].split(", ")
+    return _agprs(ops[0]), _agprs(ops[-1])
+
+
+def _agpr_reads(line):
+    if line.startswith("v_accvgpr_read"):
+        return _agprs(line.split(", ", 1)[1])
+    if line.startswith(("global_store", "buffer_store", "ds_write")):
+        return _agprs(line.split(None, 1)[1])
+    return set()
+
+
+def fence_violations(body, far=8):
+    """Accumulator writes (v_accvgpr_write) with fewer than two s_nop 7 and
+    fewer than `far` MFMAs before the next MFMA that reads the register, and
+    AGPR reads with fewer than three s_nop 7 and fewer than `far` MFMAs since
+    the MFMA that wrote it (in layout order)."""
     bad = []
+    mfma = [(i,) + _mfma_regs(l) for i, l in enumerate(body) if l.startswith("v_mfma")]
+    nops = [0]
+    for line in body:
+        nops.append(nops[-1] + (line == "s_nop 7"))
     for i, line in enumerate(body):
         if line.startswith("v_accvgpr_write"):
-            nxt = next((j for j in range(i, len(body)) if body[j].startswith("v_mfma")), len(body))
-            if sum(body[j] == "s_nop 7" for j in range(i, nxt)) < 2:
+            reg = _agprs(line.split(",")[0])
+            later = [m for m in mfma if m[0] > i]
+            hit = next((k for k, m in enumerate(later) if m[2] & reg), None)
+            if hit is not None and hit < far and nops[later[hit][0]] - nops[i] < 2:
                 bad.append((i, line))
-        if _reads_agpr(line):
-            prev = [j for j in range(i) if body[j].startswith("v_mfma")]
-            start = prev[-1] if prev else 0
-            if sum(body[j] == "s_nop 7" for j in range(start, i)) < 3:
+        reads = _agpr_reads(line)
+        if reads:
+            earlier = [m for m in mfma if m[0] < i]
+            hit = next((k for k, m in enumerate(reversed(earlier)) if m[1] & reads), None)
+            if hit is not None and hit < far and nops[i] - nops[earlier[-1 - hit][0]] < 3:
                 bad.append((i, line))
     return bad
 
@@ -158,3 +187,9 @@ def test_fence_check_catches_missing_nops():
     assert fence_violations(ok[:2] + ok[3:]) == [(0, ok[0])]                 # one nop short
     assert fence_violations(ok[:5] + ok[6:]) == [(6, ok[7])]                 # store too early
     assert fence_violations(ok[:4] + ["v_accvgpr_read_b32 v0, a0"]) != []
+    # distance in MFMAs on other accumulators counts as a fence
+    other = "v_mfma_i32_16x16x64_i8 a[4:7], v[0:3], v[4:7], a[4:7]"
+    assert fence_violations(["v_accvgpr_write_b32 a0, v1"] + [other] * 8 + [mf]) == []
+    assert fence_violations(["v_accvgpr_write_b32 a0, v1"] + [other] * 3 + [mf]) != []
+    assert fence_violations([mf] + [other] * 8 + ["v_accvgpr_read_b32 v0, a2"]) == []
+    assert fence_violations([mf] + [other] * 2 + ["v_accvgpr_read_b32 v0, a2"]) != []

@@ -43,8 +43,9 @@ def run(dev, plan, A, B, D=None, in_place=False):
     return hg.run(plan, At, Bt, Dt).cpu().numpy()
 
 
-@pytest.mark.parametrize("m,n,k", [(256, 256, 256), (512, 256, 1024), (256, 256, 5120),
-                                   (512, 256, 8192), (256, 768, 5376)])
+@pytest.mark.parametrize("m,n,k", [(256, 256, 256), (512, 256, 1024), (512, 512, 2048),
+                                   (256, 512, 2304), (256, 256, 5120), (512, 256, 8192),
+                                   (256, 768, 5376)])
 def test_row_major_full_tiles(dev, m, n, k):
     say("dma16", m, n, k)
     rng = np.random.default_rng(m + n + k)
@@ -110,6 +111,29 @@ def test_packed_dma_rows_equal_row_major_and_the_oracle(dev):
     assert np.array_equal(Cp, Cr) and np.array_equal(Cr, C128)
     for rows in (slice(0, 256), slice(1792, 2048), slice(m - 256, m)):
         assert np.array_equal(Cr[rows], go.gemm_i8_f64(A[rows], B)), rows
+
+
+@pytest.mark.parametrize("k", [2304, 4096])
+def test_packed_dma_rows_with_d(dev, k):
+    """Packed B with D on the 256x256 kernel: 4096 x 2048 (128 tiles) plus
+    100 rows on 128x128 tiles, out of place and in place."""
+    m, n = 4096 + 100, 2048
+    rng = np.random.default_rng(k)
+    A = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    B = rng.integers(-128, 128, (k, n), dtype=np.int8)
+    D = rng.integers(-2**30, 2**30, (m, n), dtype=np.int32)
+    plan = hg.make_plan(m, n, k, has_d=True, d_max_abs=2**30, variant=hg.PACKED_VARIANT)
+    assert hg.packed_dma_rows(plan) == 4096
+    say("packed dma16 with D", m, n, k)
+    At, Bp = to_dev(dev, A), hg.pack_b(to_dev(dev, B))
+    Dt = to_dev(dev, D)
+    C = hg.run(plan, At, Bp, Dt).cpu().numpy()
+    C2 = hg.run(plan, At, Bp, Dt, out=Dt).cpu().numpy()
+    for rows in (slice(0, 256), slice(2048, 2304), slice(3840, 4196)):
+        want = go.gemm_i8(A[rows], B, D[rows])
+        assert np.array_equal(C[rows], want), rows
+        assert np.array_equal(C2[rows], want), rows
+    assert np.array_equal(C, C2)
 
 
 def test_k_not_a_multiple_of_256(dev):
