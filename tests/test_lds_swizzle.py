@@ -234,3 +234,19 @@ def test_epilogue_round_trip_matches_accumulator_layout():
     assert not np.array_equal(simulate_epilogue(acc, write=swapped), want)
     unswizzled_read = lambda lane, j: (2 * j + (lane >> 5)) * 512 + (lane & 31) * 16
     assert not np.array_equal(simulate_epilogue(acc, read=unswizzled_read), want)
+
+
+def test_strip_lane_bases_equal_strip_off():
+    """The epilogue addresses the strip as per-lane bases plus immediate
+    offsets (strip_lanes in vt_hip_gemm.hip): writes wb[ni % 4] + 512 e +
+    64 (ni & 4), reads rb[j / 2] + 1024 j. Both equal strip_off's layout."""
+    for lane in range(64):
+        g = lane >> 4
+        wb = [2048 * g + (((k ^ g) & 3) << 6) + (lane & 15) * 4 for k in range(4)]
+        rb = [512 * (lane >> 5) + (((lane & 31) ^ (m << 2)) << 4) for m in range(4)]
+        for ni in range(8):
+            for e in range(4):
+                assert wb[ni & 3] + 512 * e + 64 * (ni & 4) == strip_write_addr(lane, ni, e)
+                assert 512 * e + 64 * (ni & 4) < 65536
+        for j in range(8):
+            assert rb[j >> 1] + 1024 * j == strip_read_addr(lane, j)

@@ -817,39 +817,70 @@ __device__ __forceinline__ int strip_off(int row, int chunk) {
   return row * 512 + ((chunk ^ (((row >> 2) & 3) << 2)) << 4);
 }
 
-template <int MI, int NI, bool HAS_D>
+// Per-lane addressing of the epilogue strip, computed once per kernel so
+// that every strip access is a base register plus an immediate offset.
+// Write of element e of block ni (strip row 4 g + e, g = lane / 16, column
+// 16 ni + lane % 16): strip_off gives wb[ni % 4] + 512 e + 64 (ni & 4), with
+// wb[k] = 2048 g + 64 ((k ^ g) % 4) + 4 (lane % 16). Read j (strip row
+// 2 j + lane / 32, chunk lane % 32): rb[j / 2] + 1024 j, with rb[m] =
+// 512 (lane / 32) + 16 ((lane % 32) ^ 4 m). The bases include the strip's own
+// offset in LDS. gofs_c / gofs_d: byte offset of the lane's 16 bytes from the
+// start of its row pair (row 2 j of the strip, the wave's first column).
+struct StripLanes {
+  int wb[4], rb[4];
+  uint32_t gofs_c, gofs_d;
+};
+
+__device__ __forceinline__ StripLanes strip_lanes(int lane, int strip_base, int64_t ldc, int64_t ldd) {
+  StripLanes s;
+  const int g = lane >> 4;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) s.wb[k] = strip_base + 2048 * g + (((k ^ g) & 3) << 6) + (lane & 15) * 4;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) s.rb[m] = strip_base + 512 * (lane >> 5) + (((lane & 31) ^ (m << 2)) << 4);
+  s.gofs_c = (uint32_t)(((lane >> 5) * ldc + (lane & 31) * 4) * 4);
+  s.gofs_d = (uint32_t)(((lane >> 5) * ldd + (lane & 31) * 4) * 4);
+  return s;
+}
+
+// One 16-row strip of store_tile16_lds: Cs / Ds point at the strip's first
+// row and the wave's first column.
+template <int NI, bool HAS_D>
+__device__ __forceinline__ void store_strip16_lds(const v4i (&acc)[NI], int32_t *Cs,
+                                                  const int32_t *Ds, int64_t ldc, int64_t ldd,
+                                                  const StripLanes &sl, LDS_AS int8_t *lds) {
+  static_assert(NI * 16 == 128, "two 512-byte rows per wave instruction");
+#pragma unroll
+  for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      *(LDS_AS int32_t *)(lds + sl.wb[ni & 3] + e * 512 + (ni & 4) * 64) = acc[ni][e];
+  v4i v[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = *(LDS_AS v4i *)(lds + sl.rb[j >> 1] + j * 1024);
+  if constexpr (HAS_D) {
+    v4i d[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      d[j] = *(const v4i *)((const int8_t *)(Ds + 2 * j * ldd) + sl.gofs_d);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[j][q] = add_wrap(v[j][q], d[j][q]);
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    __builtin_nontemporal_store(v[j], (v4i *)((int8_t *)(Cs + 2 * j * ldc) + sl.gofs_c));
+}
+
+template <int MI, int NI, bool HAS_D, int FIRST = 0>
 __device__ __forceinline__ void store_tile16_lds(const v4i (&acc)[MI][NI], int32_t *Cb,
                                                  const int32_t *Db, int64_t ldc, int64_t ldd,
-                                                 int row0, int col0, int lane,
-                                                 LDS_AS int8_t *strip) {
-  static_assert(NI * 16 == 128, "two 512-byte rows per wave instruction");
-  const int c = lane & 15, g = lane >> 4;
+                                                 const StripLanes &sl, LDS_AS int8_t *lds) {
 #pragma unroll
-  for (int mi = 0; mi < MI; ++mi) {
-#pragma unroll
-    for (int ni = 0; ni < NI; ++ni)
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        *(LDS_AS int32_t *)(strip + strip_off(4 * g + e, ni * 4 + (c >> 2)) + (c & 3) * 4) =
-            acc[mi][ni][e];
-    v4i v[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      v[j] = *(LDS_AS v4i *)(strip + strip_off(2 * j + (lane >> 5), lane & 31));
-    const int64_t r0 = row0 + mi * 16 + (lane >> 5);
-    const int col = col0 + (lane & 31) * 4;
-    if constexpr (HAS_D) {
-      v4i d[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) d[j] = *(const v4i *)(Db + (r0 + 2 * j) * ldd + col);
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) v[j][q] = add_wrap(v[j][q], d[j][q]);
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      __builtin_nontemporal_store(v[j], (v4i *)(Cb + (r0 + 2 * j) * ldc + col));
+  for (int mi = FIRST; mi < MI; ++mi) {
+    store_strip16_lds<NI, HAS_D>(acc[mi], Cb + mi * 16 * ldc, HAS_D ? Db + mi * 16 * ldd : nullptr,
+                                 ldc, ldd, sl, lds);
     __builtin_amdgcn_sched_barrier(0);
   }
 }
@@ -1042,11 +1073,21 @@ __global__ __launch_bounds__(256, 1) void gemm_dma16_kernel(GemmArgs p) {
       else fb[u >> 1].zw = ld_lds_tr8(Bs, b_frag[u >> 1] + 8 * BN);
     }
   };
+  // The early step's C placement (set per tile) and the wave's strip.
+  constexpr int EARLY_STRIPS = (64 - DMAS - 15 + 8) / 8 < 6 ? (64 - DMAS - 15 + 8) / 8 : 6;
+  static_assert(8 * EARLY_STRIPS + DMAS <= 63, "vmcnt counts at most 63");
+  int32_t *c_tile = nullptr;   // the wave's block of C in the current tile
+  LDS_AS int8_t *const lds = (LDS_AS int8_t *)smem;
+  const StripLanes sl = strip_lanes(lane, NSTAGE * (A_BYTES + B_BYTES) + wave * 8192, p.ldc, p.ldd);
   // One step: MFMAs of slice gs, row by row, from fa and fb; slice gs + 1's B
   // blocks go to gb in the first BU slots (block order = first use), its A
   // blocks to fa as each row's last MFMA retires.
   // stg = gs % 4, a compile-time constant at every call.
-  auto step = [&](int stg, v4i *fb, v4i *gb) {
+  // early (compile time; the last step of a tile without D): strips 0 ..
+  // EARLY_STRIPS - 1 of the tile's C go out during the step, strip r at slot
+  // 8 r + 15, 8 MFMAs after row r's last one, beside the other rows' MFMAs.
+  auto step = [&](auto early, int stg, v4i *fb, v4i *gb) {
+    constexpr bool EARLY = decltype(early)::value;
     const int s1 = (stg + 1) & 3, s3 = (stg + 3) & 3;
     const int8_t *abase, *bbase;
     next_bases(abase, bbase);   // slice gs + 3
@@ -1063,13 +1104,26 @@ __global__ __launch_bounds__(256, 1) void gemm_dma16_kernel(GemmArgs p) {
         if (d < DPW) dma_b128(abase, a_lane[d], ma + d * 1024);
         else dma_b128(bbase, b_lane[d - DPW], mb + (d - DPW) * 1024);
       }
+      if constexpr (EARLY) {
+        if (slot >= 15 && (slot - 15) % 8 == 0 && (slot - 15) / 8 < EARLY_STRIPS) {
+          // The slot barriers keep the strip's AGPR reads here, at least 8
+          // MFMAs after row r's last one (tests/test_dma_asm.py checks the
+          // distance in the compiled code); a pin (an empty asm redefining
+          // the accumulators) made the register allocator spill.
+          const int r = (slot - 15) / 8;
+          store_strip16_lds<NI, false>(acc[r], c_tile + r * 16 * p.ldc, nullptr, p.ldc, p.ldd, sl, lds);
+        }
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
-    // Slice gs + 2 has landed (only slice gs + 3's DMAs remain in flight;
-    // older stores are waited for as well); after the barrier every wave may
-    // read it, and stage gs % 4 (read in step gs - 1) may be refilled.
-    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" :: "n"(DMAS) : "memory");
+    // Slice gs + 2 has landed (only slice gs + 3's DMAs, and in the early
+    // step the strips' 8 stores each, remain in flight; older stores are
+    // waited for as well); after the barrier every wave may read it, and
+    // stage gs % 4 (read in step gs - 1) may be refilled.
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" :: "n"(DMAS + (EARLY ? 8 * EARLY_STRIPS : 0)) : "memory");
   };
+  using Plain = std::integral_constant<bool, false>;
+  using Early = std::integral_constant<bool, !HAS_D>;
 
   issue_slice(0);
   issue_slice(1);
@@ -1088,20 +1142,34 @@ __global__ __launch_bounds__(256, 1) void gemm_dma16_kernel(GemmArgs p) {
     // KT is a multiple of 4 (the host requires K % 256 == 0), so every tile
     // starts at stage 0 with register set 0, and stages and sets rotate
     // statically.
-    for (int kt = 0; kt < KT; kt += 4, gs += 4) {
-      step(0, fb0, fb1);
-      step(1, fb1, fb0);
-      step(2, fb0, fb1);
-      step(3, fb1, fb0);
+    int bidx, m0, n0;
+    tile_coords(it, bidx, m0, n0);
+    c_tile = p.C + bidx * p.sc + (int64_t)(m0 + wm * WTM) * p.ldc + n0 + wn * WTN;
+    // Without D the tile's last iteration is peeled: its last step stores
+    // the first EARLY_STRIPS strips of C (straight-line code: a branch over
+    // steps that write the accumulators makes the register allocator
+    // shuffle them).
+    const int KL = HAS_D ? KT : KT - 4;
+    for (int kt = 0; kt < KL; kt += 4, gs += 4) {
+      step(Plain(), 0, fb0, fb1);
+      step(Plain(), 1, fb1, fb0);
+      step(Plain(), 2, fb0, fb1);
+      step(Plain(), 3, fb1, fb0);
+    }
+    if constexpr (!HAS_D) {
+      step(Plain(), 0, fb0, fb1);
+      step(Plain(), 1, fb1, fb0);
+      step(Plain(), 2, fb0, fb1);
+      step(Early(), 3, fb1, fb0);
+      gs += 4;
     }
     // The last MFMAs' result latency before the epilogue reads any AGPR.
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
     fence_acc();
-    int bidx, m0, n0;
-    tile_coords(it, bidx, m0, n0);
-    store_tile16_lds<MI, NI, HAS_D>(acc, p.C + bidx * p.sc, HAS_D ? p.D + bidx * p.sd : nullptr,
-                                    p.ldc, p.ldd, m0 + wm * WTM, n0 + wn * WTN, lane,
-                                    (LDS_AS int8_t *)smem + NSTAGE * (A_BYTES + B_BYTES) + wave * 8192);
+    store_tile16_lds<MI, NI, HAS_D, HAS_D ? 0 : EARLY_STRIPS>(
+        acc, c_tile,
+        HAS_D ? p.D + bidx * p.sd + (int64_t)(m0 + wm * WTM) * p.ldd + n0 + wn * WTN : nullptr,
+        p.ldc, p.ldd, sl, lds);
     zero_acc();
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
