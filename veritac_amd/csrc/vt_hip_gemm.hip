@@ -2049,15 +2049,19 @@ constexpr int kDmaWaves = 4;
 // Full 256x256 tiles run on gemm_dma16_kernel (16x16x64) when K is a whole
 // number of 256-deep groups of four slices and its epilogue's 16-byte C and D
 // accesses are aligned (C, D 16-byte aligned; ldc, ldd and the batch strides
-// multiples of 4 elements); otherwise on gemm_dma_kernel (32x32x32, 4-byte
-// stores). Measured per launch (HIP graphs, two passes), 16x16x64 against
+// multiples of 4 elements, ldc and ldd below 2^29); otherwise on
+// gemm_dma_kernel (32x32x32, 4-byte stores, 64-bit row addresses). Measured per launch (HIP graphs, two passes), 16x16x64 against
 // 32x32x32 at 8192 x 8192 x K: K = 256 58-61 against 62-63 us, 1024 91-99
 // against 99, 2048 139-145 against 149-150, 4096 226-229 against 245-249,
 // 8192 400 against 447, 8192 with D 459 against 518; config 3 (K = 1024) 46-49
 // against 49; 4096^3 60-69 against 66-67.
 bool use_dma16(const Problem &r) {
-  const bool c_ok = aligned16(r.C) && r.ldc % 4 == 0 && (r.batch == 1 || r.sc % 4 == 0);
-  const bool d_ok = !r.D || (aligned16(r.D) && r.ldd % 4 == 0 && (r.batch == 1 || r.sd % 4 == 0));
+  // The epilogue also addresses a lane's 16 bytes as a 32-bit byte offset
+  // from its row pair's base (one row of ldc or ldd plus 512 bytes).
+  const bool c_ok = aligned16(r.C) && r.ldc % 4 == 0 && (r.batch == 1 || r.sc % 4 == 0) &&
+                    r.ldc < (1ll << 29);
+  const bool d_ok = !r.D || (aligned16(r.D) && r.ldd % 4 == 0 && (r.batch == 1 || r.sd % 4 == 0) &&
+                             r.ldd < (1ll << 29));
   return r.K % 256 == 0 && c_ok && d_ok;
 }
 
