@@ -44,7 +44,7 @@ DECODE_SETS = 10
 # profiles/ (FETCH_SIZE scaled by 2.00, WRITE_SIZE by 1.00: the factors a plain
 # 1 GiB copy gives). tests/test_traffic_profiles.py checks them against those
 # summaries, so a refreshed profile and these figures cannot drift apart.
-TRAFFIC_GEMM_8192 = {"read": 805.6e6, "written": 269.0e6}   # gemm_dma16_kernel
+TRAFFIC_GEMM_8192 = {"read": 805.7e6, "written": 268.7e6}   # gemm_dma16_kernel
 TRAFFIC_DECODE = {  # (packed B, M) -> bytes per step
     (False, 16): {"read": 58.9e6 + 3.7e6, "written": 3.95e6 + 0.92e6},
     (True, 16): {"read": 59.3e6, "written": 0.92e6},

@@ -17,6 +17,8 @@ from veritac_amd.specializations.hip_gemm import backend as hg
 
 pytestmark = pytest.mark.gpu
 
+INT32_MIN = -2**31
+
 
 @pytest.fixture(scope="module")
 def dev():
@@ -113,6 +115,41 @@ def test_packed_dma_rows_equal_row_major_and_the_oracle(dev):
         assert np.array_equal(Cr[rows], go.gemm_i8_f64(A[rows], B)), rows
 
 
+@pytest.mark.parametrize("shared", [True, False])
+def test_batches_without_d(dev, shared):
+    """Without D the tile's last step stores six of its eight C strips (the
+    rest after the loop); batches of unshared B are not folded, so tiles of
+    every batch index run in one launch."""
+    rng = np.random.default_rng(15 + shared)
+    batch, m, n, k = 3, 512, 256, 1024
+    A = rng.integers(-128, 128, (batch, m, k), dtype=np.int8)
+    B = rng.integers(-128, 128, (k, n) if shared else (batch, k, n), dtype=np.int8)
+    plan = hg.make_plan(m, n, k, batch=batch, b_shared=shared, variant="mfma_256x256")
+    say("dma16 batches without D", shared)
+    C = hg.run(plan, to_dev(dev, A), to_dev(dev, B)).cpu().numpy()
+    for b in range(batch):
+        assert np.array_equal(C[b], go.gemm_i8_f64(A[b], B if shared else B[b])), b
+
+
+@pytest.mark.parametrize("k", [256, 4096])
+def test_padded_ldc_without_d(dev, k):
+    """ldc = N + 4: 16-byte rows with padding, early strips, padding untouched."""
+    m, n = 256, 512
+    ldc = n + 4
+    rng = np.random.default_rng(k + 3)
+    A = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    B = rng.integers(-128, 128, (k, n), dtype=np.int8)
+    At, Bt = to_dev(dev, A), to_dev(dev, B)
+    Cbuf = torch.full((m, ldc), INT32_MIN, dtype=torch.int32, device=dev)
+    say("dma16 padded ldc without D", k)
+    _lib.gemm_raw(At.data_ptr(), Bt.data_ptr(), None, Cbuf.data_ptr(), m, n, k, k, n, n, ldc,
+                  variant="mfma_256x256")
+    _lib.sync(None)
+    C = Cbuf.cpu().numpy()
+    assert np.array_equal(C[:, :n], go.gemm_i8_f64(A, B))
+    assert (C[:, n:] == INT32_MIN).all()
+
+
 @pytest.mark.parametrize("k", [2304, 4096])
 def test_packed_dma_rows_with_d(dev, k):
     """Packed B with D on the 256x256 kernel: 4096 x 2048 (128 tiles) plus
@@ -146,8 +183,6 @@ def test_k_not_a_multiple_of_256(dev):
         plan = hg.make_plan(256, 256, k, variant="mfma_256x256")
         assert np.array_equal(run(dev, plan, A, B), go.gemm_i8_f64(A, B)), k
 
-
-INT32_MIN = -2**31
 
 
 @pytest.mark.parametrize("ldc,c_off,ldd,d_off", [
