@@ -50,9 +50,14 @@ extern "C" {
 
 /* Kernel variants. VT_VARIANT_AUTO picks one from the shape. */
 #define VT_VARIANT_AUTO 0
-#define VT_VARIANT_MFMA_256x256 1  /* compute-bound: 256x256 tile, 4 waves,
+#define VT_VARIANT_MFMA_256x256 1  /* compute-bound: 256x256 tile, 4 waves;
+                                      whole tiles with K % 256 == 0 and
+                                      16-byte C / D rows on
+                                      v_mfma_i32_16x16x64_i8 (C stored
+                                      through LDS), else
                                       v_mfma_i32_32x32x32_i8                  */
-#define VT_VARIANT_MFMA_128x128 2  /* 128x128 tile, 4 waves, same MFMA        */
+#define VT_VARIANT_MFMA_128x128 2  /* 128x128 tile, 4 waves,
+                                      v_mfma_i32_32x32x32_i8                  */
 #define VT_VARIANT_SKINNY 3        /* M <= 64 decode shapes: B streamed once,
                                       v_mfma_i32_16x16x64_i8, K split         */
 #define VT_VARIANT_GENERIC 4       /* any shape/stride/alignment, VALU        */
@@ -345,9 +350,9 @@ int vt_pack_b_i8(const int8_t *B, int8_t *Bp, int64_t K, int64_t N, int64_t ldb,
  * that overlaps B). Any M. The rows run on three kernels:
  *   - whole 256-row tiles, when N % 256 == 0, K % 64 == 0 and there are at
  *     least 128 such tiles over all batches: the persistent 256x256 MFMA
- *     kernel of vt_gemm_i8, which reads each 32 x 32 B operand with one
- *     ds_read_b128 (a 1 KiB tile holds 16 consecutive k per lane, the k
- *     order of its A operand);
+ *     kernels of vt_gemm_i8 (16x16x64 when K % 256 == 0, else 32x32x32),
+ *     which read each B operand with one ds_read_b128 (a 1 KiB tile holds
+ *     16 consecutive k per lane, the k order of the A operand);
  *   - more than 64 remaining rows: 128 x 128 MFMA tiles reading the packed
  *     tiles the same way, K split into up to 16 slices (a second kernel adds
  *     them) when fewer than 64 tiles would run, as vt_gemm_i8 does;
