@@ -9,8 +9,9 @@
 // kernel here relies on.
 //
 // Kernels
-//   gemm_dma16_kernel  full 256x256 tiles with K % 256 == 0, with or without
-//       D, row-major or packed B (the 8192^3 case). Persistent: one workgroup
+//   gemm_dma16_kernel  full 256x256 tiles with K % 256 == 0 and 16-byte C
+//       (and D) rows, with or without D, row-major or packed B (the 8192^3
+//       case and config 3). Persistent: one workgroup
 //       per CU walks its tiles in XCD-contiguous order; k slices go global ->
 //       LDS by direct-to-LDS DMA (global_load_lds_dwordx4) into four stages,
 //       three slices ahead, and the slice stream runs across tile
@@ -18,9 +19,13 @@
 //       accumulators (half the accumulator traffic per multiply-add of the
 //       32x32x32 form, so more work per joule under the board's power limit);
 //       the MFMA, fragment-read and DMA instructions follow an explicit
-//       per-slot schedule.
-//   gemm_dma_kernel  the same on 4 x 4 v_mfma_i32_32x32x32_i8 accumulators,
-//       for full tiles whose K is a multiple of 64 but not of 256.
+//       per-slot schedule. C leaves through an 8 KB LDS strip per wave as
+//       whole 512-byte row segments; without D, six of a tile's eight strips
+//       go out during its last k step.
+//   gemm_dma_kernel  the same on 4 x 4 v_mfma_i32_32x32x32_i8 accumulators
+//       (4-byte C stores), for full tiles the 16x16x64 kernel does not take:
+//       K a multiple of 64 but not of 256, or C / D rows it cannot store as
+//       16-byte pieces.
 //   gemm_mfma_kernel<BM,BN>  every other compute-bound case. 256 threads = 4
 //       waves in a 2x2 grid, each wave owns a (BM/2)x(BN/2) block of 32x32
 //       accumulators fed by v_mfma_i32_32x32x32_i8. A/B k-slices of 64 bytes
