@@ -818,19 +818,41 @@ __device__ __forceinline__ int b16_swz(int row) { return (row & 7) | (((row >> 4
 // one row. With D, the strip's D values (the same row-contiguous 16 bytes each
 // lane then stores) are all loaded before its stores; each lane reads its own
 // D bytes before writing them, so C may be D.
-__device__ __forceinline__ int strip_off(int row, int chunk) {
+__host__ __device__ constexpr int strip_off(int row, int chunk) {
   return row * 512 + ((chunk ^ (((row >> 2) & 3) << 2)) << 4);
 }
 
 // Per-lane addressing of the epilogue strip, computed once per kernel so
 // that every strip access is a base register plus an immediate offset.
 // Write of element e of block ni (strip row 4 g + e, g = lane / 16, column
-// 16 ni + lane % 16): strip_off gives wb[ni % 4] + 512 e + 64 (ni & 4), with
-// wb[k] = 2048 g + 64 ((k ^ g) % 4) + 4 (lane % 16). Read j (strip row
-// 2 j + lane / 32, chunk lane % 32): rb[j / 2] + 1024 j, with rb[m] =
-// 512 (lane / 32) + 16 ((lane % 32) ^ 4 m). The bases include the strip's own
-// offset in LDS. gofs_c / gofs_d: byte offset of the lane's 16 bytes from the
-// start of its row pair (row 2 j of the strip, the wave's first column).
+// 16 ni + lane % 16): wb[ni % 4] + 512 e + 64 (ni & 4). Read j (strip row
+// 2 j + lane / 32, chunk lane % 32): rb[j / 2] + 1024 j. The bases include
+// the strip's own offset in LDS. gofs_c / gofs_d: byte offset of the lane's
+// 16 bytes from the start of its row pair (row 2 j of the strip, the wave's
+// first column).
+__host__ __device__ constexpr int strip_wb(int lane, int k) {
+  return 2048 * (lane >> 4) + (((k ^ (lane >> 4)) & 3) << 6) + (lane & 15) * 4;
+}
+__host__ __device__ constexpr int strip_rb(int lane, int m) {
+  return 512 * (lane >> 5) + (((lane & 31) ^ (m << 2)) << 4);
+}
+
+// The bases give strip_off's layout for every lane, block, element and read.
+constexpr bool strip_bases_match() {
+  for (int lane = 0; lane < 64; ++lane) {
+    const int g = lane >> 4, c = lane & 15;
+    for (int ni = 0; ni < 8; ++ni)
+      for (int e = 0; e < 4; ++e)
+        if (strip_wb(lane, ni & 3) + 512 * e + 64 * (ni & 4) !=
+            strip_off(4 * g + e, ni * 4 + (c >> 2)) + (c & 3) * 4)
+          return false;
+    for (int j = 0; j < 8; ++j)
+      if (strip_rb(lane, j >> 1) + 1024 * j != strip_off(2 * j + (lane >> 5), lane & 31)) return false;
+  }
+  return true;
+}
+static_assert(strip_bases_match(), "strip bases disagree with strip_off");
+
 struct StripLanes {
   int wb[4], rb[4];
   uint32_t gofs_c, gofs_d;
@@ -838,11 +860,10 @@ struct StripLanes {
 
 __device__ __forceinline__ StripLanes strip_lanes(int lane, int strip_base, int64_t ldc, int64_t ldd) {
   StripLanes s;
-  const int g = lane >> 4;
 #pragma unroll
-  for (int k = 0; k < 4; ++k) s.wb[k] = strip_base + 2048 * g + (((k ^ g) & 3) << 6) + (lane & 15) * 4;
+  for (int k = 0; k < 4; ++k) s.wb[k] = strip_base + strip_wb(lane, k);
 #pragma unroll
-  for (int m = 0; m < 4; ++m) s.rb[m] = strip_base + 512 * (lane >> 5) + (((lane & 31) ^ (m << 2)) << 4);
+  for (int m = 0; m < 4; ++m) s.rb[m] = strip_base + strip_rb(lane, m);
   s.gofs_c = (uint32_t)(((lane >> 5) * ldc + (lane & 31) * 4) * 4);
   s.gofs_d = (uint32_t)(((lane >> 5) * ldd + (lane & 31) * 4) * 4);
   return s;
