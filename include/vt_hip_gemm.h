@@ -51,11 +51,16 @@ extern "C" {
 /* Kernel variants. VT_VARIANT_AUTO picks one from the shape. */
 #define VT_VARIANT_AUTO 0
 #define VT_VARIANT_MFMA_256x256 1  /* compute-bound: 256x256 tile, 4 waves;
-                                      whole tiles with K % 256 == 0 and
+                                      M, N >= 256 with K % 256 == 0 and
                                       16-byte C / D rows on
                                       v_mfma_i32_16x16x64_i8 (C stored
                                       through LDS), else
-                                      v_mfma_i32_32x32x32_i8                  */
+                                      v_mfma_i32_32x32x32_i8; a partial
+                                      last tile row or column ends at M or
+                                      N, or (C = C + A.B in place, or when
+                                      it saves a round of tiles) the rows
+                                      past whole tiles run on 128x128
+                                      tiles                                   */
 #define VT_VARIANT_MFMA_128x128 2  /* 128x128 tile, 4 waves,
                                       v_mfma_i32_32x32x32_i8                  */
 #define VT_VARIANT_SKINNY 3        /* M <= 64 decode shapes: B streamed once,

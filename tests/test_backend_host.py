@@ -233,3 +233,46 @@ def test_mfma_k_split_mirrors_the_native_choice():
     assert hg.mfma_k_split(hg.make_plan(128, 4096, 4096)) == 8
     assert hg.mfma_k_split(hg.make_plan(128, 4096, 1024)) == 2     # slices of 512
     assert hg.mfma_k_split(hg.make_plan(128, 4096, 1152)) == 1     # 1152 = 9 x 128
+
+
+def test_mfma_row_split_mirrors_the_native_choice():
+    """Row-major 256x256 plans whose partial last tile row would add a round
+    of tiles run their whole tiles first and the other rows on 128x128 tiles.
+    The plan mirror names the same rows as the library: the workspace
+    vt_gemm_check reports is the remainder's K-split partial sums, and the
+    workgroups are both launches'."""
+    from veritac_amd import _lib
+    cases = {
+        (1100, 14336, 4096, 1): (1024, 76, 1),     # 224 + 56 tiles: 1 round -> 2
+        (2100, 8192, 1024, 1): (2048, 52, 2),      # 256 + 32; 52 rows on 64 tiles, K in 2
+        (100, 14336, 4096, 11): (1024, 76, 1),     # 11 shared-B batches folded to 1100 rows
+        (8000, 8192, 8192, 1): None,               # 992 and 1024 tiles: 4 rounds either way
+        (2000, 8192, 4096, 1): None,               # 224 and 256: one round
+        (300, 512, 256, 1): None,
+        (8192, 8192, 8192, 1): None,               # whole tiles
+        (1100, 14096, 4096, 1): None,              # N not whole tiles: one launch
+    }
+    for (m, n, k, batch), want in cases.items():
+        plan = hg.make_plan(m, n, k, batch=batch, b_shared=batch > 1, variant="mfma_256x256")
+        st, _, v, ks, ws = _lib.gemm_check(m, n, k, k, n, n, n, batch=batch,
+                                           stride_a=m * k if batch > 1 else 0,
+                                           stride_c=m * n if batch > 1 else 0,
+                                           variant="mfma_256x256")
+        assert st == _lib.VT_OK and v == "mfma_256x256" and ks == 0, (m, n, k)
+        parts = hg._mfma_parts(plan)
+        if want is None:
+            assert parts is None and hg.mfma_split_rows(plan) == 0 and ws == 0, (m, n, k)
+            continue
+        top, rest = parts
+        assert (top["m"], rest["m"], hg.mfma_k_split(rest)) == want, (m, n, k)
+        assert rest["variant"] == "mfma_128x128" and top["batch"] == rest["batch"] == 1
+        assert ws == (4 * want[2] * want[1] * n if want[2] > 1 else 0), (m, n, k)
+        wgs = top["m"] // 256 * (n // 256) + -(-rest["m"] // 128) * (n // 128) * want[2]
+        assert hg.required_resources(plan)[1] == wgs
+        assert "%d rows on the persistent 256x256 kernel" % top["m"] in hg.native_check(plan)[1]
+        # both launches priced, the first at whole tiles only
+        t = hg.modeled_objective(plan, hg.modeled_counts(plan))[0]
+        assert t == pytest.approx(sum(hg.modeled_objective(p, hg.modeled_counts(p))[0]
+                                      for p in parts))
+    # the 128x128 and 256x128 variants never split
+    assert hg._mfma_parts(hg.make_plan(1100, 14336, 4096, variant="mfma_128x128")) is None

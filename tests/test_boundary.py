@@ -314,18 +314,20 @@ def test_gemm_check_reports_padded_and_skinny_workspace():
 
 def test_select_follows_b_sharing():
     """The fold into a stacked-M GEMM needs one shared B: with per-batch B
-    the selection is the one vt_gemm_i8 makes for unshared batches."""
-    shared = _lib.select_variant(128, 51200, 128, 2, b_shared=True)
-    unshared = _lib.select_variant(128, 51200, 128, 2, b_shared=False)
-    assert shared == ("mfma_256x128", 0) and unshared == ("mfma_256x256", 0)
-    assert _lib.gemm_check(128, 51200, 128, 128, 51200, 51200, 51200, batch=2,
-                           stride_a=128 * 128, stride_b=128 * 51200,
-                           stride_c=128 * 51200)[2] == unshared[0]
-    assert _lib.gemm_check(128, 51200, 128, 128, 51200, 51200, 51200, batch=2,
-                           stride_a=128 * 128, stride_b=0,
-                           stride_c=128 * 51200)[2] == shared[0]
-    assert hg.make_plan(128, 51200, 128, batch=2)["variant"] == unshared[0]
-    assert hg.make_plan(128, 51200, 128, batch=2, b_shared=True)["variant"] == shared[0]
+    the selection is the one vt_gemm_i8 makes for unshared batches (two
+    batches of 64 rows: 400 tiles of 256x256, against 128 stacked rows on
+    128x128 tiles)."""
+    shared = _lib.select_variant(64, 51200, 128, 2, b_shared=True)
+    unshared = _lib.select_variant(64, 51200, 128, 2, b_shared=False)
+    assert shared == ("mfma_128x128", 0) and unshared == ("mfma_256x256", 0)
+    assert _lib.gemm_check(64, 51200, 128, 128, 51200, 51200, 51200, batch=2,
+                           stride_a=64 * 128, stride_b=128 * 51200,
+                           stride_c=64 * 51200)[2] == unshared[0]
+    assert _lib.gemm_check(64, 51200, 128, 128, 51200, 51200, 51200, batch=2,
+                           stride_a=64 * 128, stride_b=0,
+                           stride_c=64 * 51200)[2] == shared[0]
+    assert hg.make_plan(64, 51200, 128, batch=2)["variant"] == unshared[0]
+    assert hg.make_plan(64, 51200, 128, batch=2, b_shared=True)["variant"] == shared[0]
     lib = veritac_amd.load_library()
     v, ks = ctypes.c_int32(), ctypes.c_int32()
     assert lib.vt_gemm_select(16, 16, 16, 1, 16, 16, 4, ctypes.byref(v), ctypes.byref(ks)) \

@@ -1,0 +1,149 @@
+"""Row-major problems whose M or N is not a whole number of 256 tiles on the
+persistent 256x256 kernels (needs a gfx950 GPU), against the oracle through
+the C ABI.
+
+One launch takes them when M, N >= 256 and K is whole 64-deep slices: the
+last tile row (column) starts at M - 256 (N - 256), so its loads stay inside
+A and B, and it stores its neighbour's overlapping rows (columns) again with
+the same values. C = C + A.B in place cannot do that (the neighbour may
+already have added D), so there, and when the partial tile row would add a
+round of tiles, the whole 256-row tiles run first and the remaining rows on
+128x128 tiles. Cases cover both kernels (K % 256 == 0 on 16x16x64, other
+multiples of 64 on 32x32x32), D out of place and in place, batches, the
+split with a K-split remainder, and that nothing outside C's M x N block is
+written.
+"""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from oracle import gemm_oracle as go
+from veritac_amd import _lib
+from veritac_amd.specializations.hip_gemm import backend as hg
+
+pytestmark = pytest.mark.gpu
+
+INT32_MIN = -2**31
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    assert _lib.load_library().vt_device_count() >= 1, "GPU visible but not gfx950"
+    return torch.device("cuda", 0)
+
+
+def say(*args):
+    print(*args, flush=True)
+
+
+def to_dev(dev, x):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+
+
+def operands(m, n, k, seed, batch=None, d_bound=2**30):
+    rng = np.random.default_rng(seed)
+    lead = () if batch is None else (batch,)
+    A = rng.integers(-128, 128, lead + (m, k), dtype=np.int8)
+    B = rng.integers(-128, 128, lead + (k, n), dtype=np.int8)
+    A.reshape(-1)[:k] = -128             # an extreme row and column
+    B[..., :, 0] = -128
+    D = rng.integers(-d_bound, d_bound, lead + (m, n), dtype=np.int32)
+    return A, B, D
+
+
+def gemm_padded(dev, A, B, D, ldc, extra_rows, in_place=False):
+    """One vt_gemm_i8 call on mfma_256x256 with C inside a buffer of ldc
+    columns and extra_rows more rows, all poisoned: returns (C, buffer)."""
+    m, k = A.shape
+    n = B.shape[1]
+    At, Bt = to_dev(dev, A), to_dev(dev, B)
+    buf = torch.full((m + extra_rows, ldc), INT32_MIN, dtype=torch.int32, device=dev)
+    Dt, ldd = None, 0
+    if D is not None and in_place:
+        buf[:m, :n] = to_dev(dev, D)
+        Dt, ldd = buf, ldc
+    elif D is not None:
+        Dt, ldd = to_dev(dev, D), n
+    _lib.gemm_raw(At.data_ptr(), Bt.data_ptr(), Dt.data_ptr() if Dt is not None else None,
+                  buf.data_ptr(), m, n, k, k, n, ldd, ldc, variant="mfma_256x256")
+    _lib.sync(None)
+    got = buf.cpu().numpy()
+    return got[:m, :n], got
+
+
+@pytest.mark.parametrize("m,n,k", [
+    (300, 512, 256),      # M ragged, 16x16x64
+    (256, 272, 1024),     # N ragged by 16 columns
+    (520, 784, 2304),     # both, 16x16x64
+    (700, 1040, 320),     # both, 32x32x32 (K % 256 != 0)
+    (257, 257 + 15, 192),  # one row and 16 columns past a tile, 32x32x32
+])
+@pytest.mark.parametrize("with_d", [False, True])
+def test_last_tiles_moved_back(dev, m, n, k, with_d):
+    n = n // 16 * 16
+    say("edge tiles", m, n, k, "D" if with_d else "")
+    A, B, D = operands(m, n, k, m * 7 + n + k)
+    want = go.gemm_i8(A, B, D) if with_d else go.gemm_i8_f64(A, B)
+    C, buf = gemm_padded(dev, A, B, D if with_d else None, ldc=n + 4, extra_rows=3)
+    assert np.array_equal(C, want)
+    assert (buf[:m, n:] == INT32_MIN).all() and (buf[m:] == INT32_MIN).all()
+
+
+@pytest.mark.parametrize("m,n,k", [(300, 512, 256), (520, 784, 2304), (700, 1040, 320)])
+def test_in_place_on_ragged_tiles(dev, m, n, k):
+    """C = C + A.B: M ragged with whole N splits into the persistent kernel's
+    whole tiles and 128x128 tiles for the rest; N ragged runs on the edge
+    kernel. Either way no element adds D twice."""
+    n = n // 16 * 16
+    say("edge tiles in place", m, n, k)
+    A, B, D = operands(m, n, k, m + n + k + 1)
+    C, buf = gemm_padded(dev, A, B, D, ldc=n + 4, extra_rows=2, in_place=True)
+    assert np.array_equal(C, go.gemm_i8(A, B, D))
+    assert (buf[:m, n:] == INT32_MIN).all() and (buf[m:] == INT32_MIN).all()
+
+
+@pytest.mark.parametrize("shared", [False, True])
+def test_batches_with_ragged_rows(dev, shared):
+    """Unshared B: each batch's last tile row moves back inside that batch.
+    Shared B folds 3 x 100 rows into 300 stacked rows whose last tile spans
+    the batch boundaries."""
+    batch, m, n, k = 3, (100 if shared else 300), 512, 512
+    rng = np.random.default_rng(41 + shared)
+    A = rng.integers(-128, 128, (batch, m, k), dtype=np.int8)
+    B = rng.integers(-128, 128, (k, n) if shared else (batch, k, n), dtype=np.int8)
+    D = rng.integers(-1000, 1000, (batch, m, n), dtype=np.int32)
+    plan = hg.make_plan(m, n, k, batch=batch, b_shared=shared, has_d=True, d_max_abs=1000,
+                        variant="mfma_256x256")
+    say("edge tiles batches", shared)
+    C = hg.run(plan, to_dev(dev, A), to_dev(dev, B), to_dev(dev, D)).cpu().numpy()
+    for b in range(batch):
+        assert np.array_equal(C[b], go.gemm_i8(A[b], B if shared else B[b], D[b])), b
+
+
+@pytest.mark.parametrize("m,n,k,rest_split", [
+    (1100, 14336, 256, 1),    # 224 whole tiles + 56 partial: the split saves a round
+    (2100, 8192, 1024, 2),    # 256 + 32: the remaining 52 rows run with K in 2 slices
+])
+def test_split_when_the_partial_row_adds_a_round(dev, m, n, k, rest_split):
+    plan = hg.make_plan(m, n, k, has_d=True, d_max_abs=2**30, variant="mfma_256x256")
+    top, rest = hg._mfma_parts(plan)
+    assert top["m"] == m // 256 * 256 and rest["m"] == m % 256
+    assert hg.mfma_k_split(rest) == rest_split
+    ok, reason = hg.native_check(plan)
+    assert ok and "%d rows on the persistent 256x256 kernel, %d on 128x128 tiles" % (
+        top["m"], rest["m"]) in reason, reason
+    say("edge tiles split", m, n, k)
+    A, B, D = operands(m, n, k, m + n)
+    At, Bt, Dt = to_dev(dev, A), to_dev(dev, B), to_dev(dev, D)
+    C = hg.run(plan, At, Bt, Dt).cpu().numpy()
+    C128 = hg.run(hg.make_plan(m, n, k, has_d=True, d_max_abs=2**30, variant="mfma_128x128"),
+                  At, Bt, Dt).cpu().numpy()
+    assert np.array_equal(C, C128)
+    C2 = hg.run(plan, At, Bt, Dt, out=Dt).cpu().numpy()      # in place
+    assert np.array_equal(C2, C)
+    cut = m // 256 * 256
+    for rows in (slice(0, 64), slice(cut - 64, cut + 16), slice(m - 40, m)):
+        assert np.array_equal(C[rows], go.gemm_i8(A[rows], B, D[rows])), rows

@@ -9,9 +9,13 @@
 // kernel here relies on.
 //
 // Kernels
-//   gemm_dma16_kernel  full 256x256 tiles with K % 256 == 0 and 16-byte C
-//       (and D) rows, with or without D, row-major or packed B (the 8192^3
-//       case and config 3). Persistent: one workgroup
+//   gemm_dma16_kernel  256x256 tiles with M, N >= 256, K % 256 == 0 and
+//       16-byte C (and D) rows, with or without D, row-major or packed B (the
+//       8192^3 case and config 3). When M or N is not whole tiles, the last
+//       tile row or column starts at M - 256 or N - 256 and stores its
+//       neighbour's overlapping values again, unchanged (not for C = C + A.B
+//       in place: its whole tiles run here, the other rows on 128x128 tiles).
+//       Persistent: one workgroup
 //       per CU walks its tiles in XCD-contiguous order; k slices go global ->
 //       LDS by direct-to-LDS DMA (global_load_lds_dwordx4) into four stages,
 //       three slices ahead, and the slice stream runs across tile
@@ -23,9 +27,9 @@
 //       whole 512-byte row segments; without D, six of a tile's eight strips
 //       go out during its last k step.
 //   gemm_dma_kernel  the same on 4 x 4 v_mfma_i32_32x32x32_i8 accumulators
-//       (4-byte C stores), for full tiles the 16x16x64 kernel does not take:
-//       K a multiple of 64 but not of 256, or C / D rows it cannot store as
-//       16-byte pieces.
+//       (4-byte C stores), for the problems the 16x16x64 kernel does not
+//       take: K a multiple of 64 but not of 256, or C / D rows it cannot
+//       store as 16-byte pieces.
 //   gemm_mfma_kernel<BM,BN>  every other compute-bound case. 256 threads = 4
 //       waves in a 2x2 grid, each wave owns a (BM/2)x(BN/2) block of 32x32
 //       accumulators fed by v_mfma_i32_32x32x32_i8. A/B k-slices of 64 bytes
@@ -539,8 +543,10 @@ __device__ __forceinline__ void dma_b128(const int8_t *base, uint32_t voff, uint
                :: "v"(voff), "s"(base), "s"(m0));
 }
 
-// Same contract as gemm_mfma_kernel<256, 256, 0, HAS_D, false> (full tiles only:
-// M % 256 == 0, N % 256 == 0, K % 64 == 0), but the k slices go global -> LDS
+// Same contract as gemm_mfma_kernel<256, 256, EDGE, HAS_D, false> for
+// M, N >= 256 and K % 64 == 0 (a last tile row or column that would pass M or
+// N starts at M - 256 or N - 256 instead, so no load or store leaves A, B, C
+// or D; C = C + A.B in place needs whole tiles), but the k slices go global -> LDS
 // by DMA (no VGPR staging, no ds_write instructions) and the kernel is
 // persistent: one workgroup per CU walks its tiles in order and the slice
 // stream runs on across tile boundaries, so the last steps of a tile already
@@ -607,8 +613,11 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_dma_kernel(GemmArgs p) {
     const int first_m = gid * p.group_m;
     const int gm = min(p.tiles_m - first_m, p.group_m);
     const int within = t - gid * group;
-    m0 = (first_m + within % gm) * BM;
-    n0 = (within / gm) * BN;
+    // A last tile row or column past M or N is moved back to end at M or N
+    // (the launch ensures M, N >= 256): it recomputes rows or columns of its
+    // neighbour and stores the same values there.
+    m0 = min((first_m + within % gm) * BM, p.M - BM);
+    n0 = min((within / gm) * BN, p.N - BN);
   };
 
   const int64_t lda = p.lda, ldb = p.ldb;
@@ -978,8 +987,8 @@ __global__ __launch_bounds__(256, 1) void gemm_dma16_kernel(GemmArgs p) {
     const int first_m = gid * p.group_m;
     const int gm = min(p.tiles_m - first_m, p.group_m);
     const int within = t - gid * group;
-    m0 = (first_m + within % gm) * BM;
-    n0 = (within / gm) * BN;
+    m0 = min((first_m + within % gm) * BM, p.M - BM);   // last tiles end at M, N
+    n0 = min((within / gm) * BN, p.N - BN);
   };
 
   const int64_t lda = p.lda, ldb = p.ldb;
@@ -2058,7 +2067,13 @@ int select_variant(const Problem &q, bool vec, int32_t *variant, int32_t *k_spli
   const int64_t m_eff = fold ? q.M * q.batch : q.M;
   const int64_t b_eff = fold ? 1 : q.batch;
   const int64_t t256 = (m_eff + 255) / 256 * ((q.N + 255) / 256) * b_eff;
-  if (t256 >= 256 && q.N >= 256) {
+  // The persistent kernel (K whole 64-deep slices, M, N >= 256) beats the
+  // smaller tiles once its tiles cover more than half the chip: N = 4096,
+  // K = 4096, 160 tiles 49.2 us against 59.3 (128x128) and 61.9 (256x128),
+  // 224 tiles 56.3 against 70.7; at 128 tiles 256x128 is ahead (43.0 against
+  // 46.8 us), and from 96 down the smaller tiles are.
+  const bool persistent = q.K % 64 == 0 && m_eff >= 256 && q.N >= 256;
+  if ((t256 >= 256 && q.N >= 256) || (persistent && t256 > 128)) {
     *variant = VT_VARIANT_MFMA_256x256;
   } else {
     const int64_t t128 = (m_eff + 255) / 256 * ((q.N + 127) / 128) * b_eff;
@@ -2069,10 +2084,10 @@ int select_variant(const Problem &q, bool vec, int32_t *variant, int32_t *k_spli
 }
 
 
-// Waves per workgroup of the persistent full-tile kernel.
+// Waves per workgroup of the persistent 256x256 kernel.
 constexpr int kDmaWaves = 4;
 
-// Full 256x256 tiles run on gemm_dma16_kernel (16x16x64) when K is a whole
+// Persistent 256x256 problems run on gemm_dma16_kernel (16x16x64) when K is a whole
 // number of 256-deep groups of four slices and its epilogue's 16-byte C and D
 // accesses are aligned (C, D 16-byte aligned; ldc, ldd and the batch strides
 // multiples of 4 elements, ldc and ldd below 2^29); otherwise on
@@ -2139,6 +2154,42 @@ int mfma_k_split(const Problem &r) {
   return ks;
 }
 
+bool same_buffer(const int32_t *D, const int32_t *C) { return D && (const void *)D == (const void *)C; }
+
+// Whether the persistent 256x256 kernels take a row-major problem: K in whole
+// 64-deep slices and M, N at least one tile (N is a multiple of 16 on every
+// vector path). A last tile row or column past M or N is moved back to end
+// there and stores its neighbour's rows or columns again with the same
+// values, which is exact unless C is D itself: then the neighbour may already
+// have added D, so ragged in-place problems stay off this path.
+bool persistent_fits(const Problem &r) {
+  const bool whole = r.M % 256 == 0 && r.N % 256 == 0;
+  return r.K > 0 && r.K % 64 == 0 && r.M >= 256 && r.N >= 256 &&
+         (whole || !same_buffer(r.D, r.C));
+}
+
+// Rows of a row-major 256x256 problem (after the fold) that run on the
+// persistent kernel before the rest run on 128x128 tiles: the whole 256-row
+// tiles, when N is whole tiles and either C is D itself or the last, partial
+// tile row would add a round of tiles on a 256-CU chip (M = 1100, N = 14336,
+// K = 4096: 224 + 56 tiles; 114 us as 280 tiles, 78 us split). 0: one launch.
+int64_t mfma_split_rows(const Problem &r) {
+  if (r.M < 256 || r.M % 256 == 0 || r.N % 256 || r.K == 0 || r.K % 64) return 0;
+  const int64_t row_tiles = r.N / 256 * r.batch, full = r.M / 256 * row_tiles;
+  const bool more_rounds = (full + row_tiles + kSplitCus - 1) / kSplitCus > (full + kSplitCus - 1) / kSplitCus;
+  return same_buffer(r.D, r.C) || more_rounds ? r.M / 256 * 256 : 0;
+}
+
+// Rows [r0, M) of a problem, in every batch.
+Problem rows_from(const Problem &r, int64_t r0) {
+  Problem g = r;
+  g.A = r.A + r0 * r.lda;
+  g.C = r.C + r0 * r.ldc;
+  g.D = r.D ? r.D + r0 * r.ldd : nullptr;
+  g.M = r.M - r0;
+  return g;
+}
+
 // The K split vt_gemm_i8 launches for an MFMA variant (1 for the others).
 int mfma_split_for(const Problem &q, int32_t variant) {
   const Problem r = mfma_fold(q);
@@ -2171,6 +2222,14 @@ int launch_mfma(const Problem &q, Scratch &scr) {
   hipStream_t stream = (hipStream_t)scr.stream;
   const int num_cus = scr.st->num_cus;
   const int ks = mfma_k_split<BM, BN>(r);
+  if constexpr (!PACKED && BM == 256 && BN == 256) {
+    if (const int64_t rows = ks == 1 ? mfma_split_rows(r) : 0) {
+      Problem top = r;
+      top.M = rows;
+      if (int rc = launch_mfma_tiles<BM, BN, PACKED>(top, stream, num_cus)) return rc;
+      return launch_mfma<128, 128, false>(rows_from(r, rows), scr);
+    }
+  }
   if (ks == 1) return launch_mfma_tiles<BM, BN, PACKED>(r, stream, num_cus);
   // K slices as batches: slice i reads A columns and B rows [i*kc, (i+1)*kc)
   // and writes its partial sums to slice i of the workspace.
@@ -2217,7 +2276,7 @@ int launch_mfma_tiles(const Problem &r, hipStream_t stream, int num_cus) {
   const bool has_d = r.D != nullptr;
   dim3 grid((unsigned)blocks), block(256);
   a.batch_count = (int)r.batch;
-  if (!PACKED && BM == 256 && BN == 256 && !(r.M % BM) && !(r.N % BN) && !(r.K % 64)) {
+  if (!PACKED && BM == 256 && BN == 256 && persistent_fits(r)) {
     // Persistent: one workgroup per CU (the kernel's LDS allows no more).
     const int64_t g = blocks < num_cus ? blocks : num_cus;
     dim3 pgrid((unsigned)g);
@@ -2635,6 +2694,12 @@ int64_t scratch_need(const Problem &q, int32_t variant, int32_t k_split) {
       variant == VT_VARIANT_MFMA_256x128) {
     const int ks = mfma_split_for(q, variant);
     const Problem r = mfma_fold(q);
+    const int64_t rows = variant == VT_VARIANT_MFMA_256x256 && ks == 1 ? mfma_split_rows(r) : 0;
+    if (rows) {   // the rows after the persistent kernel's, on 128x128 tiles
+      const Problem g = mfma_fold(rows_from(r, rows));
+      const int ks2 = mfma_k_split<128, 128>(g);
+      return ks2 > 1 ? round256(ks2 * g.M * g.N * 4) : 0;
+    }
     return ks > 1 ? round256(ks * r.M * r.N * 4) : 0;
   }
   if (variant != VT_VARIANT_PADDED || !padded_fits(q)) return 0;

@@ -190,6 +190,39 @@ def mfma_k_split(plan):
     return ks
 
 
+def mfma_split_rows(plan):
+    """Rows of an mfma_256x256 plan (contiguous shared-B batches folded into
+    m) that vt_gemm_i8 runs on the persistent 256x256 kernel before the rest
+    run on 128x128 tiles (mfma_split_rows in the HIP source): the whole
+    256-row tiles, when n is whole tiles and the last, partial tile row would
+    add a round of tiles on 256 CUs. 0: one launch, whose last tile row, when
+    partial, is moved back to end at m. (C = C + A.B in place also splits; a
+    plan does not know its buffers.)"""
+    if plan["variant"] != "mfma_256x256":
+        return 0
+    m, n, k, b = plan["m"], plan["n"], plan["k"], plan["batch"]
+    if plan["b_shared"] and b > 1:
+        m, b = m * b, 1
+    if m < 256 or m % 256 == 0 or n % 256 or k == 0 or k % 64:
+        return 0
+    row_tiles = n // 256 * b
+    full = m // 256 * row_tiles
+    return m // 256 * 256 if -(-(full + row_tiles) // NUM_CUS) > -(-full // NUM_CUS) else 0
+
+
+def _mfma_parts(plan):
+    """(rows on the persistent 256x256 kernel, the rest on 128x128 tiles) as
+    two plans, or None when mfma_split_rows is 0."""
+    rows = mfma_split_rows(plan)
+    if not rows:
+        return None
+    if plan["b_shared"] and plan["batch"] > 1:
+        plan = dict(plan, m=plan["m"] * plan["batch"], batch=1)
+    top = dict(plan, m=rows, k_split=0)
+    rest = dict(plan, m=plan["m"] - rows, variant="mfma_128x128", k_split=0)
+    return top, rest
+
+
 PACKED_DMA_MIN_TILES = 128   # kPackedDmaMinTiles in the HIP source
 
 
@@ -246,6 +279,11 @@ def required_resources(plan):
     tm, tn, _, _, lds = TILES[variant]
     m, n, batch = plan["m"], plan["n"], plan["batch"]
     if variant.startswith("mfma"):
+        parts = _mfma_parts(plan)
+        if parts is not None:   # whole tiles on the persistent kernel, then the rest
+            top, rest = parts
+            lds_r, wgs_r = required_resources(rest)
+            return max(lds, lds_r), top["m"] // tm * (n // tn) * top["batch"] + wgs_r
         if plan["b_shared"] and batch > 1:      # stacked-M fold
             m, batch = m * batch, 1
         return lds, -(-m // tm) * -(-n // tn) * batch * mfma_k_split(plan)
@@ -410,7 +448,10 @@ def modeled_counts(plan):
     lds, wgs = required_resources(plan)
     ops = 2 * b * m * n * k
     alg = algorithmic_bytes(plan)
-    if variant.startswith("mfma"):
+    parts = _mfma_parts(plan) if variant.startswith("mfma") else None
+    if parts is not None:
+        l2_bytes = sum(modeled_counts(p)["bytes_l2_modeled"] for p in parts)
+    elif variant.startswith("mfma"):
         m_eff, b_eff = (m * b, 1) if (plan["b_shared"] and b > 1) else (m, b)
         tiles_m, tiles_n = -(-m_eff // tm), -(-n // tn)
         # every tile reads its A row-panel and B column-panel once
@@ -486,6 +527,13 @@ def modeled_objective(plan, counts):
         copy_a, copy_b, copy_c = _padded_copies(plan)
         launches = int(copy_a or copy_b) + int(copy_c)
         return (t_inner + _padded_copy_bytes(plan, inner) / PEAK_HBM_BYTES + launches * _LAUNCH_S, wgs)
+    if variant.startswith("mfma") and _mfma_parts(plan) is not None:
+        # whole 256-row tiles on the persistent kernel, then 128x128 tiles
+        t, wgs = 0.0, 0
+        for part in _mfma_parts(plan):
+            tp, wp = modeled_objective(part, modeled_counts(part))
+            t, wgs = t + tp, wgs + wp
+        return t, wgs
     if variant == PACKED_VARIANT:
         parts = [p for p in _packed_parts(plan) if p is not None]
         if any(p["variant"] != PACKED_VARIANT for p in parts):
@@ -582,8 +630,13 @@ def native_check(plan):
     if variant != plan["variant"] and plan["variant"] != "auto":
         return False, ("vt_gemm_check would run %r for a %r plan (fail-closed)"
                        % (variant, plan["variant"]))
-    return True, "accepted by vt_gemm_check: runs %s (k_split %d, %d bytes of workspace)" % (
-        variant, ks, ws)
+    how = ""
+    parts = _mfma_parts(dict(plan, variant=variant))
+    if parts is not None:
+        how = "; %d rows on the persistent 256x256 kernel, %d on 128x128 tiles" % (
+            parts[0]["m"], parts[1]["m"])
+    return True, "accepted by vt_gemm_check: runs %s (k_split %d, %d bytes of workspace%s)" % (
+        variant, ks, ws, how)
 
 
 def gen_candidates(m, n, k, *, batch=1, b_shared=False, has_d=False, d_max_abs=0):
