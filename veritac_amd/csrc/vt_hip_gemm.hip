@@ -2067,18 +2067,24 @@ int select_variant(const Problem &q, bool vec, int32_t *variant, int32_t *k_spli
   const int64_t m_eff = fold ? q.M * q.batch : q.M;
   const int64_t b_eff = fold ? 1 : q.batch;
   const int64_t t256 = (m_eff + 255) / 256 * ((q.N + 255) / 256) * b_eff;
-  // The persistent kernel (K whole 64-deep slices, M, N >= 256) beats the
-  // smaller tiles once its tiles cover more than half the chip: N = 4096,
-  // K = 4096, 160 tiles 49.2 us against 59.3 (128x128) and 61.9 (256x128),
-  // 224 tiles 56.3 against 70.7; at 128 tiles 256x128 is ahead (43.0 against
-  // 46.8 us), and from 96 down the smaller tiles are.
+  // Below a full round of 256x256 tiles, the persistent kernel (K whole
+  // 64-deep slices, M, N >= 256) wins from more than half a round when K is
+  // long: N = 4096, K = 4096, 160 tiles 49.2 us against 59.3 (128x128) and
+  // 61.9 (256x128), 224 tiles 56.3 against 70.7; at 128 tiles 256x128 is
+  // ahead (43.0 against 46.8 us). With K = 1024 it wins only near a full
+  // round (224 tiles 24.7-25.9 us against 26.2-27.6; 192 tiles 23.1-25.3
+  // against 23.1-23.2 on 128x128), and at K <= 1024 128x128 beats 256x128
+  // (K = 512, 144-168 tiles: 14.8-15.0 us against 16.9-17.4). With K >= 4096
+  // 256x128 also wins at 192 of its tiles (96 of 256x256; M = 1536, N = 4096:
+  // 36.1 against 38.7 us, K = 8192 64.8 against 71.7).
   const bool persistent = q.K % 64 == 0 && m_eff >= 256 && q.N >= 256;
-  if ((t256 >= 256 && q.N >= 256) || (persistent && t256 > 128)) {
+  const int64_t t128 = (m_eff + 255) / 256 * ((q.N + 127) / 128) * b_eff;
+  if ((t256 >= 256 && q.N >= 256) ||
+      (persistent && ((q.K >= 2048 && t256 > 128) || (q.K >= 1024 && t256 > 192)))) {
     *variant = VT_VARIANT_MFMA_256x256;
   } else {
-    const int64_t t128 = (m_eff + 255) / 256 * ((q.N + 127) / 128) * b_eff;
-    *variant = (t128 >= 256 && m_eff >= 256) ? VT_VARIANT_MFMA_256x128
-                                              : VT_VARIANT_MFMA_128x128;
+    const bool wide = q.K >= 2048 && (t128 >= 256 || (q.K >= 4096 && t128 >= 192));
+    *variant = (wide && m_eff >= 256) ? VT_VARIANT_MFMA_256x128 : VT_VARIANT_MFMA_128x128;
   }
   return VT_OK;
 }
