@@ -147,3 +147,33 @@ def test_split_when_the_partial_row_adds_a_round(dev, m, n, k, rest_split):
     cut = m // 256 * 256
     for rows in (slice(0, 64), slice(cut - 64, cut + 16), slice(m - 40, m)):
         assert np.array_equal(C[rows], go.gemm_i8(A[rows], B, D[rows])), rows
+
+
+def test_extremes_on_moved_back_tiles(dev):
+    """K = 8192 with M and N both ragged: every product is the closed form."""
+    m, n, k = 300, 528, 8192
+    plan = hg.make_plan(m, n, k, variant="mfma_256x256")
+    A = np.full((m, k), -128, np.int8)
+    say("edge tiles extremes")
+    assert np.all(hg.run(plan, to_dev(dev, A), to_dev(dev, np.full((k, n), -128, np.int8)))
+                  .cpu().numpy() == 134217728)
+    assert np.all(hg.run(plan, to_dev(dev, A), to_dev(dev, np.full((k, n), 127, np.int8)))
+                  .cpu().numpy() == -133169152)
+
+
+def test_large_ragged_problem(dev):
+    """4000 x 4112 x 1024, both ragged, auto selection (256x256, 16 x 17
+    tiles): the whole output passes the projection check and the rows
+    around the moved-back tile row equal the oracle."""
+    from veritac_amd.specializations.hip_gemm import verify
+    m, n, k = 4000, 4112, 1024
+    plan = hg.make_plan(m, n, k)
+    assert plan["variant"] == "mfma_256x256" and hg._mfma_parts(plan) is None
+    A, B, _ = operands(m, n, k, 99)
+    At, Bt = to_dev(dev, A), to_dev(dev, B)
+    say("edge tiles large")
+    Ct = hg.run(plan, At, Bt)
+    assert verify.exact_check(At, Bt, Ct)["passed"]
+    C = Ct.cpu().numpy()
+    for rows in (slice(3700, 3800), slice(m - 60, m)):
+        assert np.array_equal(C[rows], go.gemm_i8_f64(A[rows], B)), rows
