@@ -4,8 +4,10 @@ with its scratch from the library's static array instead of allocations.
 Each case makes two calls in a row through the C ABI, the second smaller,
 and compares both outputs bit for bit with vt_gemm_i8 on the same operands
 (outputs poisoned with INT32_MIN first), and with the CPU oracle. The cases
-are the ones that take scratch: the decode kernel's K-split partial sums and
-the padded variant's copies (with an inner K split as well).
+are the ones that take scratch: the decode kernel's K-split partial sums,
+the padded variant's copies (with an inner K split as well), and the K-split
+partial sums of the rows a 256x256 problem runs on 128x128 tiles after its
+whole tiles.
 """
 import numpy as np
 import pytest
@@ -61,6 +63,10 @@ PAIRS = [
     ("decode explicit split", (16, 4096, 8192, "skinny", 16, True), (1, 1024, 2048, "skinny", 3, False)),
     ("padded", (1000, 1000, 1000, "auto", 0, True), (300, 500, 700, "padded", 0, False)),
     ("padded inner k-split", (16, 2047, 4095, "padded", 0, False), (5, 999, 1001, "padded", 0, True)),
+    # whole 256-row tiles on the persistent kernel, the last 52 (40) rows on
+    # 128x128 tiles with K in 2 slices
+    ("256x256 row split", (2100, 8192, 1024, "mfma_256x256", 0, True),
+     (4136, 4096, 1024, "mfma_256x256", 0, False)),
 ]
 
 
