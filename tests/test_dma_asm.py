@@ -18,12 +18,18 @@ import pytest
 
 from veritac_amd import build as vb
 
+def _k32(has_d, packed, edge=0):
+    """gemm_dma_kernel<4, HAS_D, PACKED_B, EDGE>"""
+    return "_ZN12_GLOBAL__N_115gemm_dma_kernelILi4ELb%dELb%dELb%dEEEvNS_8GemmArgsE" % (
+        has_d, packed, edge)
+
+
 # (mangled name, fragment reads of one 32-deep k step): 4 A blocks plus the
-# lo/hi halves of 4 row-major B blocks, or 4 whole packed B blocks
-KERNELS = {"no_d": ("_ZN12_GLOBAL__N_115gemm_dma_kernelILi4ELb0ELb0EEEvNS_8GemmArgsE", 12),
-           "with_d": ("_ZN12_GLOBAL__N_115gemm_dma_kernelILi4ELb1ELb0EEEvNS_8GemmArgsE", 12),
-           "packed_b": ("_ZN12_GLOBAL__N_115gemm_dma_kernelILi4ELb0ELb1EEEvNS_8GemmArgsE", 8),
-           "packed_b_with_d": ("_ZN12_GLOBAL__N_115gemm_dma_kernelILi4ELb1ELb1EEEvNS_8GemmArgsE", 8)}
+# lo/hi halves of 4 row-major B blocks, or 4 whole packed B blocks. The edge
+# kinds (last tiles moved back, masked stores) read row-major B.
+KERNELS = {"no_d": (_k32(0, 0), 12), "with_d": (_k32(1, 0), 12),
+           "packed_b": (_k32(0, 1), 8), "packed_b_with_d": (_k32(1, 1), 8),
+           "edge": (_k32(0, 0, 1), 12), "edge_with_d": (_k32(1, 0, 1), 12)}
 
 
 @pytest.fixture(scope="module")
@@ -82,14 +88,17 @@ def test_k_loop_waits_are_the_kernels_own(asm, kind):
 # itself: s_nop 7 pairs between the accumulators' zeroing (v_accvgpr_write)
 # and the next MFMA, and three s_nop 7 between the last MFMA of a tile and
 # the epilogue's reads of the AGPRs.
-def _k16(has_d, packed):
-    return "_ZN12_GLOBAL__N_117gemm_dma16_kernelILb%dELb%dEEEvNS_8GemmArgsE" % (has_d, packed)
+def _k16(has_d, packed, edge=0):
+    return "_ZN12_GLOBAL__N_117gemm_dma16_kernelILb%dELb%dELb%dEEEvNS_8GemmArgsE" % (
+        has_d, packed, edge)
 
 
-# gemm_dma16_kernel<HAS_D, PACKED_B>
+# gemm_dma16_kernel<HAS_D, PACKED_B, EDGE>
 KERNELS16 = {"no_d": _k16(0, 0), "with_d": _k16(1, 0), "packed_b": _k16(0, 1),
-             "packed_b_with_d": _k16(1, 1)}
-WITH_D16 = {"with_d", "packed_b_with_d"}
+             "packed_b_with_d": _k16(1, 1), "edge": _k16(0, 0, 1), "edge_with_d": _k16(1, 0, 1)}
+# kinds whose tile's last k iteration is peeled to store early strips: no D,
+# and all tiles whole (the edge kinds mask their stores after the loop)
+EARLY16 = {"no_d", "packed_b"}
 
 
 def instructions(asm, name):
@@ -108,9 +117,9 @@ def test_dma16_m0_is_only_written_by_the_dma_sequences(asm, kind):
             assert body[i + 2].startswith("global_load_lds_dwordx4"), body[i + 2]
             dmas += 1
     # prologue (3 slices) and the k loop unrolled over the 4 stages, 8 DMAs
-    # per wave per slice; without D the tile's last iteration is a second,
-    # peeled copy of the loop body
-    assert dmas == (3 + 4 + (0 if kind in WITH_D16 else 4)) * 8
+    # per wave per slice; with early strips the tile's last iteration is a
+    # second, peeled copy of the loop body
+    assert dmas == (3 + 4 + (4 if kind in EARLY16 else 0)) * 8
     assert sum(l.startswith("global_load_lds_dwordx4") for l in body) == dmas
 
 
@@ -121,14 +130,14 @@ def test_dma16_slice_barriers_and_no_full_waits_in_the_k_loop(asm, kind):
     # 4 unrolled steps of 8 x 8 MFMAs accumulating in place (and without D
     # the peeled last iteration's 4)
     loop_mfma = [i for i in mfma if re.match(r"v_mfma_i32_16x16x64_i8 (a\[\d+:\d+\]), v.*, \1$", body[i])]
-    steps = 4 if kind in WITH_D16 else 8
+    steps = 8 if kind in EARLY16 else 4
     assert len(loop_mfma) == len(mfma) == steps * 64
     loop = body[loop_mfma[0]:loop_mfma[-1] + 1]
     assert not [l for l in loop if re.match(r"s_waitcnt .*vmcnt\(0\)", l)]
     # every slice barrier waits for all but the slice's own 8 DMAs; the
     # tile's last step also leaves the 6 early strips' 8 stores each
     waits = [body[i - 1] for i in range(loop_mfma[0], loop_mfma[-1] + 8) if body[i] == "s_barrier"]
-    want = ["s_waitcnt vmcnt(8)"] * 4 if kind in WITH_D16 else ["s_waitcnt vmcnt(8)"] * 7 + ["s_waitcnt vmcnt(56)"]
+    want = ["s_waitcnt vmcnt(8)"] * 7 + ["s_waitcnt vmcnt(56)"] if kind in EARLY16 else ["s_waitcnt vmcnt(8)"] * 4
     assert sorted(waits) == sorted(want), waits
 
 

@@ -4,14 +4,13 @@ the C ABI.
 
 One launch takes them when M, N >= 256 and K is whole 64-deep slices: the
 last tile row (column) starts at M - 256 (N - 256), so its loads stay inside
-A and B, and it stores its neighbour's overlapping rows (columns) again with
-the same values. C = C + A.B in place cannot do that (the neighbour may
-already have added D), so there, and when the partial tile row would add a
-round of tiles, the whole 256-row tiles run first and the remaining rows on
-128x128 tiles. Cases cover both kernels (K % 256 == 0 on 16x16x64, other
-multiples of 64 on 32x32x32), D out of place and in place, batches, the
-split with a K-split remainder, and that nothing outside C's M x N block is
-written.
+A and B, and it leaves the rows (columns) it shares with its neighbour to the
+neighbour's stores, so every element is written once, in place as well. When
+the partial tile row would add a round of tiles, the whole 256-row tiles run
+first and the remaining rows on 128x128 tiles. Cases cover both kernels
+(K % 256 == 0 on 16x16x64, other multiples of 64 on 32x32x32), D out of
+place and in place, batches, the split with a K-split remainder, and that
+nothing outside C's M x N block is written.
 """
 import numpy as np
 import pytest
@@ -94,9 +93,8 @@ def test_last_tiles_moved_back(dev, m, n, k, with_d):
 
 @pytest.mark.parametrize("m,n,k", [(300, 512, 256), (520, 784, 2304), (700, 1040, 320)])
 def test_in_place_on_ragged_tiles(dev, m, n, k):
-    """C = C + A.B: M ragged with whole N splits into the persistent kernel's
-    whole tiles and 128x128 tiles for the rest; N ragged runs on the edge
-    kernel. Either way no element adds D twice."""
+    """C = C + A.B on moved-back tiles: the rows and columns a last tile
+    shares with its neighbour are stored once, so no element adds D twice."""
     n = n // 16 * 16
     say("edge tiles in place", m, n, k)
     A, B, D = operands(m, n, k, m + n + k + 1)

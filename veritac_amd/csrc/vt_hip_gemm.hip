@@ -12,9 +12,8 @@
 //   gemm_dma16_kernel  256x256 tiles with M, N >= 256, K % 256 == 0 and
 //       16-byte C (and D) rows, with or without D, row-major or packed B (the
 //       8192^3 case and config 3). When M or N is not whole tiles, the last
-//       tile row or column starts at M - 256 or N - 256 and stores its
-//       neighbour's overlapping values again, unchanged (not for C = C + A.B
-//       in place: its whole tiles run here, the other rows on 128x128 tiles).
+//       tile row or column starts at M - 256 or N - 256 and leaves the rows
+//       and columns it shares with its neighbour to the neighbour's stores.
 //       Persistent: one workgroup
 //       per CU walks its tiles in XCD-contiguous order; k slices go global ->
 //       LDS by direct-to-LDS DMA (global_load_lds_dwordx4) into four stages,
@@ -159,10 +158,15 @@ __device__ __forceinline__ int a_off(int row, int c) {
 // would make every element wait one full memory round trip (this took an
 // 8192^3 GEMM with D from ~480 to ~870 us). Each element's D is still read
 // before its own C is written, and no other lane writes that element.
-template <int MI, int NI, bool EDGE, bool HAS_D>
+//
+// LOWER: the tile may have been moved back to end at M or N (persistent
+// kernels); rows below row_min and columns below col_min belong to the
+// neighbouring tile, which stores them, so they are not stored here.
+template <int MI, int NI, bool EDGE, bool HAS_D, bool LOWER = false>
 __device__ __forceinline__ void store_tile(const v16i (&acc)[MI][NI], int32_t *Cb,
                                            const int32_t *Db, int64_t ldc, int64_t ldd,
-                                           int row0, int col0, int M, int N, int lane) {
+                                           int row0, int col0, int M, int N, int lane,
+                                           int row_min = 0, int col_min = 0) {
 #pragma unroll
   for (int mi = 0; mi < MI; ++mi) {
     int32_t d[HAS_D ? NI : 1][16];
@@ -183,7 +187,7 @@ __device__ __forceinline__ void store_tile(const v16i (&acc)[MI][NI], int32_t *C
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int row = row0 + mi * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
-        if (!EDGE || (row < M && col < N)) {
+        if ((!EDGE || (row < M && col < N)) && (!LOWER || (row >= row_min && col >= col_min))) {
           int32_t v = acc[mi][ni][e];
           if constexpr (HAS_D) v = add_wrap(v, d[ni][e]);
           __builtin_nontemporal_store(v, Cb + (int64_t)row * ldc + col);
@@ -546,7 +550,7 @@ __device__ __forceinline__ void dma_b128(const int8_t *base, uint32_t voff, uint
 // Same contract as gemm_mfma_kernel<256, 256, EDGE, HAS_D, false> for
 // M, N >= 256 and K % 64 == 0 (a last tile row or column that would pass M or
 // N starts at M - 256 or N - 256 instead, so no load or store leaves A, B, C
-// or D; C = C + A.B in place needs whole tiles), but the k slices go global -> LDS
+// or D), but the k slices go global -> LDS
 // by DMA (no VGPR staging, no ds_write instructions) and the kernel is
 // persistent: one workgroup per CU walks its tiles in order and the slice
 // stream runs on across tile boundaries, so the last steps of a tile already
@@ -574,7 +578,10 @@ __device__ __forceinline__ void dma_b128(const int8_t *base, uint32_t voff, uint
 // (column l % 32, k 16 * (l / 32) .. +15 of the 32-deep step, the same k as
 // its A operand) is one ds_read_b128: two fragment reads per B block fewer
 // than the transposing ds_read_b64_tr_b8 pair that row-major B needs.
-template <int WAVES, bool HAS_D, bool PACKED_B = false>
+// EDGE: M or N is not a whole number of tiles; a last tile row or column
+// starts at M - 256 or N - 256, and the rows and columns it shares with its
+// neighbour are left to the neighbour's stores.
+template <int WAVES, bool HAS_D, bool PACKED_B = false, bool EDGE = false>
 __global__ __launch_bounds__(64 * WAVES, 1) void gemm_dma_kernel(GemmArgs p) {
   static_assert(WAVES == 4 || WAVES == 8, "4 or 8 waves");
   constexpr int BM = 256, BN = 256, BK = 64;
@@ -604,8 +611,9 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_dma_kernel(GemmArgs p) {
   if (wl >= total_tiles) return;
   const int ntiles = (total_tiles - 1 - wl) / G + 1;
   const int group = p.group_m * p.tiles_n;
-  // Tile iteration -> (batch, row origin, column origin).
-  auto tile_coords = [&](int it, int &bidx, int &m0, int &n0) {
+  // Tile iteration -> (batch, row origin, column origin, and the origins
+  // before a last tile row or column is moved back).
+  auto tile_coords = [&](int it, int &bidx, int &m0, int &n0, int &mn, int &nn) {
     const int lt = wl + it * G;
     bidx = lt / per_batch;
     const int t = lt - bidx * per_batch;
@@ -614,10 +622,12 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_dma_kernel(GemmArgs p) {
     const int gm = min(p.tiles_m - first_m, p.group_m);
     const int within = t - gid * group;
     // A last tile row or column past M or N is moved back to end at M or N
-    // (the launch ensures M, N >= 256): it recomputes rows or columns of its
-    // neighbour and stores the same values there.
-    m0 = min((first_m + within % gm) * BM, p.M - BM);
-    n0 = min((within / gm) * BN, p.N - BN);
+    // (the launch ensures M, N >= 256). It recomputes rows or columns of its
+    // neighbour and does not store them (store_tile's lower bounds).
+    mn = (first_m + within % gm) * BM;
+    nn = (within / gm) * BN;
+    m0 = min(mn, p.M - BM);
+    n0 = min(nn, p.N - BN);
   };
 
   const int64_t lda = p.lda, ldb = p.ldb;
@@ -651,8 +661,8 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_dma_kernel(GemmArgs p) {
   int d_it = 0, d_kt = 0;
   const int8_t *a_tile = nullptr, *b_tile = nullptr;
   auto set_tile = [&](int it) {
-    int bidx, m0, n0;
-    tile_coords(it, bidx, m0, n0);
+    int bidx, m0, n0, mn, nn;
+    tile_coords(it, bidx, m0, n0, mn, nn);
     a_tile = p.A + bidx * p.sa + (int64_t)m0 * lda;
     b_tile = p.B + bidx * p.sb + (PACKED_B ? (int64_t)(n0 / 16) * ldb * 1024 : (int64_t)n0);
   };
@@ -787,10 +797,11 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_dma_kernel(GemmArgs p) {
       // barrier step gs+1 may refill stage s0.
       asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(%1)\n\ts_barrier" :: "n"(DMAS), "n"(NUNIT) : "memory");
     }
-    int bidx, m0, n0;
-    tile_coords(it, bidx, m0, n0);
-    store_tile<MI, NI, false, HAS_D>(acc, p.C + bidx * p.sc, HAS_D ? p.D + bidx * p.sd : nullptr,
-                                     p.ldc, p.ldd, m0 + wm * WTM, n0 + wn * WTN, p.M, p.N, lane);
+    int bidx, m0, n0, mn, nn;
+    tile_coords(it, bidx, m0, n0, mn, nn);
+    store_tile<MI, NI, false, HAS_D, EDGE>(acc, p.C + bidx * p.sc,
+                                           HAS_D ? p.D + bidx * p.sd : nullptr, p.ldc, p.ldd,
+                                           m0 + wm * WTM, n0 + wn * WTN, p.M, p.N, lane, mn, nn);
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
@@ -879,11 +890,14 @@ __device__ __forceinline__ StripLanes strip_lanes(int lane, int strip_base, int6
 }
 
 // One 16-row strip of store_tile16_lds: Cs / Ds point at the strip's first
-// row and the wave's first column.
-template <int NI, bool HAS_D>
+// row and the wave's first column. MASKED: store j of a lane writes only when
+// row_rel + 2 j >= 0 and col_ok (a moved-back tile leaves the rows and
+// columns it shares with its neighbour to the neighbour).
+template <int NI, bool HAS_D, bool MASKED = false>
 __device__ __forceinline__ void store_strip16_lds(const v4i (&acc)[NI], int32_t *Cs,
                                                   const int32_t *Ds, int64_t ldc, int64_t ldd,
-                                                  const StripLanes &sl, LDS_AS int8_t *lds) {
+                                                  const StripLanes &sl, LDS_AS int8_t *lds,
+                                                  int row_rel = 0, bool col_ok = true) {
   static_assert(NI * 16 == 128, "two 512-byte rows per wave instruction");
 #pragma unroll
   for (int ni = 0; ni < NI; ++ni)
@@ -902,20 +916,33 @@ __device__ __forceinline__ void store_strip16_lds(const v4i (&acc)[NI], int32_t 
     for (int j = 0; j < 8; ++j)
 #pragma unroll
       for (int q = 0; q < 4; ++q) v[j][q] = add_wrap(v[j][q], d[j][q]);
+    // Masked: the sums are formed before the conditional stores. Sunk into
+    // them, a masked lane's D load would stay outstanding into the next
+    // tile, where the compiler waits for all vector memory (vmcnt(0))
+    // before reusing its register in the k loop.
+    if constexpr (MASKED) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) asm volatile("" : "+v"(v[j]));
+    }
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j)
-    __builtin_nontemporal_store(v[j], (v4i *)((int8_t *)(Cs + 2 * j * ldc) + sl.gofs_c));
+    if (!MASKED || (col_ok && row_rel + 2 * j >= 0))
+      __builtin_nontemporal_store(v[j], (v4i *)((int8_t *)(Cs + 2 * j * ldc) + sl.gofs_c));
 }
 
-template <int MI, int NI, bool HAS_D, int FIRST = 0>
+// row_rel0: the lane's row in the wave's first strip (2 j + lane / 32 for
+// store j) less the rows the tile leaves to its neighbour (MASKED).
+template <int MI, int NI, bool HAS_D, int FIRST = 0, bool MASKED = false>
 __device__ __forceinline__ void store_tile16_lds(const v4i (&acc)[MI][NI], int32_t *Cb,
                                                  const int32_t *Db, int64_t ldc, int64_t ldd,
-                                                 const StripLanes &sl, LDS_AS int8_t *lds) {
+                                                 const StripLanes &sl, LDS_AS int8_t *lds,
+                                                 int row_rel0 = 0, bool col_ok = true) {
 #pragma unroll
   for (int mi = FIRST; mi < MI; ++mi) {
-    store_strip16_lds<NI, HAS_D>(acc[mi], Cb + mi * 16 * ldc, HAS_D ? Db + mi * 16 * ldd : nullptr,
-                                 ldc, ldd, sl, lds);
+    store_strip16_lds<NI, HAS_D, MASKED>(acc[mi], Cb + mi * 16 * ldc,
+                                         HAS_D ? Db + mi * 16 * ldd : nullptr, ldc, ldd, sl, lds,
+                                         row_rel0 + mi * 16, col_ok);
     __builtin_amdgcn_sched_barrier(0);
   }
 }
@@ -931,9 +958,10 @@ __device__ __forceinline__ void mfma16_in_place(v4i &acc, const v4i &a, const v4
   asm volatile("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
 }
 
-// Same contract and structure as gemm_dma_kernel<4, HAS_D, PACKED_B> (full
-// 256x256 tiles, persistent, k slices by DMA into 4 LDS stages, 3 slices
-// ahead, one barrier per slice), with each wave's 128x128 block held as 8 x 8
+// Same contract and structure as gemm_dma_kernel<4, HAS_D, PACKED_B, EDGE>
+// (256x256 tiles, the last ones moved back to end at M and N when EDGE,
+// persistent, k slices by DMA into 4 LDS stages, 3 slices ahead, one barrier
+// per slice), with each wave's 128x128 block held as 8 x 8
 // v_mfma_i32_16x16x64_i8 accumulators instead of 4 x 4 of 32x32x32. The
 // 16x16x64 form does the same work per slice from the same 16 KB of fragment
 // reads per wave, and on config-5 data its register-only loop sustains about
@@ -949,7 +977,7 @@ __device__ __forceinline__ void mfma16_in_place(v4i &acc, const v4i &a, const v4
 // slice gs + 2, whose fragments step gs + 1 reads. Stage gs % 4 is refilled in
 // step gs + 1; its reads were issued in step gs - 1 and consumed by step gs's
 // MFMAs.
-template <bool HAS_D, bool PACKED_B>
+template <bool HAS_D, bool PACKED_B, bool EDGE = false>
 __global__ __launch_bounds__(256, 1) void gemm_dma16_kernel(GemmArgs p) {
   constexpr int BM = 256, BN = 256, BK = 64;
   constexpr int WTM = 128, WTN = 128, MI = WTM / 16, NI = WTN / 16;
@@ -979,7 +1007,7 @@ __global__ __launch_bounds__(256, 1) void gemm_dma16_kernel(GemmArgs p) {
   if (wl >= total_tiles) return;
   const int ntiles = (total_tiles - 1 - wl) / G + 1;
   const int group = p.group_m * p.tiles_n;
-  auto tile_coords = [&](int it, int &bidx, int &m0, int &n0) {
+  auto tile_coords = [&](int it, int &bidx, int &m0, int &n0, int &mn, int &nn) {
     const int lt = wl + it * G;
     bidx = lt / per_batch;
     const int t = lt - bidx * per_batch;
@@ -987,8 +1015,10 @@ __global__ __launch_bounds__(256, 1) void gemm_dma16_kernel(GemmArgs p) {
     const int first_m = gid * p.group_m;
     const int gm = min(p.tiles_m - first_m, p.group_m);
     const int within = t - gid * group;
-    m0 = min((first_m + within % gm) * BM, p.M - BM);   // last tiles end at M, N
-    n0 = min((within / gm) * BN, p.N - BN);
+    mn = (first_m + within % gm) * BM;   // last tiles end at M, N
+    nn = (within / gm) * BN;
+    m0 = min(mn, p.M - BM);
+    n0 = min(nn, p.N - BN);
   };
 
   const int64_t lda = p.lda, ldb = p.ldb;
@@ -1017,8 +1047,8 @@ __global__ __launch_bounds__(256, 1) void gemm_dma16_kernel(GemmArgs p) {
   const int8_t *a_next = nullptr, *b_next = nullptr;
   const int64_t b_step = PACKED_B ? 1024 : (int64_t)BK * ldb;
   auto set_tile = [&](int it) {
-    int bidx, m0, n0;
-    tile_coords(it, bidx, m0, n0);
+    int bidx, m0, n0, mn, nn;
+    tile_coords(it, bidx, m0, n0, mn, nn);
     a_next = p.A + bidx * p.sa + (int64_t)m0 * lda;
     b_next = p.B + bidx * p.sb + (PACKED_B ? (int64_t)(n0 / 16) * ldb * 1024 : (int64_t)n0);
   };
@@ -1158,7 +1188,9 @@ __global__ __launch_bounds__(256, 1) void gemm_dma16_kernel(GemmArgs p) {
     asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" :: "n"(DMAS + (EARLY ? 8 * EARLY_STRIPS : 0)) : "memory");
   };
   using Plain = std::integral_constant<bool, false>;
-  using Early = std::integral_constant<bool, !HAS_D>;
+  // EDGE (moved-back tiles, masked stores): no early strips, so no store
+  // branch enters the scheduled step.
+  using Early = std::integral_constant<bool, !HAS_D && !EDGE>;
 
   issue_slice(0);
   issue_slice(1);
@@ -1177,21 +1209,21 @@ __global__ __launch_bounds__(256, 1) void gemm_dma16_kernel(GemmArgs p) {
     // KT is a multiple of 4 (the host requires K % 256 == 0), so every tile
     // starts at stage 0 with register set 0, and stages and sets rotate
     // statically.
-    int bidx, m0, n0;
-    tile_coords(it, bidx, m0, n0);
+    int bidx, m0, n0, mn, nn;
+    tile_coords(it, bidx, m0, n0, mn, nn);
     c_tile = p.C + bidx * p.sc + (int64_t)(m0 + wm * WTM) * p.ldc + n0 + wn * WTN;
     // Without D the tile's last iteration is peeled: its last step stores
     // the first EARLY_STRIPS strips of C (straight-line code: a branch over
     // steps that write the accumulators makes the register allocator
     // shuffle them).
-    const int KL = HAS_D ? KT : KT - 4;
+    const int KL = HAS_D || EDGE ? KT : KT - 4;
     for (int kt = 0; kt < KL; kt += 4, gs += 4) {
       step(Plain(), 0, fb0, fb1);
       step(Plain(), 1, fb1, fb0);
       step(Plain(), 2, fb0, fb1);
       step(Plain(), 3, fb1, fb0);
     }
-    if constexpr (!HAS_D) {
+    if constexpr (!HAS_D && !EDGE) {
       step(Plain(), 0, fb0, fb1);
       step(Plain(), 1, fb1, fb0);
       step(Plain(), 2, fb0, fb1);
@@ -1201,10 +1233,13 @@ __global__ __launch_bounds__(256, 1) void gemm_dma16_kernel(GemmArgs p) {
     // The last MFMAs' result latency before the epilogue reads any AGPR.
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
     fence_acc();
-    store_tile16_lds<MI, NI, HAS_D, HAS_D ? 0 : EARLY_STRIPS>(
+    // Rows [m0, mn) and columns [n0, nn) of a moved-back tile are its
+    // neighbour's to store (0 unless EDGE).
+    store_tile16_lds<MI, NI, HAS_D, HAS_D || EDGE ? 0 : EARLY_STRIPS, EDGE>(
         acc, c_tile,
         HAS_D ? p.D + bidx * p.sd + (int64_t)(m0 + wm * WTM) * p.ldd + n0 + wn * WTN : nullptr,
-        p.ldc, p.ldd, sl, lds);
+        p.ldc, p.ldd, sl, lds, wm * WTM + (lane >> 5) - (mn - m0),
+        wn * WTN + (lane & 31) * 4 >= nn - n0);
     zero_acc();
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -2160,30 +2195,26 @@ int mfma_k_split(const Problem &r) {
   return ks;
 }
 
-bool same_buffer(const int32_t *D, const int32_t *C) { return D && (const void *)D == (const void *)C; }
-
 // Whether the persistent 256x256 kernels take a row-major problem: K in whole
 // 64-deep slices and M, N at least one tile (N is a multiple of 16 on every
 // vector path). A last tile row or column past M or N is moved back to end
-// there and stores its neighbour's rows or columns again with the same
-// values, which is exact unless C is D itself: then the neighbour may already
-// have added D, so ragged in-place problems stay off this path.
+// there; the rows and columns it shares with its neighbour are stored by the
+// neighbour alone (their EDGE instantiations), so every element of C is
+// written once and in-place C = C + A.B adds D once.
 bool persistent_fits(const Problem &r) {
-  const bool whole = r.M % 256 == 0 && r.N % 256 == 0;
-  return r.K > 0 && r.K % 64 == 0 && r.M >= 256 && r.N >= 256 &&
-         (whole || !same_buffer(r.D, r.C));
+  return r.K > 0 && r.K % 64 == 0 && r.M >= 256 && r.N >= 256;
 }
 
 // Rows of a row-major 256x256 problem (after the fold) that run on the
 // persistent kernel before the rest run on 128x128 tiles: the whole 256-row
-// tiles, when N is whole tiles and either C is D itself or the last, partial
-// tile row would add a round of tiles on a 256-CU chip (M = 1100, N = 14336,
-// K = 4096: 224 + 56 tiles; 114 us as 280 tiles, 78 us split). 0: one launch.
+// tiles, when N is whole tiles and the last, partial tile row would add a
+// round of tiles on a 256-CU chip (M = 1100, N = 14336, K = 4096: 224 + 56
+// tiles; 114 us as 280 tiles, 78 us split). 0: one launch.
 int64_t mfma_split_rows(const Problem &r) {
   if (r.M < 256 || r.M % 256 == 0 || r.N % 256 || r.K == 0 || r.K % 64) return 0;
   const int64_t row_tiles = r.N / 256 * r.batch, full = r.M / 256 * row_tiles;
   const bool more_rounds = (full + row_tiles + kSplitCus - 1) / kSplitCus > (full + kSplitCus - 1) / kSplitCus;
-  return same_buffer(r.D, r.C) || more_rounds ? r.M / 256 * 256 : 0;
+  return more_rounds ? r.M / 256 * 256 : 0;
 }
 
 // Rows [r0, M) of a problem, in every batch.
@@ -2286,11 +2317,21 @@ int launch_mfma_tiles(const Problem &r, hipStream_t stream, int num_cus) {
     // Persistent: one workgroup per CU (the kernel's LDS allows no more).
     const int64_t g = blocks < num_cus ? blocks : num_cus;
     dim3 pgrid((unsigned)g);
+    const bool edge = r.M % BM || r.N % BN;
     if (use_dma16(r)) {
-      if (has_d) hipLaunchKernelGGL((gemm_dma16_kernel<true, false>), pgrid, dim3(256), 0, stream, a);
+      if (edge && has_d) hipLaunchKernelGGL((gemm_dma16_kernel<true, false, true>), pgrid, dim3(256), 0, stream, a);
+      else if (edge) hipLaunchKernelGGL((gemm_dma16_kernel<false, false, true>), pgrid, dim3(256), 0, stream, a);
+      else if (has_d) hipLaunchKernelGGL((gemm_dma16_kernel<true, false>), pgrid, dim3(256), 0, stream, a);
       else hipLaunchKernelGGL((gemm_dma16_kernel<false, false>), pgrid, dim3(256), 0, stream, a);
-    } else if (has_d) hipLaunchKernelGGL((gemm_dma_kernel<kDmaWaves, true>), pgrid, dim3(64 * kDmaWaves), 0, stream, a);
-    else hipLaunchKernelGGL((gemm_dma_kernel<kDmaWaves, false>), pgrid, dim3(64 * kDmaWaves), 0, stream, a);
+    } else if (edge && has_d) {
+      hipLaunchKernelGGL((gemm_dma_kernel<kDmaWaves, true, false, true>), pgrid, dim3(64 * kDmaWaves), 0, stream, a);
+    } else if (edge) {
+      hipLaunchKernelGGL((gemm_dma_kernel<kDmaWaves, false, false, true>), pgrid, dim3(64 * kDmaWaves), 0, stream, a);
+    } else if (has_d) {
+      hipLaunchKernelGGL((gemm_dma_kernel<kDmaWaves, true>), pgrid, dim3(64 * kDmaWaves), 0, stream, a);
+    } else {
+      hipLaunchKernelGGL((gemm_dma_kernel<kDmaWaves, false>), pgrid, dim3(64 * kDmaWaves), 0, stream, a);
+    }
     VT_HIP_CHECK(hipGetLastError());
     return VT_OK;
   }

@@ -196,8 +196,7 @@ def mfma_split_rows(plan):
     run on 128x128 tiles (mfma_split_rows in the HIP source): the whole
     256-row tiles, when n is whole tiles and the last, partial tile row would
     add a round of tiles on 256 CUs. 0: one launch, whose last tile row, when
-    partial, is moved back to end at m. (C = C + A.B in place also splits; a
-    plan does not know its buffers.)"""
+    partial, is moved back to end at m."""
     if plan["variant"] != "mfma_256x256":
         return 0
     m, n, k, b = plan["m"], plan["n"], plan["k"], plan["batch"]
