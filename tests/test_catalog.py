@@ -45,8 +45,8 @@ def test_descriptor_schema_and_paths():
 
 
 def _reference_tree(tmp_path):
-    """A tree laid out as INTEGRATION.md says: the reference-side files copied
-    to specializations/hip_gemm/, and the reference's own files the
+    """A reference tree after the maintainer's install step: the reference-side
+    files copied to specializations/hip_gemm/, and the reference's own files the
     descriptor names present (placeholders here; they are checked against a
     real reference checkout separately when one is present)."""
     desc = json.load(open(os.path.join(SHIM, "specialization.json")))
