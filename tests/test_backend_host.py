@@ -276,3 +276,24 @@ def test_mfma_row_split_mirrors_the_native_choice():
                                       for p in parts))
     # the 128x128 and 256x128 variants never split
     assert hg._mfma_parts(hg.make_plan(1100, 14336, 4096, variant="mfma_128x128")) is None
+
+
+def test_mfma_selection_follows_the_measured_sweep():
+    """The automatic choice among the MFMA tile shapes, on shapes whose three
+    variants were timed on the GPU: the measured fastest (ties within 1 % take
+    either). Moving a threshold of select_variant fails here."""
+    from veritac_amd import _lib
+    fastest = {
+        (1024, 4096, 4096): "mfma_128x128", (1536, 4096, 4096): "mfma_256x128",
+        (1536, 4096, 8192): "mfma_256x128", (2048, 4096, 4096): "mfma_256x128",
+        (2560, 4096, 4096): "mfma_256x256", (3584, 4096, 4096): "mfma_256x256",
+        (2560, 4096, 2048): "mfma_256x256", (768, 14336, 4096): "mfma_256x256",
+        (9000, 1024, 4096): "mfma_256x256", (2048, 4096, 1024): "mfma_128x128",
+        (1536, 8192, 1024): "mfma_128x128", (1024, 14336, 1024): "mfma_256x256",
+        (768, 14336, 512): "mfma_128x128", (9000, 1024, 512): "mfma_128x128",
+        (3584, 4096, 256): "mfma_128x128", (600, 28672, 4096): "mfma_256x256",
+        (8192, 8192, 8192): "mfma_256x256", (8000, 8192, 8192): "mfma_256x256",
+    }
+    for (m, n, k), want in fastest.items():
+        assert _lib.select_variant(m, n, k, 1)[0] == want, (m, n, k)
+        assert hg.make_plan(m, n, k)["variant"] == want, (m, n, k)
