@@ -175,3 +175,27 @@ def test_large_ragged_problem(dev):
     C = Ct.cpu().numpy()
     for rows in (slice(3700, 3800), slice(m - 60, m)):
         assert np.array_equal(C[rows], go.gemm_i8_f64(A[rows], B)), rows
+
+
+def test_split_with_unshared_batches(dev):
+    """16 batches of 300 rows with their own B: 256 whole tiles and 256 partial
+    ones, so every batch's whole 256-row tile runs in one persistent launch
+    and every batch's last 44 rows in one batched launch of 128x128 tiles,
+    out of place and in place."""
+    batch, m, n, k = 16, 300, 4096, 256
+    plan = hg.make_plan(m, n, k, batch=batch, has_d=True, d_max_abs=2**20,
+                        variant="mfma_256x256")
+    top, rest = hg._mfma_parts(plan)
+    assert (top["m"], rest["m"], top["batch"], rest["batch"]) == (256, 44, batch, batch)
+    rng = np.random.default_rng(31)
+    A = rng.integers(-128, 128, (batch, m, k), dtype=np.int8)
+    B = rng.integers(-128, 128, (batch, k, n), dtype=np.int8)
+    D = rng.integers(-2**20, 2**20, (batch, m, n), dtype=np.int32)
+    At, Bt, Dt = to_dev(dev, A), to_dev(dev, B), to_dev(dev, D)
+    say("edge tiles split, unshared batches")
+    C = hg.run(plan, At, Bt, Dt).cpu().numpy()
+    C2 = hg.run(plan, At, Bt, Dt, out=Dt).cpu().numpy()
+    for b in range(batch):
+        want = go.gemm_i8(A[b], B[b], D[b])
+        assert np.array_equal(C[b], want), b
+        assert np.array_equal(C2[b], want), b
