@@ -26,10 +26,11 @@ def _k32(has_d, packed, edge=0):
 
 # (mangled name, fragment reads of one 32-deep k step): 4 A blocks plus the
 # lo/hi halves of 4 row-major B blocks, or 4 whole packed B blocks. The edge
-# kinds (last tiles moved back, masked stores) read row-major B.
+# kinds move last tiles back and mask their stores.
 KERNELS = {"no_d": (_k32(0, 0), 12), "with_d": (_k32(1, 0), 12),
            "packed_b": (_k32(0, 1), 8), "packed_b_with_d": (_k32(1, 1), 8),
-           "edge": (_k32(0, 0, 1), 12), "edge_with_d": (_k32(1, 0, 1), 12)}
+           "edge": (_k32(0, 0, 1), 12), "edge_with_d": (_k32(1, 0, 1), 12),
+           "packed_b_edge": (_k32(0, 1, 1), 8), "packed_b_edge_with_d": (_k32(1, 1, 1), 8)}
 
 
 @pytest.fixture(scope="module")
@@ -95,7 +96,8 @@ def _k16(has_d, packed, edge=0):
 
 # gemm_dma16_kernel<HAS_D, PACKED_B, EDGE>
 KERNELS16 = {"no_d": _k16(0, 0), "with_d": _k16(1, 0), "packed_b": _k16(0, 1),
-             "packed_b_with_d": _k16(1, 1), "edge": _k16(0, 0, 1), "edge_with_d": _k16(1, 0, 1)}
+             "packed_b_with_d": _k16(1, 1), "edge": _k16(0, 0, 1), "edge_with_d": _k16(1, 0, 1),
+             "packed_b_edge": _k16(0, 1, 1), "packed_b_edge_with_d": _k16(1, 1, 1)}
 # kinds whose tile's last k iteration is peeled to store early strips: no D,
 # and all tiles whole (the edge kinds mask their stores after the loop)
 EARLY16 = {"no_d", "packed_b"}

@@ -152,15 +152,16 @@ def test_padded_ldc_without_d(dev, k):
 
 @pytest.mark.parametrize("k", [2304, 4096])
 def test_packed_dma_rows_with_d(dev, k):
-    """Packed B with D on the 256x256 kernel: 4096 x 2048 (128 tiles) plus
-    100 rows on 128x128 tiles, out of place and in place."""
+    """Packed B with D on the 256x256 kernel: 4096 + 100 rows x 2048, the last
+    tile row moved back to end at M (stores masked), out of place and in
+    place."""
     m, n = 4096 + 100, 2048
     rng = np.random.default_rng(k)
     A = rng.integers(-128, 128, (m, k), dtype=np.int8)
     B = rng.integers(-128, 128, (k, n), dtype=np.int8)
     D = rng.integers(-2**30, 2**30, (m, n), dtype=np.int32)
     plan = hg.make_plan(m, n, k, has_d=True, d_max_abs=2**30, variant=hg.PACKED_VARIANT)
-    assert hg.packed_dma_rows(plan) == 4096
+    assert hg.packed_dma_rows(plan) == m
     say("packed dma16 with D", m, n, k)
     At, Bp = to_dev(dev, A), hg.pack_b(to_dev(dev, B))
     Dt = to_dev(dev, D)

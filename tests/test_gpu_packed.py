@@ -372,12 +372,13 @@ def test_packed_tiles_k_split_extremes(dev):
 
 @pytest.mark.parametrize("extra,k", [(0, 192), (44, 192), (100, 192), (0, 256), (100, 512)])
 def test_dma_rows_with_packed_b(dev, extra, k):
-    """4096 rows x 2048 columns: 128 whole 256-row tiles on the DMA kernel
-    (32x32x32 at K = 192, 16x16x64 at K = 256 and 512), then 44 rows in a
-    decode group or 100 rows on 128x128 tiles."""
+    """4096 + extra rows x 2048 columns, all on the DMA kernel (32x32x32 at
+    K = 192, 16x16x64 at K = 256 and 512): 128 whole 256-row tiles, and for
+    44 or 100 extra rows a last tile row moved back to end at M (136 tiles,
+    still one round), its stores masked; in place as well."""
     m, n = 4096 + extra, 2048
     plan = hg.make_plan(m, n, k, variant=hg.PACKED_VARIANT)
-    assert hg.packed_dma_rows(plan) == 4096
+    assert hg.packed_dma_rows(plan) == m
     say("packed dma", m, k, n, hg.native_check(plan)[1])
     rng = np.random.default_rng(300 + extra + k)
     A = rng.integers(-128, 128, (m, k), dtype=np.int8)
@@ -405,15 +406,19 @@ def test_dma_rows_with_packed_b_batches(dev, shared):
         assert np.array_equal(C[b], go.gemm_i8(A[b], Bb, D[b])), b
 
 
-def test_packed_tiles_after_dma_rows_in_batches(dev):
-    """2 batches of 4096 + 100 rows, shared packed B: the DMA kernel takes the
-    whole tiles of both batches, then 100 rows of each batch run on 128x128
-    tiles batch by batch (not folded: those rows are not contiguous)."""
-    rng = np.random.default_rng(61)
-    batch, m, k, n = 2, 4196, 128, 2048
+@pytest.mark.parametrize("extra", [100, 44])
+def test_packed_tiles_after_dma_rows_in_batches(dev, extra):
+    """2 batches of 4096 + extra rows, shared packed B: 256 whole tiles plus
+    16 partial ones would add a round, so the DMA kernel takes the whole
+    tiles of both batches, then each batch's last rows run batch by batch
+    (not folded: those rows are not contiguous), 100 on 128x128 tiles or 44
+    in a decode group."""
+    rng = np.random.default_rng(61 + extra)
+    batch, m, k, n = 2, 4096 + extra, 128, 2048
     A = rng.integers(-128, 128, (batch, m, k), dtype=np.int8)
     B = rng.integers(-128, 128, (k, n), dtype=np.int8)
     plan = hg.make_plan(m, n, k, batch=batch, b_shared=True, variant=hg.PACKED_VARIANT)
+    assert hg.packed_dma_rows(plan) == 4096
     At, Bt = to_dev(dev, A), to_dev(dev, B)
     C = hg.run(plan, At, hg.pack_b(Bt)).cpu().numpy()
     for b in range(batch):

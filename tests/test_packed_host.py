@@ -110,14 +110,17 @@ def test_packed_plans_validate():
 
 
 def test_packed_rows_in_whole_tiles_go_to_the_256_kernel():
-    """Rows in whole 256-row tiles run on the 256x256 kernel when n % 256 == 0,
-    k % 64 == 0 and there are at least 128 such tiles; more than 64 other rows
-    on 128x128 tiles; up to 64 in one group on the decode kernel (the split
-    vt_gemm_i8_packed makes in the library)."""
+    """Rows run on the 256x256 kernel when n % 256 == 0, k % 64 == 0 and there
+    are at least 128 whole 256-row tiles: all of them, the last partial tile
+    row moved back to end at m, unless that row adds a round of tiles on 256
+    CUs; then the whole tiles, and more than 64 other rows on 128x128 tiles,
+    up to 64 in one group on the decode kernel (the split vt_gemm_i8_packed
+    makes in the library)."""
     plan = lambda m, n, k, **kw: hg.make_plan(m, n, k, variant=hg.PACKED_VARIANT, **kw)
     assert hg.PACKED_DMA_MIN_TILES == 128
     assert hg.packed_dma_rows(plan(8192, 8192, 8192)) == 8192
-    assert hg.packed_dma_rows(plan(4096 + 44, 2048, 128)) == 4096     # 16 x 8 = 128 tiles
+    assert hg.packed_dma_rows(plan(4096 + 44, 2048, 128)) == 4140     # 128 + 8 tiles: one round
+    assert hg.packed_dma_rows(plan(4096 + 44, 2048, 128, batch=2)) == 4096   # 256 + 16: two
     assert hg.packed_dma_rows(plan(4096 + 44, 1792, 128)) == 0        # 16 x 7 = 112 tiles
     assert hg.packed_dma_rows(plan(768, 14336, 4096)) == 768          # 3 x 56 tiles
     assert hg.packed_dma_rows(plan(512, 14336, 4096)) == 0            # 2 x 56 tiles
@@ -128,10 +131,13 @@ def test_packed_rows_in_whole_tiles_go_to_the_256_kernel():
     assert hg.packed_dma_rows(plan(256 * 128, 256, 64 * 262143)) == 256 * 128
     assert hg.packed_dma_rows(plan(256 * 128, 256, 64 * 262144)) == 0
     p = plan(4096 + 44, 2048, 128)
-    assert hg.required_resources(p) == (hg.DMA_LDS, 128 + hg.packed_columns(dict(p, m=44))[1])
+    assert hg.required_resources(p) == (hg.DMA_LDS, 136)
+    assert "(4140 rows on the 256x256 kernel)" in hg.native_check(p)[1]
+    p = plan(4096 + 44, 2048, 128, batch=2)
+    assert hg.required_resources(p) == (hg.DMA_LDS, 256 + 2 * hg.packed_columns(dict(p, m=44))[1])
     assert "4096 rows on the 256x256 kernel, 44 in a group of up to 64" in hg.native_check(p)[1]
-    p = plan(4096 + 100, 2048, 128)
-    assert hg.required_resources(p) == (hg.DMA_LDS, 128 + 16)
+    p = plan(4096 + 100, 2048, 128, batch=2)
+    assert hg.required_resources(p) == (hg.DMA_LDS, 256 + 2 * 16)
     assert "4096 rows on the 256x256 kernel, 100 on 128x128 tiles" in hg.native_check(p)[1]
     p = plan(300, 512, 128)
     assert hg.required_resources(p) == (hg.TILES["mfma_128x128"][4], 3 * 4)

@@ -2489,26 +2489,51 @@ bool packed_dma_fits(const Problem &q) {
 // against 63.4 us).
 constexpr int64_t kPackedDmaMinTiles = 128;
 
-// Rows [0, 256 * (M / 256)) of a packed-B GEMM on the persistent 256x256 DMA
-// kernel, every batch in one launch.
-int launch_packed_dma(const Problem &q, hipStream_t stream, int num_cus) {
+// Rows of a packed-B GEMM that run on the persistent 256x256 DMA kernel: all
+// of them when its partial last tile row (moved back to end at M, its stores
+// masked to the rows no other tile writes) adds no round of tiles on a
+// 256-CU chip, else the whole 256-row tiles; 0 when fewer than
+// kPackedDmaMinTiles whole tiles exist.
+int64_t packed_dma_rows(const Problem &q) {
+  if (!packed_dma_fits(q)) return 0;
+  const int64_t row_tiles = q.N / 256 * q.batch, full = q.M / 256 * row_tiles;
+  if (full < kPackedDmaMinTiles) return 0;
+  if (q.M % 256 == 0) return q.M;
+  const bool more_rounds =
+      (full + row_tiles + kSplitCus - 1) / kSplitCus > (full + kSplitCus - 1) / kSplitCus;
+  return more_rounds ? q.M / 256 * 256 : q.M;
+}
+
+// Rows [0, rows) of a packed-B GEMM (rows from packed_dma_rows) on the
+// persistent 256x256 DMA kernel, every batch in one launch.
+int launch_packed_dma(const Problem &q, int64_t rows, hipStream_t stream, int num_cus) {
   GemmArgs a;
   a.A = q.A; a.B = q.B; a.D = q.D; a.C = q.C;
   a.lda = q.lda; a.ldb = packed_kbt(q.K); a.ldd = q.ldd; a.ldc = q.ldc;
   a.sa = q.sa; a.sb = q.sb; a.sd = q.sd; a.sc = q.sc;
-  a.M = (int)(q.M / 256 * 256); a.N = (int)q.N; a.K = (int)q.K;
-  a.tiles_m = a.M / 256;
+  a.M = (int)rows; a.N = (int)q.N; a.K = (int)q.K;
+  a.tiles_m = (a.M + 255) / 256;
   a.tiles_n = a.N / 256;
   a.group_m = 4;
   a.batch_count = (int)q.batch;
   const int64_t blocks = (int64_t)a.tiles_m * a.tiles_n * q.batch;
   if (blocks > 0x7fffffff) return fail(VT_EUNSUPPORTED, "grid of %lld tiles too large", (long long)blocks);
   dim3 pgrid((unsigned)(blocks < num_cus ? blocks : num_cus));
+  const bool edge = rows % 256 != 0;
   if (use_dma16(q)) {
-    if (q.D) hipLaunchKernelGGL((gemm_dma16_kernel<true, true>), pgrid, dim3(256), 0, stream, a);
+    if (edge && q.D) hipLaunchKernelGGL((gemm_dma16_kernel<true, true, true>), pgrid, dim3(256), 0, stream, a);
+    else if (edge) hipLaunchKernelGGL((gemm_dma16_kernel<false, true, true>), pgrid, dim3(256), 0, stream, a);
+    else if (q.D) hipLaunchKernelGGL((gemm_dma16_kernel<true, true>), pgrid, dim3(256), 0, stream, a);
     else hipLaunchKernelGGL((gemm_dma16_kernel<false, true>), pgrid, dim3(256), 0, stream, a);
-  } else if (q.D) hipLaunchKernelGGL((gemm_dma_kernel<kDmaWaves, true, true>), pgrid, dim3(64 * kDmaWaves), 0, stream, a);
-  else hipLaunchKernelGGL((gemm_dma_kernel<kDmaWaves, false, true>), pgrid, dim3(64 * kDmaWaves), 0, stream, a);
+  } else if (edge && q.D) {
+    hipLaunchKernelGGL((gemm_dma_kernel<kDmaWaves, true, true, true>), pgrid, dim3(64 * kDmaWaves), 0, stream, a);
+  } else if (edge) {
+    hipLaunchKernelGGL((gemm_dma_kernel<kDmaWaves, false, true, true>), pgrid, dim3(64 * kDmaWaves), 0, stream, a);
+  } else if (q.D) {
+    hipLaunchKernelGGL((gemm_dma_kernel<kDmaWaves, true, true>), pgrid, dim3(64 * kDmaWaves), 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((gemm_dma_kernel<kDmaWaves, false, true>), pgrid, dim3(64 * kDmaWaves), 0, stream, a);
+  }
   VT_HIP_CHECK(hipGetLastError());
   return VT_OK;
 }
@@ -3264,15 +3289,16 @@ int vt_gemm_i8_packed(const int8_t *A, const int8_t *Bp, const int32_t *D, int32
   scr.st = st;
   scr.stream = stream;
   if (K == 0) return launch_generic(q, (hipStream_t)stream);   // C = D (or 0)
-  // Whole 256-row tiles on the persistent DMA kernel when there are enough of
-  // them; more than 64 remaining rows on 128x128 tiles; up to 64 rows, or
-  // tiles whose offsets do not fit 32 bits, in groups of up to 64 rows on the
+  // Rows on the persistent DMA kernel when there are enough whole 256-row
+  // tiles (all rows, unless the partial last tile row would add a round);
+  // more than 64 remaining rows on 128x128 tiles; up to 64 rows, or tiles
+  // whose offsets do not fit 32 bits, in groups of up to 64 rows on the
   // decode kernel, each group streaming B once.
   int64_t r_first = 0;
-  if (packed_dma_fits(q) && M / 256 * (N / 256) * batch >= kPackedDmaMinTiles) {
-    rc = launch_packed_dma(q, (hipStream_t)stream, st->num_cus);
+  if (const int64_t rows = packed_dma_rows(q)) {
+    rc = launch_packed_dma(q, rows, (hipStream_t)stream, st->num_cus);
     if (rc) return rc;
-    r_first = M / 256 * 256;
+    r_first = rows;
   }
   if (M - r_first > kSkinnyMaxM && packed_tiles_fit(q)) {
     Problem g = q;

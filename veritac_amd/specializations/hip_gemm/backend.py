@@ -226,19 +226,26 @@ PACKED_DMA_MIN_TILES = 128   # kPackedDmaMinTiles in the HIP source
 
 
 def packed_dma_rows(plan):
-    """Rows of a skinny_packed plan that run on the 256x256 MFMA kernel: the
-    whole 256-row tiles, when n % 256 == 0, k % 64 == 0, there are at least
-    PACKED_DMA_MIN_TILES of them over all batches, and every lane offset from
-    a tile's base fits 32 bits (contiguous A: 256 * k; packed B: 16 column
-    blocks of kbt 1 KiB tiles). Mirrors packed_dma_fits and vt_gemm_i8_packed
-    in csrc/vt_hip_gemm.hip."""
+    """Rows of a skinny_packed plan that run on the 256x256 MFMA kernel, when
+    n % 256 == 0, k % 64 == 0, there are at least PACKED_DMA_MIN_TILES whole
+    256-row tiles over all batches, and every lane offset from a tile's base
+    fits 32 bits (contiguous A: 256 * k; packed B: 16 column blocks of kbt
+    1 KiB tiles): all m rows (a partial last tile row is moved back to end at
+    m, its stores masked), unless that partial row would add a round of tiles
+    on 256 CUs, then the whole 256-row tiles. Mirrors packed_dma_rows in
+    csrc/vt_hip_gemm.hip."""
     m, n, k, batch = plan["m"], plan["n"], plan["k"], plan["batch"]
     kbt = -(-k // 64)
-    if (m >= 256 and n % 256 == 0 and k % 64 == 0 and k > 0 and 256 * k < 2**32 - 4096
-            and 16 * 1024 * kbt < 2**32 - 4096
-            and m // 256 * (n // 256) * batch >= PACKED_DMA_MIN_TILES):
-        return m // 256 * 256
-    return 0
+    if not (m >= 256 and n % 256 == 0 and k % 64 == 0 and k > 0 and 256 * k < 2**32 - 4096
+            and 16 * 1024 * kbt < 2**32 - 4096):
+        return 0
+    row_tiles = n // 256 * batch
+    full = m // 256 * row_tiles
+    if full < PACKED_DMA_MIN_TILES:
+        return 0
+    if m % 256 == 0 or -(-(full + row_tiles) // NUM_CUS) == -(-full // NUM_CUS):
+        return m
+    return m // 256 * 256
 
 
 def packed_tiles_fit(plan):
