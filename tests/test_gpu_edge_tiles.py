@@ -199,3 +199,27 @@ def test_split_with_unshared_batches(dev):
         want = go.gemm_i8(A[b], B[b], D[b])
         assert np.array_equal(C[b], want), b
         assert np.array_equal(C2[b], want), b
+
+
+@pytest.mark.parametrize("k", [2304, 320])
+def test_padded_pitches_on_moved_back_tiles(dev, k):
+    """A, B, C and D each with a padded pitch (lda = K + 64, ldb = N + 48,
+    ldc = N + 4, ldd = N + 8) and M, N both ragged, on the 16x16x64 kernel
+    (K = 2304) and the 32x32x32 one (K = 320): the DMA lane offsets and the
+    masked stores follow the pitches, and the padding is never written."""
+    m, n = 520, 784
+    lda, ldb, ldc, ldd = k + 64, n + 48, n + 4, n + 8
+    rng = np.random.default_rng(k + 5)
+    Afull = rng.integers(-128, 128, (m, lda), dtype=np.int8)
+    Bfull = rng.integers(-128, 128, (k, ldb), dtype=np.int8)
+    Dfull = rng.integers(-2**20, 2**20, (m, ldd), dtype=np.int32)
+    At, Bt, Dt = to_dev(dev, Afull), to_dev(dev, Bfull), to_dev(dev, Dfull)
+    Cbuf = torch.full((m + 1, ldc), INT32_MIN, dtype=torch.int32, device=dev)
+    say("edge tiles padded pitches", k)
+    _lib.gemm_raw(At.data_ptr(), Bt.data_ptr(), Dt.data_ptr(), Cbuf.data_ptr(), m, n, k,
+                  lda, ldb, ldd, ldc, variant="mfma_256x256")
+    _lib.sync(None)
+    got = Cbuf.cpu().numpy()
+    want = go.gemm_i8(Afull[:, :k], Bfull[:, :n], Dfull[:, :n])
+    assert np.array_equal(got[:m, :n], want)
+    assert (got[:m, n:] == INT32_MIN).all() and (got[m:] == INT32_MIN).all()
