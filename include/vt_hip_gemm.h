@@ -59,8 +59,8 @@ extern "C" {
                                       last tile row or column ends at M or
                                       N (stores masked to the elements no
                                       other tile writes), or, when it saves
-                                      a round of tiles, the rows past whole
-                                      tiles run on 128x128 tiles              */
+                                      a round of tiles, the rows (columns)
+                                      past whole tiles run on 128x128 tiles   */
 #define VT_VARIANT_MFMA_128x128 2  /* 128x128 tile, 4 waves,
                                       v_mfma_i32_32x32x32_i8                  */
 #define VT_VARIANT_SKINNY 3        /* M <= 64 decode shapes: B streamed once,

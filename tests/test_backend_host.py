@@ -297,3 +297,27 @@ def test_mfma_selection_follows_the_measured_sweep():
     for (m, n, k), want in fastest.items():
         assert _lib.select_variant(m, n, k, 1)[0] == want, (m, n, k)
         assert hg.make_plan(m, n, k)["variant"] == want, (m, n, k)
+
+
+def test_mfma_column_split_mirrors_the_native_choice():
+    """The column counterpart: whole 256-column tiles first when M is whole
+    tiles and the partial tile column would add a round; the plan mirror
+    names the same columns, remainder K split and workspace as the library."""
+    from veritac_amd import _lib
+    cases = {(8192, 8208, 8192): (8192, 16, 4), (4096, 4112, 4096): (4096, 16, 8),
+             (4096, 4112, 1024): (4096, 16, 2), (2048, 4112, 1024): None,
+             (8192, 8448, 8192): None, (8200, 8208, 8192): None}
+    for (m, n, k), want in cases.items():
+        plan = hg.make_plan(m, n, k, variant="mfma_256x256")
+        st, _, v, ks, ws = _lib.gemm_check(m, n, k, k, n, n, n, variant="mfma_256x256")
+        assert st == _lib.VT_OK and v == "mfma_256x256", (m, n, k)
+        if want is None:
+            assert hg.mfma_split_cols(plan) == 0, (m, n, k)
+            continue
+        top, rest = hg._mfma_parts(plan)
+        assert (top["n"], rest["n"], hg.mfma_k_split(rest)) == want, (m, n, k)
+        assert top["m"] == rest["m"] == m and rest["variant"] == "mfma_128x128"
+        assert ws == 4 * want[2] * m * want[1], (m, n, k)
+        assert hg.required_resources(plan)[1] == (m // 256) * (want[0] // 256) + \
+            (m // 128) * want[2]
+        assert "%d columns on the persistent 256x256 kernel" % want[0] in hg.native_check(plan)[1]

@@ -223,3 +223,25 @@ def test_padded_pitches_on_moved_back_tiles(dev, k):
     want = go.gemm_i8(Afull[:, :k], Bfull[:, :n], Dfull[:, :n])
     assert np.array_equal(got[:m, :n], want)
     assert (got[:m, n:] == INT32_MIN).all() and (got[m:] == INT32_MIN).all()
+
+
+def test_column_split_when_the_partial_column_adds_a_round(dev):
+    """4096 x 4112 x 1024: 256 whole tiles plus 16 partial ones, so the whole
+    4096 columns run on the persistent kernel and the last 16 on 128x128 tiles
+    with K in 2 slices, out of place and in place."""
+    m, n, k = 4096, 4112, 1024
+    plan = hg.make_plan(m, n, k, has_d=True, d_max_abs=2**20, variant="mfma_256x256")
+    top, rest = hg._mfma_parts(plan)
+    assert (top["n"], rest["n"], hg.mfma_k_split(rest)) == (4096, 16, 2)
+    A, B, D = operands(m, n, k, 17, d_bound=2**20)
+    At, Bt, Dt = to_dev(dev, A), to_dev(dev, B), to_dev(dev, D)
+    say("edge tiles column split")
+    C = hg.run(plan, At, Bt, Dt).cpu().numpy()
+    C128 = hg.run(hg.make_plan(m, n, k, has_d=True, d_max_abs=2**20, variant="mfma_128x128"),
+                  At, Bt, Dt).cpu().numpy()
+    assert np.array_equal(C, C128)
+    C2 = hg.run(plan, At, Bt, Dt, out=Dt).cpu().numpy()
+    assert np.array_equal(C2, C)
+    assert np.array_equal(C[:, 4080:], go.gemm_i8(A, B[:, 4080:], D[:, 4080:]))
+    for rows in (slice(0, 32), slice(m - 32, m)):
+        assert np.array_equal(C[rows], go.gemm_i8(A[rows], B, D[rows])), rows

@@ -2217,6 +2217,27 @@ int64_t mfma_split_rows(const Problem &r) {
   return more_rounds ? r.M / 256 * 256 : 0;
 }
 
+// The same for columns: the whole 256-column tiles first, when M is whole
+// tiles and the last, partial tile column would add a round of tiles
+// (M = 8192, N = 8208: 1024 + 32 tiles). 0: one launch.
+int64_t mfma_split_cols(const Problem &r) {
+  if (r.N < 256 || r.N % 256 == 0 || r.M % 256 || r.K == 0 || r.K % 64) return 0;
+  const int64_t col_tiles = r.M / 256 * r.batch, full = r.N / 256 * col_tiles;
+  const bool more_rounds = (full + col_tiles + kSplitCus - 1) / kSplitCus > (full + kSplitCus - 1) / kSplitCus;
+  return more_rounds ? r.N / 256 * 256 : 0;
+}
+
+// Columns [c0, N) of a problem, in every batch (c0 a multiple of 256, so B,
+// C and D keep their alignment).
+Problem cols_from(const Problem &r, int64_t c0) {
+  Problem g = r;
+  g.B = r.B + c0;
+  g.C = r.C + c0;
+  g.D = r.D ? r.D + c0 : nullptr;
+  g.N = r.N - c0;
+  return g;
+}
+
 // Rows [r0, M) of a problem, in every batch.
 Problem rows_from(const Problem &r, int64_t r0) {
   Problem g = r;
@@ -2265,6 +2286,12 @@ int launch_mfma(const Problem &q, Scratch &scr) {
       top.M = rows;
       if (int rc = launch_mfma_tiles<BM, BN, PACKED>(top, stream, num_cus)) return rc;
       return launch_mfma<128, 128, false>(rows_from(r, rows), scr);
+    }
+    if (const int64_t cols = ks == 1 ? mfma_split_cols(r) : 0) {
+      Problem left = r;
+      left.N = cols;
+      if (int rc = launch_mfma_tiles<BM, BN, PACKED>(left, stream, num_cus)) return rc;
+      return launch_mfma<128, 128, false>(cols_from(r, cols), scr);
     }
   }
   if (ks == 1) return launch_mfma_tiles<BM, BN, PACKED>(r, stream, num_cus);
@@ -2766,9 +2793,11 @@ int64_t scratch_need(const Problem &q, int32_t variant, int32_t k_split) {
       variant == VT_VARIANT_MFMA_256x128) {
     const int ks = mfma_split_for(q, variant);
     const Problem r = mfma_fold(q);
-    const int64_t rows = variant == VT_VARIANT_MFMA_256x256 && ks == 1 ? mfma_split_rows(r) : 0;
-    if (rows) {   // the rows after the persistent kernel's, on 128x128 tiles
-      const Problem g = mfma_fold(rows_from(r, rows));
+    const bool split = variant == VT_VARIANT_MFMA_256x256 && ks == 1;
+    const int64_t rows = split ? mfma_split_rows(r) : 0;
+    const int64_t cols = split && !rows ? mfma_split_cols(r) : 0;
+    if (rows || cols) {   // the rows or columns after the persistent kernel's, on 128x128 tiles
+      const Problem g = mfma_fold(rows ? rows_from(r, rows) : cols_from(r, cols));
       const int ks2 = mfma_k_split<128, 128>(g);
       return ks2 > 1 ? round256(ks2 * g.M * g.N * 4) : 0;
     }

@@ -209,16 +209,39 @@ def mfma_split_rows(plan):
     return m // 256 * 256 if -(-(full + row_tiles) // NUM_CUS) > -(-full // NUM_CUS) else 0
 
 
+def mfma_split_cols(plan):
+    """The same for columns (mfma_split_cols in the HIP source): the whole
+    256-column tiles of an mfma_256x256 plan run first when m is whole tiles
+    and the last, partial tile column would add a round of tiles on 256 CUs;
+    the other columns then run on 128x128 tiles. 0: no column split."""
+    if plan["variant"] != "mfma_256x256":
+        return 0
+    m, n, k, b = plan["m"], plan["n"], plan["k"], plan["batch"]
+    if plan["b_shared"] and b > 1:
+        m, b = m * b, 1
+    if n < 256 or n % 256 == 0 or m % 256 or k == 0 or k % 64:
+        return 0
+    col_tiles = m // 256 * b
+    full = n // 256 * col_tiles
+    return n // 256 * 256 if -(-(full + col_tiles) // NUM_CUS) > -(-full // NUM_CUS) else 0
+
+
 def _mfma_parts(plan):
-    """(rows on the persistent 256x256 kernel, the rest on 128x128 tiles) as
-    two plans, or None when mfma_split_rows is 0."""
+    """(the whole rows or columns on the persistent 256x256 kernel, the rest
+    on 128x128 tiles) as two plans, or None when neither mfma_split_rows nor
+    mfma_split_cols splits the plan."""
     rows = mfma_split_rows(plan)
-    if not rows:
+    cols = 0 if rows else mfma_split_cols(plan)
+    if not rows and not cols:
         return None
     if plan["b_shared"] and plan["batch"] > 1:
         plan = dict(plan, m=plan["m"] * plan["batch"], batch=1)
-    top = dict(plan, m=rows, k_split=0)
-    rest = dict(plan, m=plan["m"] - rows, variant="mfma_128x128", k_split=0)
+    if rows:
+        top = dict(plan, m=rows, k_split=0)
+        rest = dict(plan, m=plan["m"] - rows, variant="mfma_128x128", k_split=0)
+    else:
+        top = dict(plan, n=cols, k_split=0)
+        rest = dict(plan, n=plan["n"] - cols, variant="mfma_128x128", k_split=0)
     return top, rest
 
 
@@ -289,7 +312,7 @@ def required_resources(plan):
         if parts is not None:   # whole tiles on the persistent kernel, then the rest
             top, rest = parts
             lds_r, wgs_r = required_resources(rest)
-            return max(lds, lds_r), top["m"] // tm * (n // tn) * top["batch"] + wgs_r
+            return max(lds, lds_r), top["m"] // tm * (top["n"] // tn) * top["batch"] + wgs_r
         if plan["b_shared"] and batch > 1:      # stacked-M fold
             m, batch = m * batch, 1
         return lds, -(-m // tm) * -(-n // tn) * batch * mfma_k_split(plan)
@@ -638,9 +661,12 @@ def native_check(plan):
                        % (variant, plan["variant"]))
     how = ""
     parts = _mfma_parts(dict(plan, variant=variant))
-    if parts is not None:
+    if parts is not None and parts[0]["n"] == parts[1]["n"]:
         how = "; %d rows on the persistent 256x256 kernel, %d on 128x128 tiles" % (
             parts[0]["m"], parts[1]["m"])
+    elif parts is not None:
+        how = "; %d columns on the persistent 256x256 kernel, %d on 128x128 tiles" % (
+            parts[0]["n"], parts[1]["n"])
     return True, "accepted by vt_gemm_check: runs %s (k_split %d, %d bytes of workspace%s)" % (
         variant, ks, ws, how)
 
