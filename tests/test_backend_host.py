@@ -228,7 +228,15 @@ def test_mfma_k_split_mirrors_the_native_choice():
         assert hg.mfma_k_split(plan) == want, (m, n, k)
         if variant.startswith("mfma"):
             tm, tn = hg.TILES[variant][:2]
-            assert hg.required_resources(plan)[1] == -(-m // tm) * -(-n // tn) * want
+            tiles = -(-m // tm) * -(-n // tn) * want
+            assert hg.mfma_tiles(plan) == tiles
+            persistent = variant == "mfma_256x256" and m >= 256 and n >= 256 and \
+                (k // want) % 64 == 0
+            # the persistent kernel: one workgroup per CU, 160 KiB (K slice % 256
+            # == 0) or 128 KiB of LDS; the tile kernel: a workgroup per tile
+            assert hg.required_resources(plan) == (
+                (hg.DMA16_LDS if (k // want) % 256 == 0 else hg.DMA_LDS, min(tiles, 256))
+                if persistent else (hg.TILES[variant][4], tiles)), (m, n, k)
             assert ws == (want * m * n * 4 if want > 1 else 0)
     assert hg.mfma_k_split(hg.make_plan(128, 4096, 4096)) == 8
     assert hg.mfma_k_split(hg.make_plan(128, 4096, 1024)) == 2     # slices of 512
@@ -267,8 +275,8 @@ def test_mfma_row_split_mirrors_the_native_choice():
         assert (top["m"], rest["m"], hg.mfma_k_split(rest)) == want, (m, n, k)
         assert rest["variant"] == "mfma_128x128" and top["batch"] == rest["batch"] == 1
         assert ws == (4 * want[2] * want[1] * n if want[2] > 1 else 0), (m, n, k)
-        wgs = top["m"] // 256 * (n // 256) + -(-rest["m"] // 128) * (n // 128) * want[2]
-        assert hg.required_resources(plan)[1] == wgs
+        wgs = min(top["m"] // 256 * (n // 256), 256) + -(-rest["m"] // 128) * (n // 128) * want[2]
+        assert hg.required_resources(plan) == (hg.persistent_lds(k), wgs)
         assert "%d rows on the persistent 256x256 kernel" % top["m"] in hg.native_check(plan)[1]
         # both launches priced, the first at whole tiles only
         t = hg.modeled_objective(plan, hg.modeled_counts(plan))[0]
@@ -318,6 +326,6 @@ def test_mfma_column_split_mirrors_the_native_choice():
         assert (top["n"], rest["n"], hg.mfma_k_split(rest)) == want, (m, n, k)
         assert top["m"] == rest["m"] == m and rest["variant"] == "mfma_128x128"
         assert ws == 4 * want[2] * m * want[1], (m, n, k)
-        assert hg.required_resources(plan)[1] == (m // 256) * (want[0] // 256) + \
-            (m // 128) * want[2]
+        assert hg.required_resources(plan) == (
+            hg.DMA16_LDS, min((m // 256) * (want[0] // 256), 256) + (m // 128) * want[2])
         assert "%d columns on the persistent 256x256 kernel" % want[0] in hg.native_check(plan)[1]

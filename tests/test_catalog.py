@@ -126,6 +126,43 @@ def test_reference_style_candidate_loop_runs_unchanged(tmp_path):
     assert "mfma_256x256" in out["eligible"] and "skinny" not in out["eligible"]
 
 
+# tests/test_specializations.py:16 of the reference with the count the
+# installed tree has (the one-line change INTEGRATION.md ships): five
+# specializations plus hip_gemm.
+COUNT_LINE = ("from specializations.catalog import list_specializations; import sys; "
+              "assert len(list_specializations()) == %d; "
+              "assert not any(n in sys.modules for n in ('torch', 'numpy', 'mlx'))")
+REFERENCE_IDS = ("cpu_gemm", "cuda_attention", "gemmini_gemm", "metal_attention",
+                 "tenstorrent_protocol")
+
+
+def test_the_reference_count_assertion_reads_six_once_installed(tmp_path):
+    """The installed tree holds the reference's five descriptors (its own
+    files when a checkout is here, else minimal ones with the same ids) and
+    hip_gemm; the catalog module is this repo's restatement of the
+    reference's rules. The reference's assertion then holds with 6 and fails
+    with the 5 it states today."""
+    root, _ = _reference_tree(tmp_path)
+    packages = root / "specializations"
+    for name in REFERENCE_IDS:
+        (packages / name).mkdir(exist_ok=True)
+        src = os.path.join(REFERENCE, "specializations", name, "specialization.json")
+        if os.path.isfile(src):
+            shutil.copyfile(src, packages / name / "specialization.json")
+        else:
+            (packages / name / "specialization.json").write_text(
+                json.dumps({"schema_version": 1, "id": name}))
+    (packages / "__init__.py").write_text("")
+    shutil.copyfile(os.path.join(ROOT, "veritac_amd", "specializations", "catalog.py"),
+                    packages / "catalog.py")
+    ids = [d["id"] for d in catalog.list_specializations(packages=str(packages))]
+    assert ids == sorted(REFERENCE_IDS + ("hip_gemm",))
+    proc = _run_in_tree(root, COUNT_LINE % 6, None)
+    assert proc.returncode == 0, proc.stderr
+    proc = _run_in_tree(root, COUNT_LINE % 5, None)
+    assert proc.returncode != 0 and "AssertionError" in proc.stderr
+
+
 def test_reference_side_import_fails_closed_without_the_repo(tmp_path):
     root, _ = _reference_tree(tmp_path)
     (root / "specializations" / "__init__.py").write_text("")

@@ -6,8 +6,8 @@ and compares both outputs bit for bit with vt_gemm_i8 on the same operands
 (outputs poisoned with INT32_MIN first), and with the CPU oracle. The cases
 are the ones that take scratch: the decode kernel's K-split partial sums,
 the padded variant's copies (with an inner K split as well), and the K-split
-partial sums of the rows a 256x256 problem runs on 128x128 tiles after its
-whole tiles.
+partial sums of the rows, or the columns, a 256x256 problem runs on 128x128
+tiles after its whole tiles.
 """
 import numpy as np
 import pytest
@@ -67,6 +67,10 @@ PAIRS = [
     # 128x128 tiles with K in 2 slices
     ("256x256 row split", (2100, 8192, 1024, "mfma_256x256", 0, True),
      (4136, 4096, 1024, "mfma_256x256", 0, False)),
+    # whole 256-column tiles on the persistent kernel, the last 16 columns on
+    # 128x128 tiles with K in 8 (then 2) slices: 2 MiB, then 512 KiB of scratch
+    ("256x256 column split", (4096, 4112, 4096, "mfma_256x256", 0, True),
+     (4096, 4112, 1024, "mfma_256x256", 0, False)),
 ]
 
 

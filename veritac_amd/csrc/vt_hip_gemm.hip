@@ -260,6 +260,7 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma_kernel(GemmArgs p) {
 
   constexpr int NBUF = 3;                     // LDS slice buffers
   __shared__ __attribute__((aligned(16))) int8_t smem[NBUF * (A_BYTES + B_BYTES)];
+  static_assert(sizeof(smem) == 3 * (BM * 64 + 64 * BN), "LDS vt_variant_info reports");
   int8_t *const As0 = smem;                  // A slice buffer b at As0 + b*A_BYTES
   int8_t *const Bs0 = smem + NBUF * A_BYTES; // B slice buffer b at Bs0 + b*B_BYTES
 
@@ -538,6 +539,12 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma_kernel(GemmArgs p) {
 // Full-tile MFMA kernel with direct-to-LDS loads (256 x 256 tiles)
 // ---------------------------------------------------------------------------
 
+// Static LDS per workgroup of the persistent 256x256 kernels (one workgroup
+// per CU): gemm_dma_kernel's 4 slice stages, and gemm_dma16_kernel's 4 stages
+// plus the 8 KB epilogue strip of each of its 4 waves.
+constexpr int kDmaLds = 4 * (256 * 64 + 64 * 256);
+constexpr int kDma16Lds = kDmaLds + 4 * 8192;
+
 // gfx950 LDS DMA: each lane of the wave fetches the 16 global bytes at
 // base + voff and the wave writes them, in lane order, to the 1 KB of LDS
 // starting at m0. The LDS stores are tracked by vmcnt like any global load;
@@ -592,6 +599,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_dma_kernel(GemmArgs p) {
   constexpr int DPW = 16 / WAVES;        // 1 KB DMA blocks of A (and of B) per wave per slice
   constexpr int DMAS = 2 * DPW;          // DMAs per wave per slice
   __shared__ __attribute__((aligned(1024))) int8_t smem[NSTAGE * STAGE];
+  static_assert(sizeof(smem) == kDmaLds, "LDS the host reports for this kernel");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -992,6 +1000,7 @@ __global__ __launch_bounds__(256, 1) void gemm_dma16_kernel(GemmArgs p) {
   constexpr int DMAS = 2 * DPW;
   // The 32 KB past the stages hold each wave's 8 KB epilogue strip.
   __shared__ __attribute__((aligned(1024))) int8_t smem[NSTAGE * (A_BYTES + B_BYTES) + 4 * 8192];
+  static_assert(sizeof(smem) == kDma16Lds, "LDS the host reports for this kernel");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1824,15 +1833,18 @@ struct VariantInfo {
   int tile_m, tile_n, tile_k, threads, lds_bytes;
 };
 
-// lds_bytes of the skinny variants excludes the A slice (16 x (k_chunk+16)),
-// which depends on K and the split.
+// lds_bytes of the MFMA variants is that of their tile kernel
+// (gemm_mfma_kernel, 3 slice buffers); the persistent 256x256 kernels take
+// kDma16Lds or kDmaLds per workgroup, one workgroup per CU. lds_bytes of the
+// skinny variants excludes the A slice (16 x (k_chunk+16)), which depends on
+// K and the split.
 const VariantInfo kVariants[VT_VARIANT_COUNT] = {
     {"auto", 0, 0, 0, 0, 0},
-    {"mfma_256x256", 256, 256, 64, 256, 2 * (256 * 64 + 64 * 256)},
-    {"mfma_128x128", 128, 128, 64, 256, 2 * (128 * 64 + 64 * 128)},
+    {"mfma_256x256", 256, 256, 64, 256, 3 * (256 * 64 + 64 * 256)},
+    {"mfma_128x128", 128, 128, 64, 256, 3 * (128 * 64 + 64 * 128)},
     {"skinny", 16, 256, 64, 1024, 2 * 16 * 1024},
     {"generic", 4, 64, 1, 256, 0},
-    {"mfma_256x128", 256, 128, 64, 256, 2 * (256 * 64 + 64 * 128)},
+    {"mfma_256x128", 256, 128, 64, 256, 3 * (256 * 64 + 64 * 128)},
     {"padded", 16, 16, 16, 256, 0},   // padding granularity; the inner kernel decides the rest
 };
 

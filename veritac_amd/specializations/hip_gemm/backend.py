@@ -53,10 +53,11 @@ SUPPORTED_VARIANTS = ("auto",) + ALL_VARIANTS
 
 # variant -> (tile_m, tile_n, tile_k, threads, lds_bytes); mirrors the native
 # table returned by vt_variant_info (checked by the tests).
+# The MFMA variants' LDS is their tile kernel's: three 64-deep slice buffers.
 TILES = {
-    "mfma_256x256": (256, 256, 64, 256, 2 * (256 * 64 + 64 * 256)),
-    "mfma_256x128": (256, 128, 64, 256, 2 * (256 * 64 + 64 * 128)),
-    "mfma_128x128": (128, 128, 64, 256, 2 * (128 * 64 + 64 * 128)),
+    "mfma_256x256": (256, 256, 64, 256, 3 * (256 * 64 + 64 * 256)),
+    "mfma_256x128": (256, 128, 64, 256, 3 * (256 * 64 + 64 * 128)),
+    "mfma_128x128": (128, 128, 64, 256, 3 * (128 * 64 + 64 * 128)),
     "skinny": (16, 256, 64, 1024, 2 * 16 * 1024),
     "generic": (4, 64, 1, 256, 0),
     # padding granularity: A and B copied with k and n rounded up to 16, the
@@ -67,7 +68,11 @@ TILES = {
     "skinny_packed": (64, 64, 64, 512, 8 * 4 * 1024),
 }
 PACKED_WAVES = 8
-DMA_LDS = 4 * (256 * 64 + 64 * 256)   # LDS of the persistent 256x256 kernel (4 stages)
+# LDS of the persistent 256x256 kernels, one workgroup per CU (kDmaLds and
+# kDma16Lds in the HIP source): 4 slice stages, plus the 16x16x64 kernel's
+# four 8 KiB epilogue strips. The 16x16x64 kernel runs K % 256 == 0.
+DMA_LDS = 4 * (256 * 64 + 64 * 256)
+DMA16_LDS = DMA_LDS + 4 * 8192
 SKINNY_MAX_M = 64   # up to 4 row blocks of 16 (kSkinnyMaxM in the HIP source)
 SKINNY_PIPE_ROWS = 64 * 2   # stage rows x stages in flight (kSkinny* in the HIP source)
 LDS_PER_CU = 160 * 1024
@@ -297,12 +302,41 @@ def _packed_parts(plan):
     return dma, rest
 
 
+def persistent_lds(k):
+    """LDS per workgroup of the persistent 256x256 kernel for a K (slice):
+    the 16x16x64 kernel when K % 256 == 0, else the 32x32x32 one (plans
+    assume 16-byte aligned C and D with rows of n elements)."""
+    return DMA16_LDS if k % 256 == 0 else DMA_LDS
+
+
+def mfma_tiles(plan):
+    """Output tiles an MFMA plan runs, over every batch and K slice (shared-B
+    batches folded into m); the persistent kernel walks them in rounds."""
+    tm, tn = TILES[plan["variant"]][:2]
+    m, batch = plan["m"], plan["batch"]
+    if plan["b_shared"] and batch > 1:
+        m, batch = m * batch, 1
+    return -(-m // tm) * -(-plan["n"] // tn) * batch * mfma_k_split(plan)
+
+
+def _runs_persistent(plan):
+    """Whether an mfma_256x256 plan (without a row or column split) runs on
+    the persistent kernel: each K slice in whole 64-deep steps and M (after
+    the fold) and N at least one tile (persistent_fits in the HIP source)."""
+    if plan["variant"] != "mfma_256x256":
+        return False
+    m = plan["m"] * plan["batch"] if plan["b_shared"] and plan["batch"] > 1 else plan["m"]
+    kslice = plan["k"] // mfma_k_split(plan)
+    return kslice > 0 and kslice % 64 == 0 and m >= 256 and plan["n"] >= 256
+
+
 def required_resources(plan):
     """(lds_bytes per workgroup, workgroups) the plan's variant launches.
 
     The analogue of backend.py:97-104 (scratchpad / accumulator rows) for a
     gfx950 launch: LDS is the on-chip buffer a workgroup needs, workgroups
-    the grid size.
+    the grid size. The persistent 256x256 kernel launches one workgroup per
+    CU (at most) whatever the tile count.
     """
     variant = plan["variant"]
     tm, tn, _, _, lds = TILES[variant]
@@ -311,11 +345,12 @@ def required_resources(plan):
         parts = _mfma_parts(plan)
         if parts is not None:   # whole tiles on the persistent kernel, then the rest
             top, rest = parts
+            lds_t, wgs_t = required_resources(top)
             lds_r, wgs_r = required_resources(rest)
-            return max(lds, lds_r), top["m"] // tm * (top["n"] // tn) * top["batch"] + wgs_r
-        if plan["b_shared"] and batch > 1:      # stacked-M fold
-            m, batch = m * batch, 1
-        return lds, -(-m // tm) * -(-n // tn) * batch * mfma_k_split(plan)
+            return max(lds_t, lds_r), wgs_t + wgs_r
+        if _runs_persistent(plan):
+            return persistent_lds(plan["k"] // mfma_k_split(plan)), min(mfma_tiles(plan), NUM_CUS)
+        return lds, mfma_tiles(plan)
     if variant == "skinny":
         ks, chunk = skinny_split(plan)
         return (lds + 16 * skinny_row_blocks(m) * skinny_a_stride(chunk),
@@ -324,7 +359,7 @@ def required_resources(plan):
         dma, rest = _packed_parts(plan)
         lds_out, wgs = 0, 0
         if dma is not None:
-            lds_out, wgs = DMA_LDS, min(required_resources(dma)[1], NUM_CUS)
+            lds_out, wgs = persistent_lds(plan["k"]), min(required_resources(dma)[1], NUM_CUS)
         if rest is not None and rest["variant"] != PACKED_VARIANT:
             lds_r, wgs_r = required_resources(rest)
             lds_out, wgs = max(lds_out, lds_r), wgs + wgs_r
@@ -578,8 +613,11 @@ def modeled_objective(plan, counts):
         m, b = m * b, 1
     padded_ops = 2 * b * (-(-m // tm) * tm) * (-(-n // tn) * tn) * k
     wgs = counts["workgroups"]
-    waves = -(-wgs // NUM_CUS)
-    fill = wgs / (waves * NUM_CUS) if wgs else 1.0
+    # rounds of work over the CUs: MFMA tiles (the persistent kernel walks
+    # them with one workgroup per CU), else workgroups
+    units = mfma_tiles(plan) if variant.startswith("mfma") else wgs
+    waves = -(-units // NUM_CUS)
+    fill = units / (waves * NUM_CUS) if units else 1.0
     eff = _MODEL_MFMA_EFF[variant] * (fill if variant.startswith("mfma") else 1.0)
     t_compute = padded_ops / (PEAK_INT8_OPS * eff)
     t_memory = counts["bytes_algorithmic"] / (PEAK_HBM_BYTES * min(1.0, wgs / NUM_CUS))
