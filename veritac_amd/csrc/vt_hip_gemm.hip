@@ -1447,9 +1447,16 @@ struct ReduceArgs {
   int M, N, k_split;
 };
 
+// One wave per workgroup: the sums of a decode step (M = 16: 57344 threads)
+// spread over every CU instead of one 256-thread workgroup on each of 224
+// (M = 16, K = 4096, N = 14336, 120 graph steps: 14.72 -> 14.65 us; M = 1,
+// where 256-thread workgroups covered only 14 CUs: 13.46 -> 13.25 us;
+// 128 threads measured between the two, 512 and 1024 slower).
+constexpr int kReduceThreads = 64;
+
 template <bool HAS_D>
-__global__ __launch_bounds__(256) void skinny_reduce_kernel(ReduceArgs p) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;   // over M*N/4 (N % 16 == 0)
+__global__ __launch_bounds__(kReduceThreads) void skinny_reduce_kernel(ReduceArgs p) {
+  const int64_t i = (int64_t)blockIdx.x * kReduceThreads + threadIdx.x;   // over M*N/4 (N % 16 == 0)
   const int64_t per = (int64_t)p.M * p.N / 4;
   if (i >= per) return;
   const int bidx = blockIdx.y;
@@ -2184,6 +2191,18 @@ Problem mfma_fold(const Problem &q) {
   return r;
 }
 
+// C = D + the k_split partial sums in ws, on `stream` after the kernel that
+// wrote them (stream order publishes the partials).
+int launch_reduce(const ReduceArgs &r, int64_t batch, hipStream_t stream) {
+  const int64_t per = (int64_t)r.M * r.N / 4;
+  if (per > 0x7fffffff || batch > 65535) return fail(VT_EUNSUPPORTED, "reduction grid too large");
+  dim3 grid((unsigned)((per + kReduceThreads - 1) / kReduceThreads), (unsigned)batch);
+  if (r.D) hipLaunchKernelGGL(skinny_reduce_kernel<true>, grid, dim3(kReduceThreads), 0, stream, r);
+  else hipLaunchKernelGGL(skinny_reduce_kernel<false>, grid, dim3(kReduceThreads), 0, stream, r);
+  VT_HIP_CHECK(hipGetLastError());
+  return VT_OK;
+}
+
 // K slices for an MFMA launch whose tiles alone would leave most of the chip
 // idle: a K of at least 1024 over at most 64 tiles is cut into ks slices of
 // whole 128-deep steps, each at least 512 deep, for up to 256 workgroups. The
@@ -2329,12 +2348,7 @@ int launch_mfma(const Problem &q, Scratch &scr) {
   ra.ws = (const int32_t *)w; ra.D = r.D; ra.C = r.C;
   ra.ldd = r.ldd; ra.ldc = r.ldc; ra.sd = 0; ra.sc = 0;
   ra.M = (int)r.M; ra.N = (int)r.N; ra.k_split = ks;
-  const int64_t per = r.M * r.N / 4;
-  dim3 rgrid((unsigned)((per + 255) / 256), 1);
-  if (r.D) hipLaunchKernelGGL(skinny_reduce_kernel<true>, rgrid, dim3(256), 0, stream, ra);
-  else hipLaunchKernelGGL(skinny_reduce_kernel<false>, rgrid, dim3(256), 0, stream, ra);
-  VT_HIP_CHECK(hipGetLastError());
-  return VT_OK;
+  return launch_reduce(ra, 1, stream);
 }
 
 template <int BM, int BN, bool PACKED>
@@ -2464,11 +2478,8 @@ int launch_skinny_cfg(const Problem &q, int k_split, Scratch &scr) {
     r.ws = a.ws; r.D = q.D; r.C = q.C;
     r.ldd = q.ldd; r.ldc = q.ldc; r.sd = q.sd; r.sc = q.sc;
     r.M = (int)q.M; r.N = (int)q.N; r.k_split = ks;
-    const int64_t per = q.M * q.N / 4;
-    dim3 rgrid((unsigned)((per + 255) / 256), (unsigned)q.batch);
-    if (q.D) hipLaunchKernelGGL(skinny_reduce_kernel<true>, rgrid, dim3(256), 0, s, r);
-    else hipLaunchKernelGGL(skinny_reduce_kernel<false>, rgrid, dim3(256), 0, s, r);
-    VT_HIP_CHECK(hipGetLastError());
+    const int rc = launch_reduce(r, q.batch, s);
+    if (rc) return rc;
   }
   return VT_OK;
 }
@@ -2628,11 +2639,8 @@ int launch_packed_rows(const Problem &q, int k_split, Scratch &scr) {
     r.ws = a.ws; r.D = q.D; r.C = q.C;
     r.ldd = q.ldd; r.ldc = q.ldc; r.sd = q.sd; r.sc = q.sc;
     r.M = (int)q.M; r.N = (int)q.N; r.k_split = a.k_split;
-    const int64_t per = q.M * q.N / 4;
-    dim3 rgrid((unsigned)((per + 255) / 256), (unsigned)q.batch);
-    if (q.D) hipLaunchKernelGGL(skinny_reduce_kernel<true>, rgrid, dim3(256), 0, s, r);
-    else hipLaunchKernelGGL(skinny_reduce_kernel<false>, rgrid, dim3(256), 0, s, r);
-    VT_HIP_CHECK(hipGetLastError());
+    const int rc = launch_reduce(r, q.batch, s);
+    if (rc) return rc;
   }
   return VT_OK;
 }
