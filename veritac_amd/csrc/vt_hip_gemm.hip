@@ -1153,9 +1153,9 @@ __global__ __launch_bounds__(256, 1) void gemm_dma16_kernel(GemmArgs p) {
   int32_t *c_tile = nullptr;   // the wave's block of C in the current tile
   LDS_AS int8_t *const lds = (LDS_AS int8_t *)smem;
   const StripLanes sl = strip_lanes(lane, NSTAGE * (A_BYTES + B_BYTES) + wave * 8192, p.ldc, p.ldd);
-  // One step: MFMAs of slice gs, row by row, from fa and fb; slice gs + 1's B
-  // blocks go to gb in the first BU slots (block order = first use), its A
-  // blocks to fa as each row's last MFMA retires.
+  // One step: MFMAs of slice gs, row by row (odd rows right to left), from fa
+  // and fb; slice gs + 1's B blocks go to gb in the first BU slots (block
+  // order = first use), its A blocks to fa as each row's last MFMA retires.
   // stg = gs % 4, a compile-time constant at every call.
   // early (compile time; the last step of a tile without D): strips 0 ..
   // EARLY_STRIPS - 1 of the tile's C go out during the step, strip r at slot
@@ -1169,10 +1169,13 @@ __global__ __launch_bounds__(256, 1) void gemm_dma16_kernel(GemmArgs p) {
     const uint32_t mb = ma + B_REGION;
 #pragma unroll
     for (int slot = 0; slot < MI * NI; ++slot) {
-      const int mi = slot / NI, ni = slot % NI;
+      // Odd rows take their B blocks in reverse ("snake"), so each row's
+      // first MFMA reuses the previous one's B operand: 8192^3 1-2 % faster
+      // (kernel average, three interleaved rounds on each of two boxes).
+      const int mi = slot / NI, pos = slot % NI, ni = (mi & 1) ? NI - 1 - pos : pos;
       mfma16_in_place(acc[mi][ni], fa[mi], fb[ni]);
       if (slot < BU) read_b(s1, slot, gb);
-      if (ni == NI - 1) read_a(s1, mi);
+      if (pos == NI - 1) read_a(s1, mi);
       if ((slot & 7) == 2) {
         const int d = slot >> 3;
         if (d < DPW) dma_b128(abase, a_lane[d], ma + d * 1024);
