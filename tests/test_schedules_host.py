@@ -266,3 +266,15 @@ def test_every_stream_the_check_accepts_computes_the_gemm():
                 accepted += 1
                 assert oracle_equals_gemm(plan, mut, seed=3, modes=("lcg", "minmax"))
     assert refused > 300 and accepted > 0
+
+
+def test_malformed_commands_are_refused_not_raised():
+    plan = sc.make_plan(16, 16, 16, "baseline")
+    cmds = sc.gen_commands(plan)
+    for bad in (dict(cmds[7], a_spad_addr=[0]), dict(cmds[6], out_addr=None),
+                {k: v for k, v in cmds[4].items() if k != "spad_addr"}, "mvin", None):
+        mutated = cmds[:4] + [bad] + cmds[5:]
+        ok, why = sc.check_program(plan, mutated)
+        assert not ok and why.startswith(sc.EXECUTION_REJECTED), (bad, why)
+    assert not sc.check_program(plan, "not a list")[0]
+    assert not sc.check_program({"m": 16}, cmds)[0]

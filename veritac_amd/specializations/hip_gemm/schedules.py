@@ -262,6 +262,8 @@ class _Symbolic:
             op(c)
         except KeyError as exc:
             raise _Rejected("%s command lacks field %s" % (kind, exc)) from None
+        except TypeError:
+            raise _Rejected("%s command has a field of the wrong type" % kind) from None
 
     def _config_ex(self, c):
         if c["dataflow"] != _rp.WEIGHT_STATIONARY:
