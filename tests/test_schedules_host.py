@@ -65,7 +65,7 @@ def test_the_ai_repair_edge_is_baseline_to_batched_reuse(commands):
             c["accumulated"] = False
     assert relatched == dst["commands"]
     for cmds in (gen, relatched):
-        assert sc.check_program(dst["plan"], cmds) == (True, "accepted")
+        assert sc.check_program(dst["plan"], cmds)[:2] == (True, "accepted")
 
 
 def test_reuse_b_is_one_batch_of_every_row():
@@ -124,7 +124,7 @@ def test_optimize_selects_reuse_b_unless_the_accumulator_is_too_small():
 
 def test_check_accepts_every_certified_stream_and_refuses_each_witness(commands):
     for s in commands:
-        ok, why = sc.check_program(s["plan"], s["commands"])
+        ok, why, _ = sc.check_program(s["plan"], s["commands"])
         if "witness" in s:
             w = s["witness"]
             assert not ok and why.startswith(sc.OUTPUT_MISMATCH), s["name"]
@@ -140,7 +140,7 @@ def test_unseen_shapes_both_schedules():
         for schedule in sc.SCHEDULES:
             plan = sc.make_plan(*shape, schedule)
             cmds = sc.gen_commands(plan)
-            assert sc.check_program(plan, cmds) == (True, "accepted"), (shape, schedule)
+            assert sc.check_program(plan, cmds)[:2] == (True, "accepted"), (shape, schedule)
             assert oracle_equals_gemm(plan, cmds, modes=("lcg", "minmax"))
 
 
@@ -150,7 +150,7 @@ def test_independent_output_tiles_can_be_reversed():
     cmds = sc.gen_commands(plan)
     rev = cmds[:4] + cmds[13:22] + cmds[4:13] + cmds[-1:]
     assert rev != cmds
-    assert sc.check_program(plan, rev) == (True, "accepted")
+    assert sc.check_program(plan, rev)[:2] == (True, "accepted")
     assert oracle_equals_gemm(plan, rev, modes=("lcg",))
 
 
@@ -161,7 +161,7 @@ def test_partial_sum_overwrite_is_rejected():
     cmds = copy.deepcopy(sc.gen_commands(plan))
     next(c for c in cmds if c["kind"] == "preload" and c["out_addr"] & sc.ACCUMULATE_BIT)[
         "out_addr"] &= ~sc.ACCUMULATE_BIT
-    ok, why = sc.check_program(plan, cmds)
+    ok, why, _ = sc.check_program(plan, cmds)
     assert not ok and why.startswith(sc.OUTPUT_MISMATCH)
     assert not oracle_equals_gemm(plan, cmds, modes=("max",))
 
@@ -183,7 +183,7 @@ def test_batched_reuse_handles_partial_last_batch():
     plan = sc.make_plan(48, 16, 32, "baseline")
     plan["accumulator_rows"] = 32
     cmds = sc.gen_batched_reuse_b(plan, 2)
-    assert sc.check_program(plan, cmds) == (True, "accepted")
+    assert sc.check_program(plan, cmds)[:2] == (True, "accepted")
     assert sc.modeled_counts(cmds)["mvin_B"] == 4
     assert oracle_equals_gemm(plan, cmds)
 
@@ -193,7 +193,7 @@ def test_overlarge_batch_is_rejected_by_execution():
     rows of a plan that has 32."""
     plan = sc.make_plan(48, 16, 32, "baseline")
     plan["accumulator_rows"] = 32
-    ok, why = sc.check_program(plan, sc.gen_batched_reuse_b(plan, 3))
+    ok, why, _ = sc.check_program(plan, sc.gen_batched_reuse_b(plan, 3))
     assert not ok and "execution rejected" in why
 
 
@@ -210,7 +210,7 @@ def test_zero_batch_and_invalid_plans_raise():
 def test_missing_fence_and_product_order_are_refused():
     plan = sc.make_plan(16, 16, 32, "baseline")
     cmds = sc.gen_commands(plan)
-    assert sc.check_program(plan, cmds[:-1]) == (False, sc.NOT_DRAINED)
+    assert sc.check_program(plan, cmds[:-1]) == (False, sc.NOT_DRAINED, None)
     # The two k steps swapped: the same sum mod 2^32, but not the product
     # sequence the specification fixes (Symbolic.lean:30-34 compares lists).
     body = cmds[4:-2]
@@ -218,7 +218,7 @@ def test_missing_fence_and_product_order_are_refused():
     swapped[6]["out_addr"] &= ~sc.ACCUMULATE_BIT
     swapped[10]["out_addr"] |= sc.ACCUMULATE_BIT
     assert oracle_equals_gemm(plan, swapped, modes=("lcg",))
-    ok, why = sc.check_program(plan, swapped)
+    ok, why, _ = sc.check_program(plan, swapped)
     assert not ok and why.startswith(sc.OUTPUT_MISMATCH)
 
 
@@ -259,7 +259,7 @@ def test_every_stream_the_check_accepts_computes_the_gemm():
                            (sc.make_plan(m, n, k, "reuse_b"), None)):
             cmds = sc.gen_commands(plan)
             for mut in _mutants(cmds, rng, 150):
-                ok, _ = sc.check_program(plan, mut)
+                ok = sc.check_program(plan, mut)[0]
                 if not ok:
                     refused += 1
                     continue
@@ -274,7 +274,80 @@ def test_malformed_commands_are_refused_not_raised():
     for bad in (dict(cmds[7], a_spad_addr=[0]), dict(cmds[6], out_addr=None),
                 {k: v for k, v in cmds[4].items() if k != "spad_addr"}, "mvin", None):
         mutated = cmds[:4] + [bad] + cmds[5:]
-        ok, why = sc.check_program(plan, mutated)
+        ok, why, _ = sc.check_program(plan, mutated)
         assert not ok and why.startswith(sc.EXECUTION_REJECTED), (bad, why)
     assert not sc.check_program(plan, "not a list")[0]
     assert not sc.check_program({"m": 16}, cmds)[0]
+
+
+def test_accepted_receipt_and_reference_return_shape():
+    plan = sc.make_plan(32, 32, 32, "reuse_b")
+    ok, why, receipt = sc.check_program(plan, sc.gen_commands(plan))
+    assert ok and why == "accepted"
+    assert receipt["cells"] == 32 * 32 and receipt["products_per_cell"] == 32
+
+
+def _mutated(schedule, m, n, k, mutate):
+    plan = sc.make_plan(m, n, k, schedule)
+    cmds = copy.deepcopy(sc.gen_commands(plan))
+    mutate(cmds)
+    return plan, cmds
+
+
+def _first(cmds, kind, **fields):
+    return next(c for c in cmds if c["kind"] == kind and all(c[f] == v for f, v in fields.items()))
+
+
+def _bump(cmd, field, by):
+    cmd[field] += by
+
+
+def _drop_last(cmds, kind):
+    del cmds[max(i for i, x in enumerate(cmds) if x["kind"] == kind)]
+
+
+# The command-level mutations of the reference's tests/test_gemmini_program.py
+# (:95-171, :261-281): each must be refused by the check alone. The
+# reference's byte-encoding mutations, and the trailing duplicate fence and
+# the swap of the two leading configuration commands (:161-171), are refused
+# there by the binding of commands to executable bytes; the command streams
+# they leave still compute the GEMM, so the check accepts them.
+PROGRAM_MUTATIONS = {
+    "mvin A offset + 16": lambda c: _bump(_first(c, "mvin", slot=0), "offset", 16),
+    "mvin B offset + 8": lambda c: _bump(_first(c, "mvin", slot=1), "offset", 8),
+    "A stride + 1": lambda c: _bump(_first(c, "config_ld", slot=0), "stride_bytes", 1),
+    "accumulate flag flipped": lambda c: _bump(_first(c, "preload"), "out_addr", sc.ACCUMULATE_BIT),
+    "preload source dropped": lambda c: _first(c, "preload").update(bd_spad_addr=sc.GARBAGE_ADDR),
+    "missing fence": lambda c: _drop_last(c, "fence"),
+    "missing mvout": lambda c: _drop_last(c, "mvout"),
+    "unknown op": lambda c: c.insert(0, {"kind": "flush"}),
+    "out of bound memory": lambda c: _first(c, "mvin", buf="A").update(offset=10 ** 9),
+    "output-stationary dataflow": lambda c: _first(c, "config_ex").update(dataflow=0),
+}
+
+
+@pytest.mark.parametrize("name", sorted(PROGRAM_MUTATIONS))
+@pytest.mark.parametrize("shape", [(16, 16, 16), (64, 64, 64)])
+def test_reference_program_mutations_are_refused(name, shape):
+    plan, cmds = _mutated("baseline", *shape, PROGRAM_MUTATIONS[name])
+    assert not sc.check_program(plan, cmds)[0], (name, shape)
+
+
+def test_retained_compute_turned_preloaded_is_refused():
+    """tests/test_gemmini_program.py:125-130: a reuse_b compute that retains
+    B, turned into one that latches it, has no B source to latch."""
+    plan = sc.make_plan(32, 16, 16, "reuse_b")
+    cmds = copy.deepcopy(sc.gen_commands(plan))
+    assert sc.check_program(plan, cmds)[0]
+    _first(cmds, "compute", accumulated=True)["accumulated"] = False
+    assert not sc.check_program(plan, cmds)[0]
+
+
+def test_byte_bound_mutations_leave_the_gemm():
+    """The two command mutations the reference refuses only through the
+    executable bytes compute the GEMM, and the check accepts them."""
+    plan = sc.make_plan(16, 16, 16, "baseline")
+    cmds = sc.gen_commands(plan)
+    for mutated in (cmds + [copy.deepcopy(cmds[-1])], [cmds[1], cmds[0]] + cmds[2:]):
+        assert sc.check_program(plan, mutated)[:2] == (True, "accepted")
+        assert oracle_equals_gemm(plan, mutated, modes=("lcg", "minmax"))

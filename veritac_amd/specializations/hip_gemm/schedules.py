@@ -187,7 +187,7 @@ def optimize(m, n, k, *, scratchpad_rows=_rp.SCRATCHPAD_ROWS, accumulator_rows=_
                  "objective": None}
         if ok:
             cmds = gen_commands(plan)
-            accepted, why = check_program(plan, cmds)
+            accepted, why, _ = check_program(plan, cmds)
             entry["check"] = {"accepted": accepted, "reason": why}
             if accepted:
                 entry["counts"] = modeled_counts(cmds)
@@ -379,26 +379,33 @@ class _Symbolic:
 
 
 def check_program(plan, commands):
-    """(accepted, reason) for a command stream under a Gemmini plan: the plan
-    is valid with dim 16, every command executes under Engine.lean's rules,
-    the stream ends drained by a fence, and every output cell holds exactly
-    its GEMM product sequence (Symbolic.lean:36-47; the reasons are the
-    diagnostics of :39-47, with the failing command or cell appended)."""
+    """(accepted, reason, receipt) for a command stream under a Gemmini plan,
+    the return shape of the reference's check_program (backend.py:989-997).
+    Accepted: the plan is valid with dim 16, every command executes under
+    Engine.lean's rules, the stream ends drained by a fence, and every output
+    cell holds exactly its GEMM product sequence (Symbolic.lean:36-47). The
+    reasons are the diagnostics of Symbolic.lean:39-47, with the failing
+    command or cell appended. The receipt (None when refused) says what was
+    checked; it is not a proof certificate, and the executable-byte half of
+    the reference's check has no counterpart here."""
     ok, why = _rp.validate_plan(plan)
     if not ok:
-        return False, why
+        return False, why, None
     if not isinstance(commands, (list, tuple)):
-        return False, EXECUTION_REJECTED + " (commands must be a list)"
+        return False, EXECUTION_REJECTED + " (commands must be a list)", None
     s = _Symbolic(plan)
     for index, c in enumerate(commands):
         try:
             s.step(c)
         except _Rejected as exc:
-            return False, "%s (command %d: %s)" % (EXECUTION_REJECTED, index, exc)
+            return False, "%s (command %d: %s)" % (EXECUTION_REJECTED, index, exc), None
     if not s.drained:
-        return False, NOT_DRAINED
+        return False, NOT_DRAINED, None
     cell = s.first_wrong_cell()
     if cell is not None:
         n = plan["n"]
-        return False, "%s (cell %d: row %d, col %d)" % (OUTPUT_MISMATCH, cell, cell // n, cell % n)
-    return True, ACCEPTED
+        return (False, "%s (cell %d: row %d, col %d)" % (OUTPUT_MISMATCH, cell, cell // n, cell % n),
+                None)
+    m, n, k = plan["m"], plan["n"], plan["k"]
+    return True, ACCEPTED, {"checker": "symbolic GEMM product sequences (Symbolic.lean:36-47)",
+                            "commands": len(commands), "cells": m * n, "products_per_cell": k}
