@@ -48,7 +48,7 @@ TRAFFIC_GEMM_8192 = {"read": 805.7e6, "written": 268.7e6}   # gemm_dma16_kernel
 TRAFFIC_DECODE = {  # (packed B, M) -> bytes per step
     (False, 16): {"read": 58.90e6 + 3.73e6, "written": 3.74e6 + 0.92e6},
     (True, 16): {"read": 59.3e6, "written": 0.92e6},
-    (False, 1): {"read": 58.78e6 + 0.28e6, "written": 0.24e6 + 0.06e6},
+    (False, 1): {"read": 58.78e6, "written": 0.63e6},
     (True, 1): {"read": 58.80e6, "written": 0.06e6},
 }
 
@@ -338,8 +338,10 @@ def bench_decode(dev, steps, warmup, packed=False, m=16):
     gbps = alg / (ms / 1e3) / 1e9
     traffic = TRAFFIC_DECODE.get((packed, m))
     split = plan["k_split"] > 1
+    finished = not packed and hg.skinny_finishes(plan)
     kernels = ("packed_skinny_kernel<4,8,2>" if packed else "skinny_kernel<256,16,2>") + \
-        (" + skinny_reduce_kernel" if split else "") + " per step"
+        (" (K slices finished in the kernel)" if finished else
+         " + skinny_reduce_kernel" if split else "") + " per step"
     out = {
         "metric": ("HBM GB/s @M=%d decode shape (M=%d, K=4096, N=14336)" % (m, m)
                    + (", B prepacked" if packed else "")),

@@ -112,12 +112,18 @@ extern "C" {
  *
  * Workspace: the skinny variant's K-split partial sums and the padded
  * variant's copies live in workspaces the library allocates per (device,
- * stream, kind). A workspace only grows, and a superseded one is kept (not
- * freed) until the process ends, so a HIP graph captured with an earlier
- * workspace stays valid. Growth is refused while the stream is being
- * captured: a call that needs more workspace than its stream has returns
- * VT_EUNSUPPORTED during capture, so make the largest call once on the
- * stream before capturing (vt_gemm_check reports the bytes a call needs).
+ * stream, kind). With a K split over at most 4 rows the skinny kernel
+ * finishes the slices' sums itself, through one 8-byte finishing word per
+ * output element in a workspace of its own kind that is zeroed when it is
+ * allocated and that every call leaves zero (no second launch, and never
+ * more bytes than the partial sums). A workspace only grows, and a
+ * superseded one is kept (not freed) until the process ends, so a HIP graph
+ * captured with an earlier workspace stays valid. Growth is refused while
+ * the stream is being captured: a call that needs more workspace than its
+ * stream has returns VT_EUNSUPPORTED during capture, so make the same calls
+ * once on the stream before capturing (vt_gemm_check reports the bytes a
+ * call takes from vt_gemm_i8_noalloc's array, which bounds what it takes
+ * from a stream's workspaces).
  *
  * Sizes up to 2^40, leading dimensions up to 2^40, batch up to 2^31, batch
  * strides up to 2^56, and every operand's byte extent below 2^56. C may not

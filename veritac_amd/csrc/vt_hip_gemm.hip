@@ -1288,7 +1288,15 @@ struct SkinnyArgs {
   int k_split;     // K slices per column slab (workgroups along K)
   int k_chunk;     // rows per slice, a multiple of the stage rows x U
   int32_t *ws;     // [batch][k_split][M][N] partials when k_split > 1
+  uint64_t *fin;   // [batch][M][N] finishing words (FIN), zero between launches
 };
+
+// Finishing word of a K-split output element finished in the kernel: each of
+// the k_split slices adds (1 << kFinCountShift) | partial, the partial as an
+// unsigned 32-bit value. Bits 0-31 then hold the slices' sum mod 2^32, bits
+// 32-47 its carries (fewer than k_split) and bits 48-63 the number of slices
+// that have added, so k_split must stay below 2^16 (the host checks).
+constexpr int kFinCountShift = 48;
 
 // One workgroup = WAVES waves streams an NB-column slab of B over one K slice.
 // Every thread moves one 16-byte chunk per stage, so a stage is R = WAVES*1024/NB
@@ -1299,7 +1307,16 @@ struct SkinnyArgs {
 // MB row blocks of 16 (M <= 16 * MB): the A slice holds 16 * MB rows and each
 // wave reuses its B fragment for MB MFMAs, one per row block, so B is still
 // streamed once for up to 64 rows.
-template <int NB, int WAVES, int U, int MB, bool HAS_D>
+// With a K split the slices' partial sums either go to the workspace for
+// skinny_reduce_kernel, or (FIN) are finished here: each slice adds its
+// partial into the element's finishing word with one agent-scope atomic add,
+// and the slice whose add returns k_split - 1 earlier arrivals holds the whole
+// sum (the low 32 bits of the returned word plus its own partial, mod 2^32).
+// It writes C (plus D) and swaps the word back to 0. Every step is a
+// read-modify-write of that one word, so the word's single modification order
+// alone decides which slice is last and what it sees: no fence, no flag in
+// other memory, no second kernel.
+template <int NB, int WAVES, int U, int MB, bool HAS_D, bool FIN = false>
 __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(SkinnyArgs p) {
   constexpr int THREADS = 64 * WAVES;
   constexpr int NBLK = NB / 16;               // 16-column blocks = chunks per row
@@ -1310,6 +1327,7 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(SkinnyArgs p) {
   static_assert(NBLK == 16, "skinny_b_swz assumes 256-byte stage rows");
   static_assert(U % 2 == 0, "stages alternate between two LDS buffers by u & 1");
   static_assert(KB == 1 || MB == 1, "the cross-wave sum holds one row block");
+  static_assert(!FIN || MB == 1, "finishing in the kernel is instantiated for M <= 16");
 
   extern __shared__ __attribute__((aligned(16))) int8_t dsmem[];
   const int a_stride = skinny_a_stride(p.k_chunk);
@@ -1425,6 +1443,26 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(SkinnyArgs p) {
           Cb[(int64_t)row * p.ldc + col] = v;
         }
       }
+  } else if constexpr (FIN) {
+    uint64_t *fb = p.fin + (int64_t)bidx * M * N;
+    const int32_t *Db = HAS_D ? p.D + bidx * p.sd : nullptr;
+    int32_t *Cb = p.C + bidx * p.sc;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int row = g * 4 + e;
+      if (row < M) {
+        uint64_t *word = fb + (int64_t)row * N + col;
+        const uint64_t old =
+            __hip_atomic_fetch_add(word, (1ull << kFinCountShift) | (uint32_t)acc[0][e],
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if ((int)(old >> kFinCountShift) == p.k_split - 1) {
+          int32_t v = add_wrap(acc[0][e], (int32_t)(uint32_t)old);
+          if (HAS_D) v = add_wrap(v, Db[(int64_t)row * p.ldd + col]);
+          Cb[(int64_t)row * p.ldc + col] = v;
+          __hip_atomic_exchange(word, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+    }
   } else {
     int32_t *wsb = p.ws + ((int64_t)bidx * p.k_split + split) * M * N;
 #pragma unroll
@@ -1863,6 +1901,12 @@ const VariantInfo kVariants[VT_VARIANT_COUNT] = {
 constexpr int kSkinnyNB = 256, kSkinnyWaves = 16, kSkinnyU = 2;
 // Rows the skinny kernel takes: up to 4 row blocks of 16.
 constexpr int kSkinnyMaxM = 64;
+// Up to this many rows a K-split skinny launch finishes its sums in the kernel
+// (skinny_kernel FIN) instead of a second launch: K = 4096, N = 14336, four
+// slices, HIP graph per step: M = 1 11.8 against 13.4 us, M = 2 12.4 against
+// 13.6, M = 4 13.7 against 14.0, M = 8 14.6 against 14.2 (one atomic per
+// element and slice; from 8 rows they cost more than the second launch).
+constexpr int kSkinnyFinMaxM = 4;
 // Row blocks of 16 the skinny kernel is instantiated with for M rows.
 int skinny_row_blocks(int64_t M) { return M <= 16 ? 1 : M <= 32 ? 2 : 4; }
 // LDS for the replay's scratchpad and accumulator (plus the latched B tile).
@@ -1871,7 +1915,7 @@ constexpr int kMaxSkinnyLds = 160 * 1024;
 
 // Scratch memory of one call: the K-split partial sums of the decode
 // kernels and the padded variant's operand copies.
-enum ScratchKind { kPartials = 0, kPadded = 1, kScratchKinds = 2 };
+enum ScratchKind { kPartials = 0, kPadded = 1, kFinWords = 2, kScratchKinds = 3 };
 
 struct Workspace {
   void *ptr = nullptr;
@@ -1954,6 +1998,10 @@ int get_workspace(DeviceState *st, void *stream, ScratchKind kind, size_t bytes,
     if (nb < (1u << 20)) nb = 1u << 20;
     void *p = nullptr;
     VT_HIP_CHECK(hipMalloc(&p, nb));
+    // Finishing words read zero before their first launch, and every launch
+    // leaves them zero. The clear is ordered before that launch on the same
+    // stream; it is never captured, since growth under capture is refused above.
+    if (kind == kFinWords) VT_HIP_CHECK(hipMemsetAsync(p, 0, nb, (hipStream_t)stream));
     if (w.ptr) st->retired.push_back(w.ptr);
     w.ptr = p;
     w.bytes = nb;
@@ -2434,11 +2482,19 @@ SkinnyGeom skinny_geometry(const Problem &q, int k_split) {
   return SkinnyGeom{chunk, lds, (int)((q.K + chunk - 1) / chunk)};
 }
 
-template <int NB, int WAVES, int U, int MB>
+template <int NB, int WAVES, int U, int MB, bool FIN = false>
 void launch_skinny_kernel(bool has_d, dim3 grid, dim3 block, size_t lds, hipStream_t s,
                           const SkinnyArgs &a) {
-  if (has_d) hipLaunchKernelGGL((skinny_kernel<NB, WAVES, U, MB, true>), grid, block, lds, s, a);
-  else hipLaunchKernelGGL((skinny_kernel<NB, WAVES, U, MB, false>), grid, block, lds, s, a);
+  if (has_d) hipLaunchKernelGGL((skinny_kernel<NB, WAVES, U, MB, true, FIN>), grid, block, lds, s, a);
+  else hipLaunchKernelGGL((skinny_kernel<NB, WAVES, U, MB, false, FIN>), grid, block, lds, s, a);
+}
+
+// Whether a K-split skinny launch finishes its sums in the kernel: few rows,
+// a finishing-word count that fits, and a per-stream workspace (the fixed
+// scratch of vt_gemm_i8_noalloc is not kept zero, so those calls take the
+// second launch).
+bool skinny_finishes(int64_t M, int ks, const Scratch &scr) {
+  return ks > 1 && ks < (1 << 16) && M <= kSkinnyFinMaxM && !scr.fixed;
 }
 
 template <int NB, int WAVES, int U>
@@ -2457,9 +2513,16 @@ int launch_skinny_cfg(const Problem &q, int k_split, Scratch &scr) {
   a.k_split = ks;
   a.k_chunk = (int)chunk;
   a.ws = nullptr;
+  a.fin = nullptr;
   if ((int64_t)a.tiles_n * ks > 0x7fffffff || q.batch > 65535)
     return fail(VT_EUNSUPPORTED, "skinny grid too large");
-  if (ks > 1) {
+  const bool fin = skinny_finishes(q.M, ks, scr);
+  if (fin) {
+    void *w = nullptr;
+    int rc = scr.take(kFinWords, (size_t)q.batch * q.M * q.N * sizeof(uint64_t), &w);
+    if (rc) return rc;
+    a.fin = (uint64_t *)w;
+  } else if (ks > 1) {
     void *w = nullptr;
     const size_t pbytes = (size_t)q.batch * ks * q.M * q.N * sizeof(int32_t);
     int rc = scr.take(kPartials, pbytes, &w);
@@ -2468,8 +2531,14 @@ int launch_skinny_cfg(const Problem &q, int k_split, Scratch &scr) {
   }
   hipStream_t s = (hipStream_t)scr.stream;
   dim3 grid((unsigned)(a.tiles_n * ks), (unsigned)q.batch), block(64 * WAVES);
-  // With a K split the slices write partials and the reduction applies D.
-  const bool d_in = q.D && ks == 1;
+  // D is added by the kernel that completes a sum: this one without a K
+  // split or when it finishes the slices itself, else the reduction.
+  const bool d_in = q.D && (ks == 1 || fin);
+  if (fin) {
+    launch_skinny_kernel<NB, WAVES, U, 1, true>(d_in, grid, block, (size_t)lds, s, a);
+    VT_HIP_CHECK(hipGetLastError());
+    return VT_OK;
+  }
   switch (skinny_row_blocks(q.M)) {
     case 1: launch_skinny_kernel<NB, WAVES, U, 1>(d_in, grid, block, (size_t)lds, s, a); break;
     case 2: launch_skinny_kernel<NB, WAVES, U, 2>(d_in, grid, block, (size_t)lds, s, a); break;
@@ -3007,6 +3076,8 @@ void set_kernel_attributes(DeviceState &st) {
       {(const void *)skinny_kernel<kSkinnyNB, kSkinnyWaves, kSkinnyU, 2, false>, kMaxSkinnyLds},
       {(const void *)skinny_kernel<kSkinnyNB, kSkinnyWaves, kSkinnyU, 4, true>, kMaxSkinnyLds},
       {(const void *)skinny_kernel<kSkinnyNB, kSkinnyWaves, kSkinnyU, 4, false>, kMaxSkinnyLds},
+      {(const void *)skinny_kernel<kSkinnyNB, kSkinnyWaves, kSkinnyU, 1, true, true>, kMaxSkinnyLds},
+      {(const void *)skinny_kernel<kSkinnyNB, kSkinnyWaves, kSkinnyU, 1, false, true>, kMaxSkinnyLds},
       {(const void *)replay_kernel, kMaxReplayLds + 256},
   };
   for (const auto &n : need) {

@@ -74,6 +74,9 @@ PACKED_WAVES = 8
 DMA_LDS = 4 * (256 * 64 + 64 * 256)
 DMA16_LDS = DMA_LDS + 4 * 8192
 SKINNY_MAX_M = 64   # up to 4 row blocks of 16 (kSkinnyMaxM in the HIP source)
+# Up to this many rows vt_gemm_i8 finishes a K-split skinny launch inside the
+# kernel, through one 64-bit finishing word per output (kSkinnyFinMaxM)
+SKINNY_FIN_MAX_M = 4
 SKINNY_PIPE_ROWS = 64 * 2   # stage rows x stages in flight (kSkinny* in the HIP source)
 LDS_PER_CU = 160 * 1024
 
@@ -112,6 +115,14 @@ def skinny_split(plan):
     if a_rows * skinny_a_stride(chunk) + stage_lds > LDS_PER_CU:
         chunk = ((LDS_PER_CU - stage_lds) // a_rows - 48) // align * align
     return -(-k // chunk), chunk
+
+
+def skinny_finishes(plan):
+    """Whether vt_gemm_i8 finishes this skinny plan's K slices inside the
+    kernel (one launch) rather than in skinny_reduce_kernel (a second
+    launch): a K split over at most SKINNY_FIN_MAX_M rows (skinny_finishes in
+    the HIP source; vt_gemm_i8_noalloc always takes the second launch)."""
+    return skinny_split(plan)[0] > 1 and plan["m"] <= SKINNY_FIN_MAX_M
 
 
 def skinny_row_blocks(m):
@@ -525,7 +536,10 @@ def modeled_counts(plan):
         l2_bytes = b_eff * (tiles_n * m_eff * k + tiles_m * k * n) + c_and_d + partial
     elif variant == "skinny":
         ks, _ = skinny_split(plan)
-        partial = 2 * 4 * b * m * n * ks if ks > 1 else 0
+        # partial sums written and read back, or each slice's atomic add on
+        # an 8-byte finishing word (read and written where it is performed)
+        partial = (16 * b * m * n * ks if skinny_finishes(plan) else
+                   2 * 4 * b * m * n * ks if ks > 1 else 0)
         l2_bytes = alg + partial + b * -(-n // tn) * 16 * k
     elif variant == PACKED_VARIANT:
         dma, rest = _packed_parts(plan)
@@ -627,7 +641,7 @@ def modeled_objective(plan, counts):
         return (_LAUNCH_S + max(t, -(-k // 16) * _GENERIC_STEP_S), wgs)
     launches = 1
     if variant == "skinny":
-        launches += skinny_split(plan)[0] > 1
+        launches += skinny_split(plan)[0] > 1 and not skinny_finishes(plan)
     elif variant == PACKED_VARIANT:
         launches += packed_split(plan)[0] > 1
     else:
