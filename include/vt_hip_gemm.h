@@ -123,7 +123,11 @@ extern "C" {
  * stream has returns VT_EUNSUPPORTED during capture, so make the same calls
  * once on the stream before capturing (vt_gemm_check reports the bytes a
  * call takes from vt_gemm_i8_noalloc's array, which bounds what it takes
- * from a stream's workspaces).
+ * from a stream's workspaces). Graphs captured on one stream use that
+ * stream's workspaces: replay them in order on that stream (or with the same
+ * ordering against it), never two at once. Overlapping launches on one
+ * workspace race, and racing finishing words can stay nonzero and spoil the
+ * later calls that use them.
  *
  * Sizes up to 2^40, leading dimensions up to 2^40, batch up to 2^31, batch
  * strides up to 2^56, and every operand's byte extent below 2^56. C may not
