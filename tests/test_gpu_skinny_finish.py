@@ -159,3 +159,27 @@ def test_graph_replays(dev):
         launch(A2t, B2t, None, C2, 4, stream=s.cuda_stream)
         s.synchronize()
         assert np.array_equal(C2.cpu().numpy(), want(A2, B2, None)), i
+
+
+def test_two_streams_at_once(dev):
+    """Each stream has its own finishing words: finishing launches on two
+    streams, enqueued together and left to overlap, are both exact."""
+    rng = np.random.default_rng(11)
+    s1, s2 = torch.cuda.Stream(device=dev), torch.cuda.Stream(device=dev)
+    jobs = []
+    for s in (s1, s2):
+        A, B, D = operands(rng, 3, 4096, 8192, True)
+        At, Bt, Dt = to_dev(dev, A, B, D)
+        C = torch.full((3, 4096), INT32_MIN, dtype=torch.int32, device=dev)
+        jobs.append((s, A, B, D, At, Bt, Dt, C))
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for s, A, B, D, At, Bt, Dt, C in jobs:
+            C.fill_(INT32_MIN)
+        torch.cuda.synchronize()
+        for s, A, B, D, At, Bt, Dt, C in jobs:
+            launch(At, Bt, Dt, C, 4, stream=s.cuda_stream)
+        torch.cuda.synchronize()
+        say("finish two streams", rep)
+        for s, A, B, D, At, Bt, Dt, C in jobs:
+            assert np.array_equal(C.cpu().numpy(), want(A, B, D)), rep
