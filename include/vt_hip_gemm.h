@@ -62,7 +62,10 @@ extern "C" {
                                       a round of tiles, the rows (columns)
                                       past whole tiles run on 128x128 tiles   */
 #define VT_VARIANT_MFMA_128x128 2  /* 128x128 tile, 4 waves,
-                                      v_mfma_i32_32x32x32_i8                  */
+                                      v_mfma_i32_32x32x32_i8; 64x128 tiles
+                                      with row-major B when that gives at
+                                      most 256 workgroups over at most 2048
+                                      of K (1024 per K slice)                 */
 #define VT_VARIANT_SKINNY 3        /* M <= 64 decode shapes: B streamed once,
                                       v_mfma_i32_16x16x64_i8, K split         */
 #define VT_VARIANT_GENERIC 4       /* any shape/stride/alignment, VALU        */

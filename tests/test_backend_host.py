@@ -228,17 +228,24 @@ def test_mfma_k_split_mirrors_the_native_choice():
         assert hg.mfma_k_split(plan) == want, (m, n, k)
         if variant.startswith("mfma"):
             tm, tn = hg.TILES[variant][:2]
+            # small mfma_128x128 grids run 64x128 tiles (pinned by
+            # test_small_128x128_grids_run_64_row_tiles)
+            half = hg.mfma_half_tiles(plan)
+            if half:
+                tm = 64
             tiles = -(-m // tm) * -(-n // tn) * want
             assert hg.mfma_tiles(plan) == tiles
             persistent = variant == "mfma_256x256" and m >= 256 and n >= 256 and \
                 (k // want) % 64 == 0
             # the persistent kernel: one workgroup per CU, 160 KiB (K slice % 256
             # == 0) or 128 KiB of LDS; the tile kernel: a workgroup per tile
+            lds = 3 * (64 * 64 + 64 * 128) if half else hg.TILES[variant][4]
             assert hg.required_resources(plan) == (
                 (hg.DMA16_LDS if (k // want) % 256 == 0 else hg.DMA_LDS, min(tiles, 256))
-                if persistent else (hg.TILES[variant][4], tiles)), (m, n, k)
+                if persistent else (lds, tiles)), (m, n, k)
             assert ws == (want * m * n * 4 if want > 1 else 0)
-    assert hg.mfma_k_split(hg.make_plan(128, 4096, 4096)) == 8
+    assert hg.mfma_k_split(hg.make_plan(128, 4096, 4096)) == 4     # on 64x128 tiles
+    assert hg.mfma_k_split(hg.make_plan(128, 4096, 8192)) == 8     # on 128x128 tiles
     assert hg.mfma_k_split(hg.make_plan(128, 4096, 1024)) == 2     # slices of 512
     assert hg.mfma_k_split(hg.make_plan(128, 4096, 1152)) == 1     # 1152 = 9 x 128
 
@@ -312,7 +319,7 @@ def test_mfma_column_split_mirrors_the_native_choice():
     tiles and the partial tile column would add a round; the plan mirror
     names the same columns, remainder K split and workspace as the library."""
     from veritac_amd import _lib
-    cases = {(8192, 8208, 8192): (8192, 16, 4), (4096, 4112, 4096): (4096, 16, 8),
+    cases = {(8192, 8208, 8192): (8192, 16, 4), (4096, 4112, 4096): (4096, 16, 4),
              (4096, 4112, 1024): (4096, 16, 2), (2048, 4112, 1024): None,
              (8192, 8448, 8192): None, (8200, 8208, 8192): None}
     for (m, n, k), want in cases.items():
@@ -326,6 +333,40 @@ def test_mfma_column_split_mirrors_the_native_choice():
         assert (top["n"], rest["n"], hg.mfma_k_split(rest)) == want, (m, n, k)
         assert top["m"] == rest["m"] == m and rest["variant"] == "mfma_128x128"
         assert ws == 4 * want[2] * m * want[1], (m, n, k)
+        # the remainder's 128x128 workgroups, or 64x128 ones on a small grid
+        half = hg.mfma_half_tiles(rest)
         assert hg.required_resources(plan) == (
-            hg.DMA16_LDS, min((m // 256) * (want[0] // 256), 256) + (m // 128) * want[2])
+            hg.DMA16_LDS, min((m // 256) * (want[0] // 256), 256) +
+            (m // (64 if half else 128)) * want[2])
         assert "%d columns on the persistent 256x256 kernel" % want[0] in hg.native_check(plan)[1]
+
+
+def test_small_128x128_grids_run_64_row_tiles():
+    """mfma_128x128 with row-major B runs 64x128 tiles, with the K split those
+    tiles call for, when that gives at most 256 workgroups, each over at most
+    2048 of K (1024 per slice when K is split); packed B and other grids keep
+    128x128 tiles. The native library reports the same K split (vt_gemm_check)."""
+    from veritac_amd import _lib
+
+    def tiles(m, n, k, **kw):
+        plan = hg.make_plan(m, n, k, variant="mfma_128x128", **kw)
+        return hg.mfma_tile_shape(plan), hg.mfma_k_split(plan), hg.required_resources(plan)
+    half, full = (64, 128), (128, 128)
+    assert tiles(256, 256, 256, has_d=True, d_max_abs=1) == (half, 1, (36864, 8))
+    assert tiles(1024, 1024, 1024) == (half, 1, (36864, 128))      # 128x128: 2 K slices
+    assert tiles(1024, 1024, 2048) == (half, 1, (36864, 128))      # 128x128: 4 K slices
+    assert tiles(512, 512, 2048) == (half, 4, (36864, 128))
+    assert tiles(1024, 2048, 512) == (half, 1, (36864, 256))
+    assert tiles(1152, 2048, 512) == (full, 1, (49152, 144))       # 288 64x128 workgroups
+    assert tiles(2048, 2048, 512) == (full, 1, (49152, 256))
+    assert tiles(256, 4096, 4096) == (full, 4, (49152, 256))       # 64x128: K 4096 unsplit
+    assert tiles(128, 4096, 4096) == (half, 4, (36864, 256))       # 128x128: 8 slices
+    assert tiles(128, 4096, 8192) == (full, 8, (49152, 256))       # 64x128: 4 slices of 2048
+    assert tiles(512, 512, 256, batch=4) == (half, 1, (36864, 128))
+    assert tiles(512, 512, 256, batch=16, b_shared=True)[0] == full   # folded: 512 workgroups
+    for m, n, k in ((1024, 1024, 1024), (512, 512, 2048), (256, 4096, 4096), (384, 1024, 1024),
+                    (128, 4096, 4096), (128, 4096, 8192)):
+        _, _, v, ks, _ = _lib.gemm_check(m, n, k, k, n, n, n, variant="mfma_128x128")
+        assert max(ks, 1) == hg.mfma_k_split(hg.make_plan(m, n, k, variant="mfma_128x128"))
+    packed = hg._packed_parts(hg.make_plan(300, 1024, 1024, variant=hg.PACKED_VARIANT))[1]
+    assert packed["variant"] == "mfma_128x128" and hg.mfma_tile_shape(packed) == full

@@ -64,11 +64,11 @@ PAIRS = [
     ("padded", (1000, 1000, 1000, "auto", 0, True), (300, 500, 700, "padded", 0, False)),
     ("padded inner k-split", (16, 2047, 4095, "padded", 0, False), (5, 999, 1001, "padded", 0, True)),
     # whole 256-row tiles on the persistent kernel, the last 52 (40) rows on
-    # 128x128 tiles with K in 2 slices
+    # 64x128 tiles with K in 2 slices
     ("256x256 row split", (2100, 8192, 1024, "mfma_256x256", 0, True),
      (4136, 4096, 1024, "mfma_256x256", 0, False)),
     # whole 256-column tiles on the persistent kernel, the last 16 columns on
-    # 128x128 tiles with K in 8 (then 2) slices: 2 MiB, then 512 KiB of scratch
+    # 64x128 tiles with K in 4 (then 2) slices: 1 MiB, then 512 KiB of scratch
     ("256x256 column split", (4096, 4112, 4096, "mfma_256x256", 0, True),
      (4096, 4112, 1024, "mfma_256x256", 0, False)),
 ]

@@ -47,7 +47,8 @@
 //       registers, LDS double buffer, the A slice resident in LDS,
 //       v_mfma_i32_16x16x64_i8 over 1, 2 or 4 row blocks of 16 (M padded up).
 //       K slices write int32 partials to a workspace and skinny_reduce_kernel,
-//       next on the same stream, adds them (and D).
+//       next on the same stream, adds them (and D); up to 4 rows the kernel
+//       finishes them itself through one 64-bit word per output element.
 //   generic_kernel  any shape, stride or alignment; one thread per output,
 //       int32 VALU. Used where the vector kernels' alignment rules fail.
 //
@@ -2331,11 +2332,40 @@ Problem rows_from(const Problem &r, int64_t r0) {
 }
 
 // The K split vt_gemm_i8 launches for an MFMA variant (1 for the others).
+// The mfma_128x128 variant with row-major B runs 64x128 tiles (and the K
+// split those tiles call for) when that gives at most one workgroup per CU
+// over at most 2048 of K, or 1024 per slice when K is split: twice the 128x128
+// workgroups, or fewer K slices (often none, and no reduction launch), with
+// half the A rows and C per workgroup. On grids that small the workgroups'
+// loads are the critical path. HIP graph per launch, interleaved on one box,
+// 128x128 against 64x128 tiles: 256^3 + D 5.31 -> 4.10 us, 512^2 x 512
+// 5.27 -> 4.37, 300 x 208 x 160 6.14 -> 4.79, 1024^2 x 512 5.78 -> 5.13,
+// 1024^3 12.4 (two K slices) -> 6.2 (none), 1024^2 x 2048 15.6 (four) -> 11.5
+// (none), 256 x 4096 x 2048 13.3 -> 11.6, 256 x 2048 x 4096 13.6 -> 11.8,
+// 128 x 4096 x 4096 13.5 (eight slices) -> 12.9 (four), and the remainders
+// of split 256x256 launches 3-5 %. Outside the rule 64-row tiles lost:
+// 2048^2 x 512 (512 workgroups) 9 %, 1536^2 x 1024 (288) 12 %,
+// 256 x 4096 x 4096 (K 4096 unsplit) 25 %, 128 x 4096 x 8192 (four slices of
+// 2048 against eight of 1024) 7 %.
+constexpr int64_t kHalfTileMaxWgs = 256, kHalfTileMaxK = 2048, kHalfTileMaxSliceK = 1024;
+
+// r: the folded problem (mfma_fold).
+bool mfma_half_rows(const Problem &r) {
+  const int ks = mfma_k_split<64, 128>(r);
+  const int64_t wgs = (r.M + 63) / 64 * ((r.N + 127) / 128) * r.batch * ks;
+  return wgs <= kHalfTileMaxWgs && r.K / ks <= (ks > 1 ? kHalfTileMaxSliceK : kHalfTileMaxK);
+}
+
+// K slices of an mfma_128x128 launch with row-major B (r folded).
+int mfma128_split(const Problem &r) {
+  return mfma_half_rows(r) ? mfma_k_split<64, 128>(r) : mfma_k_split<128, 128>(r);
+}
+
 int mfma_split_for(const Problem &q, int32_t variant) {
   const Problem r = mfma_fold(q);
   switch (variant) {
     case VT_VARIANT_MFMA_256x256: return mfma_k_split<256, 256>(r);
-    case VT_VARIANT_MFMA_128x128: return mfma_k_split<128, 128>(r);
+    case VT_VARIANT_MFMA_128x128: return mfma128_split(r);
     case VT_VARIANT_MFMA_256x128: return mfma_k_split<256, 128>(r);
     default: return 1;
   }
@@ -2351,7 +2381,8 @@ bool packed_tiles_fit(const Problem &q) {
 template <int BM, int BN, bool PACKED = false>
 int launch_mfma_tiles(const Problem &r, hipStream_t stream, int num_cus);
 
-// PACKED: B is packed (r.B = Bp, r.ldb = kbt, r.sb = the packed batch stride).
+int launch_mfma128(const Problem &q, Scratch &scr);
+
 template <int BM, int BN, bool PACKED = false>
 int launch_mfma(const Problem &q, Scratch &scr) {
   const Problem r = mfma_fold(q);
@@ -2367,13 +2398,13 @@ int launch_mfma(const Problem &q, Scratch &scr) {
       Problem top = r;
       top.M = rows;
       if (int rc = launch_mfma_tiles<BM, BN, PACKED>(top, stream, num_cus)) return rc;
-      return launch_mfma<128, 128, false>(rows_from(r, rows), scr);
+      return launch_mfma128(rows_from(r, rows), scr);
     }
     if (const int64_t cols = ks == 1 ? mfma_split_cols(r) : 0) {
       Problem left = r;
       left.N = cols;
       if (int rc = launch_mfma_tiles<BM, BN, PACKED>(left, stream, num_cus)) return rc;
-      return launch_mfma<128, 128, false>(cols_from(r, cols), scr);
+      return launch_mfma128(cols_from(r, cols), scr);
     }
   }
   if (ks == 1) return launch_mfma_tiles<BM, BN, PACKED>(r, stream, num_cus);
@@ -2454,6 +2485,13 @@ int launch_mfma_tiles(const Problem &r, hipStream_t stream, int num_cus) {
   }
   VT_HIP_CHECK(hipGetLastError());
   return VT_OK;
+}
+
+// The mfma_128x128 variant with row-major B: 64x128 or 128x128 tiles
+// (mfma_half_rows).
+int launch_mfma128(const Problem &q, Scratch &scr) {
+  if (mfma_half_rows(mfma_fold(q))) return launch_mfma<64, 128>(q, scr);
+  return launch_mfma<128, 128>(q, scr);
 }
 
 // K slices of the skinny kernel: rows per slice (a multiple of the pipeline
@@ -2890,7 +2928,7 @@ int64_t scratch_need(const Problem &q, int32_t variant, int32_t k_split) {
     const int64_t cols = split && !rows ? mfma_split_cols(r) : 0;
     if (rows || cols) {   // the rows or columns after the persistent kernel's, on 128x128 tiles
       const Problem g = mfma_fold(rows ? rows_from(r, rows) : cols_from(r, cols));
-      const int ks2 = mfma_k_split<128, 128>(g);
+      const int ks2 = mfma128_split(g);
       return ks2 > 1 ? round256(ks2 * g.M * g.N * 4) : 0;
     }
     return ks > 1 ? round256(ks * r.M * r.N * 4) : 0;
@@ -2973,7 +3011,7 @@ int launch_generic(const Problem &q, hipStream_t stream) {
 int launch_vector(const Problem &q, int32_t variant, int32_t k_split, Scratch &scr) {
   switch (variant) {
     case VT_VARIANT_MFMA_256x256: return launch_mfma<256, 256>(q, scr);
-    case VT_VARIANT_MFMA_128x128: return launch_mfma<128, 128>(q, scr);
+    case VT_VARIANT_MFMA_128x128: return launch_mfma128(q, scr);
     case VT_VARIANT_MFMA_256x128: return launch_mfma<256, 128>(q, scr);
     case VT_VARIANT_SKINNY: return launch_skinny(q, k_split, scr);
     default: return fail(VT_EINVAL, "variant %d is not a vector variant", (int)variant);

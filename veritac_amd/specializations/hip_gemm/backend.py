@@ -73,6 +73,13 @@ PACKED_WAVES = 8
 # four 8 KiB epilogue strips. The 16x16x64 kernel runs K % 256 == 0.
 DMA_LDS = 4 * (256 * 64 + 64 * 256)
 DMA16_LDS = DMA_LDS + 4 * 8192
+# An mfma_128x128 launch with row-major B runs 64x128 tiles, with this LDS
+# per workgroup, when those tiles and the K split they call for give at most
+# MFMA_HALF_MAX_WGS workgroups, each over at most MFMA_HALF_MAX_K of K
+# (MFMA_HALF_MAX_SLICE_K per slice when K is split) (kHalfTile* in the HIP
+# source).
+MFMA_HALF_MAX_WGS, MFMA_HALF_MAX_K, MFMA_HALF_MAX_SLICE_K = 256, 2048, 1024
+HALF_TILE_LDS = 3 * (64 * 64 + 64 * 128)
 SKINNY_MAX_M = 64   # up to 4 row blocks of 16 (kSkinnyMaxM in the HIP source)
 # Up to this many rows vt_gemm_i8 finishes a K-split skinny launch inside the
 # kernel, through one 64-bit finishing word per output (kSkinnyFinMaxM)
@@ -180,19 +187,16 @@ def packed_split(plan):
     return -(-kbt // per), per
 
 
-def mfma_k_split(plan):
-    """K slices vt_gemm_i8 runs an MFMA plan in (mfma_k_split in the HIP
-    source): a k of at least 1024 over at most 64 tiles (contiguous shared-B
-    batches folded into m) is cut into up to 16 slices of whole 128-deep steps,
-    each at least 512 deep, for up to 256 workgroups; the partial sums are
-    added by a second kernel. 1: no split."""
-    variant = plan["variant"]
-    if not variant.startswith("mfma"):
-        return 1
-    tm, tn = TILES[variant][:2]
-    m, n, k, b = plan["m"], plan["n"], plan["k"], plan["batch"]
-    if plan["b_shared"] and b > 1:
-        m, b = m * b, 1
+def _folded(plan):
+    """(m, batch) with contiguous shared-B batches folded into m (mfma_fold)."""
+    m, b = plan["m"], plan["batch"]
+    return (m * b, 1) if plan["b_shared"] and b > 1 else (m, b)
+
+
+def _k_split_for_tiles(m, n, k, b, tm, tn):
+    """mfma_k_split<tm, tn> in the HIP source, on a folded problem: a k of at
+    least 1024 over at most 64 tiles is cut into up to 16 slices of whole
+    128-deep steps, each at least 512 deep, for up to 256 workgroups."""
     if b != 1 or k < 1024 or n % 16:
         return 1
     tiles = -(-m // tm) * -(-n // tn)
@@ -204,6 +208,20 @@ def mfma_k_split(plan):
     while ks > 1 and (k % (128 * ks) or k // ks < 512):
         ks //= 2
     return ks
+
+
+def mfma_k_split(plan):
+    """K slices vt_gemm_i8 runs an MFMA plan in (mfma_split_for in the HIP
+    source): a k of at least 1024 over at most 64 of the tiles the plan runs
+    (contiguous shared-B batches folded into m) is cut into up to 16 slices of
+    whole 128-deep steps, each at least 512 deep, for up to 256 workgroups;
+    the partial sums are added by a second kernel. 1: no split."""
+    variant = plan["variant"]
+    if not variant.startswith("mfma"):
+        return 1
+    tm, tn = mfma_tile_shape(plan)
+    m, b = _folded(plan)
+    return _k_split_for_tiles(m, plan["n"], plan["k"], b, tm, tn)
 
 
 def mfma_split_rows(plan):
@@ -309,7 +327,7 @@ def _packed_parts(plan):
             # after the 256-row tiles the batches are no longer contiguous
             # blocks of rows, so the library does not fold them into one GEMM
             rest = dict(rest, variant="mfma_128x128", k_split=0,
-                        b_shared=plan["b_shared"] and not rows)
+                        b_shared=plan["b_shared"] and not rows, packed_b=True)
     return dma, rest
 
 
@@ -320,10 +338,31 @@ def persistent_lds(k):
     return DMA16_LDS if k % 256 == 0 else DMA_LDS
 
 
+def mfma_half_tiles(plan):
+    """Whether an mfma_128x128 plan runs 64x128 tiles (mfma_half_rows in the
+    HIP source): row-major B, and 64x128 tiles with the K split they call for
+    give at most MFMA_HALF_MAX_WGS workgroups, each over at most
+    MFMA_HALF_MAX_K of K, or MFMA_HALF_MAX_SLICE_K per slice when K is split
+    (shared-B batches folded)."""
+    if plan["variant"] != "mfma_128x128" or plan.get("packed_b"):
+        return False
+    m, b = _folded(plan)
+    n, k = plan["n"], plan["k"]
+    ks = _k_split_for_tiles(m, n, k, b, 64, 128)
+    return (-(-m // 64) * -(-n // 128) * b * ks <= MFMA_HALF_MAX_WGS and
+            k // ks <= (MFMA_HALF_MAX_SLICE_K if ks > 1 else MFMA_HALF_MAX_K))
+
+
+def mfma_tile_shape(plan):
+    """(rows, columns) of the output tiles an MFMA plan's kernel runs."""
+    tm, tn = TILES[plan["variant"]][:2]
+    return (64 if mfma_half_tiles(plan) else tm), tn
+
+
 def mfma_tiles(plan):
     """Output tiles an MFMA plan runs, over every batch and K slice (shared-B
     batches folded into m); the persistent kernel walks them in rounds."""
-    tm, tn = TILES[plan["variant"]][:2]
+    tm, tn = mfma_tile_shape(plan)
     m, batch = plan["m"], plan["batch"]
     if plan["b_shared"] and batch > 1:
         m, batch = m * batch, 1
@@ -361,7 +400,7 @@ def required_resources(plan):
             return max(lds_t, lds_r), wgs_t + wgs_r
         if _runs_persistent(plan):
             return persistent_lds(plan["k"] // mfma_k_split(plan)), min(mfma_tiles(plan), NUM_CUS)
-        return lds, mfma_tiles(plan)
+        return (HALF_TILE_LDS if mfma_half_tiles(plan) else lds), mfma_tiles(plan)
     if variant == "skinny":
         ks, chunk = skinny_split(plan)
         return (lds + 16 * skinny_row_blocks(m) * skinny_a_stride(chunk),
@@ -519,7 +558,7 @@ def modeled_counts(plan):
     """Analytic ops / bytes / workgroups for a valid plan (a model, not a measurement)."""
     m, n, k, b = plan["m"], plan["n"], plan["k"], plan["batch"]
     variant = plan["variant"]
-    tm, tn = TILES[variant][:2]
+    tm, tn = mfma_tile_shape(plan) if variant.startswith("mfma") else TILES[variant][:2]
     lds, wgs = required_resources(plan)
     ops = 2 * b * m * n * k
     alg = algorithmic_bytes(plan)
@@ -622,7 +661,7 @@ def modeled_objective(plan, counts):
                 tp, wp = modeled_objective(part, modeled_counts(part))
                 t, wgs = t + tp, wgs + wp
             return t, wgs
-    tm, tn = TILES[variant][:2]
+    tm, tn = mfma_tile_shape(plan) if variant.startswith("mfma") else TILES[variant][:2]
     if variant.startswith("mfma") and plan["b_shared"] and b > 1:
         m, b = m * b, 1
     padded_ops = 2 * b * (-(-m // tm) * tm) * (-(-n // tn) * tn) * k
