@@ -115,11 +115,12 @@ extern "C" {
  *
  * Workspace: the skinny variant's K-split partial sums and the padded
  * variant's copies live in workspaces the library allocates per (device,
- * stream, kind). With a K split over at most 4 rows the skinny kernel
- * finishes the slices' sums itself, through one 8-byte finishing word per
- * output element in a workspace of its own kind that is zeroed when it is
- * allocated and that every call leaves zero (no second launch, and never
- * more bytes than the partial sums). A workspace only grows, and a
+ * stream, kind). With a K split over at most 16 rows the skinny kernel
+ * finishes the slices' sums itself (when the split's arrival count fits the
+ * word), through one 8-byte finishing word per two output elements in a
+ * workspace of its own kind that is zeroed when it is allocated and that
+ * every call leaves zero (no second launch, and never more bytes than the
+ * partial sums). A workspace only grows, and a
  * superseded one is kept (not freed) until the process ends, so a HIP graph
  * captured with an earlier workspace stays valid. Growth is refused while
  * the stream is being captured: a call that needs more workspace than its

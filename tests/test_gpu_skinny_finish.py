@@ -1,12 +1,13 @@
 """K-split decode sums finished inside the skinny kernel (needs a gfx950 GPU).
 
-Up to 4 rows, vt_gemm_i8 finishes the K slices of the skinny (decode) kernel
-in the kernel itself, through one 64-bit finishing word per output element
-that every launch leaves zero (tests/test_fin_word.py models the word). These
-tests call the C ABI and compare every output with the oracle: every row
-count that takes that path against the two-launch path's neighbours, D and in
-place, batches, repeated calls and HIP graph replays, so a word left nonzero
-by one launch would show in the next.
+Up to 16 rows, vt_gemm_i8 finishes the K slices of the skinny (decode) kernel
+in the kernel itself, through one 64-bit finishing word per two output
+elements that every launch leaves zero (tests/test_fin_word.py models the
+word). These tests call the C ABI and compare every output with the oracle:
+row counts that take that path (odd ones, whose last word holds one row)
+against the two-launch path's neighbours (17 rows, or a split whose count
+does not fit the word), D and in place, batches, repeated calls and HIP graph
+replays, so a word left nonzero by one launch would show in the next.
 """
 import numpy as np
 import pytest
@@ -73,11 +74,13 @@ def want(A, B, D):
     return np.stack([go.gemm_i8(A[i], B, None if D is None else D[i]) for i in range(A.shape[0])])
 
 
-@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8])
-@pytest.mark.parametrize("k_split", [2, 3, 7, 64])
+@pytest.mark.parametrize("m", [1, 2, 3, 5, 8, 13, 16, 17])
+@pytest.mark.parametrize("k_split", [2, 3, 7, 64, 65])
 def test_rows_and_splits(dev, m, k_split):
-    """1-4 rows finish in the kernel, 5 and 8 take the reduction launch;
-    N = 1040 leaves a partial last slab, K = 8256 a partial last slice."""
+    """1-16 rows finish in the kernel, 17 take the reduction launch, and so
+    does k_split 65 (65 slices of 128 rows: the count needs 7 bits beside two
+    29-bit fields); N = 1040 leaves a partial last slab, K = 8256 a partial
+    last slice."""
     rng = np.random.default_rng(100 * m + k_split)
     for with_d in (False, True):
         A, B, D = operands(rng, m, 1040, 8256, with_d)
@@ -91,7 +94,7 @@ def test_in_place_and_wrap(dev):
     """C = C + A.B in place, with C near both ends of int32 so that the
     finished sum wraps (the contract's mod 2^32 result)."""
     rng = np.random.default_rng(7)
-    m, n, k = 4, 2048, 4096
+    m, n, k = 5, 2048, 4096
     A, B, _ = operands(rng, m, n, k, False)
     for base in (2**31 - 5, -2**31 + 5):
         D = np.full((m, n), base, np.int32)
@@ -106,7 +109,7 @@ def test_in_place_and_wrap(dev):
 
 def test_batches_share_b(dev):
     rng = np.random.default_rng(8)
-    A, B, D = operands(rng, 2, 1024, 4096, True, batch=5)
+    A, B, D = operands(rng, 3, 1024, 4096, True, batch=5)
     say("finish batches")
     C = run(dev, A, B, D, 4)
     _lib.sync(None)
@@ -117,7 +120,8 @@ def test_repeated_calls_mixed_with_the_reduction_path(dev):
     """Finishing and two-launch calls in turn on one stream, each on new
     data: every result exact, so every launch left its words zero."""
     rng = np.random.default_rng(9)
-    for it, (m, ks) in enumerate(((1, 4), (16, 4), (3, 5), (1, 4), (8, 2), (4, 64), (2, 3))):
+    for it, (m, ks) in enumerate(((1, 4), (17, 4), (16, 4), (3, 5), (1, 4), (8, 2), (4, 64),
+                                  (33, 4), (2, 3), (11, 7))):
         A, B, D = operands(rng, m, 1536, 4096, it % 2 == 1)
         say("finish repeat", it, m, ks)
         C = run(dev, A, B, D, ks)
@@ -134,10 +138,10 @@ def test_graph_replays(dev):
     A, B, D = operands(rng, m, n, k, True)
     s = torch.cuda.Stream(device=dev)
     At, Bt, Dt = to_dev(dev, A, B, D)
-    A2, B2, _ = operands(rng, 16, 1024, 4096, False)
+    A2, B2, _ = operands(rng, 17, 1024, 4096, False)
     A2t, B2t, _ = to_dev(dev, A2, B2, None)
     C = torch.full((m, n), INT32_MIN, dtype=torch.int32, device=dev)
-    C2 = torch.full((16, 1024), INT32_MIN, dtype=torch.int32, device=dev)
+    C2 = torch.full((17, 1024), INT32_MIN, dtype=torch.int32, device=dev)
     torch.cuda.synchronize()
     launch(At, Bt, Dt, C, 0, stream=s.cuda_stream)
     s.synchronize()

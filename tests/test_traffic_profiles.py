@@ -54,7 +54,7 @@ def test_gemm_traffic_matches_its_profile():
 
 # (packed B, M) -> (summary, kernels of one step)
 DECODE = {
-    (False, 16): ("skinny_decode_m16_k4096_n14336.md", ("skinny_kernel", "skinny_reduce_kernel")),
+    (False, 16): ("skinny_decode_m16_k4096_n14336.md", ("skinny_kernel",)),
     (True, 16): ("skinny_packed_m16_k4096_n14336.md", ("packed_skinny_kernel",)),
     (False, 1): ("decode_m1_k4096_n14336.md", ("skinny_kernel",)),
     (True, 1): ("decode_m1_k4096_n14336.md", ("packed_skinny_kernel",)),

@@ -47,8 +47,8 @@
 //       registers, LDS double buffer, the A slice resident in LDS,
 //       v_mfma_i32_16x16x64_i8 over 1, 2 or 4 row blocks of 16 (M padded up).
 //       K slices write int32 partials to a workspace and skinny_reduce_kernel,
-//       next on the same stream, adds them (and D); up to 4 rows the kernel
-//       finishes them itself through one 64-bit word per output element.
+//       next on the same stream, adds them (and D); up to 16 rows the kernel
+//       finishes them itself through one 64-bit word per two output elements.
 //   generic_kernel  any shape, stride or alignment; one thread per output,
 //       int32 VALU. Used where the vector kernels' alignment rules fail.
 //
@@ -1289,15 +1289,21 @@ struct SkinnyArgs {
   int k_split;     // K slices per column slab (workgroups along K)
   int k_chunk;     // rows per slice, a multiple of the stage rows x U
   int32_t *ws;     // [batch][k_split][M][N] partials when k_split > 1
-  uint64_t *fin;   // [batch][M][N] finishing words (FIN), zero between launches
+  uint64_t *fin;   // [batch][(M + 1) / 2][N] finishing words (FIN), zero between launches
+  int fin_bits;    // FIN: width of each of the word's two sum fields
 };
 
-// Finishing word of a K-split output element finished in the kernel: each of
-// the k_split slices adds (1 << kFinCountShift) | partial, the partial as an
-// unsigned 32-bit value. Bits 0-31 then hold the slices' sum mod 2^32, bits
-// 32-47 its carries (fewer than k_split) and bits 48-63 the number of slices
-// that have added, so k_split must stay below 2^16 (the host checks).
-constexpr int kFinCountShift = 48;
+// Finishing word of two K-split output elements (rows 2i and 2i + 1 of one
+// column) finished in the kernel. A slice's partial over k_chunk rows of int8
+// products lies in [-16256 k_chunk, 16384 k_chunk] (a product lies in
+// [-128 * 127, (-128)^2]); biased by 16256 k_chunk it lies in
+// [0, 32640 k_chunk]. Each slice adds
+//   (1 << 2F) | (biased partial of row 2i + 1) << F | (biased partial of row 2i)
+// where F (fin_bits) is the bit length of 32640 k_chunk k_split: both fields
+// then stay below 2^F after every add, with no carry between them, and bits
+// 2F-63 count the slices that have added; the host needs k_split - 1 < 2^(64-2F).
+constexpr int kFinBiasPerRow = 16256;
+constexpr int kFinSpanPerRow = 16256 + 16384;
 
 // One workgroup = WAVES waves streams an NB-column slab of B over one K slice.
 // Every thread moves one 16-byte chunk per stage, so a stage is R = WAVES*1024/NB
@@ -1310,10 +1316,11 @@ constexpr int kFinCountShift = 48;
 // streamed once for up to 64 rows.
 // With a K split the slices' partial sums either go to the workspace for
 // skinny_reduce_kernel, or (FIN) are finished here: each slice adds its
-// partial into the element's finishing word with one agent-scope atomic add,
-// and the slice whose add returns k_split - 1 earlier arrivals holds the whole
-// sum (the low 32 bits of the returned word plus its own partial, mod 2^32).
-// It writes C (plus D) and swaps the word back to 0. Every step is a
+// partials of rows 2i and 2i + 1 (biased, in two fields) into their finishing
+// word with one agent-scope atomic add, and the slice whose add returns
+// k_split - 1 earlier arrivals holds both whole sums (each field of the
+// returned word plus its own biased partial, less k_split biases). It writes
+// both rows of C (plus D) and swaps the word back to 0. Every step is a
 // read-modify-write of that one word, so the word's single modification order
 // alone decides which slice is last and what it sees: no fence, no flag in
 // other memory, no second kernel.
@@ -1445,21 +1452,38 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(SkinnyArgs p) {
         }
       }
   } else if constexpr (FIN) {
-    uint64_t *fb = p.fin + (int64_t)bidx * M * N;
+    // Rows 2i and 2i + 1 share word i of the column: elements e = 0, 1 and
+    // e = 2, 3 of the lane.
+    const int fw = p.fin_bits;
+    const uint64_t field = (1ull << fw) - 1;
+    const int64_t bias = (int64_t)kFinBiasPerRow * p.k_chunk;
+    uint64_t *fb = p.fin + (int64_t)bidx * ((M + 1) >> 1) * N;
     const int32_t *Db = HAS_D ? p.D + bidx * p.sd : nullptr;
     int32_t *Cb = p.C + bidx * p.sc;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int row = g * 4 + e;
+    for (int h = 0; h < 2; ++h) {
+      const int row = g * 4 + 2 * h;
       if (row < M) {
-        uint64_t *word = fb + (int64_t)row * N + col;
-        const uint64_t old =
-            __hip_atomic_fetch_add(word, (1ull << kFinCountShift) | (uint32_t)acc[0][e],
-                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if ((int)(old >> kFinCountShift) == p.k_split - 1) {
-          int32_t v = add_wrap(acc[0][e], (int32_t)(uint32_t)old);
-          if (HAS_D) v = add_wrap(v, Db[(int64_t)row * p.ldd + col]);
-          Cb[(int64_t)row * p.ldc + col] = v;
+        // Rows past M hold zero partials (zero A rows), so a lone last row's
+        // neighbour field adds the bias alone.
+        const uint64_t lo = (uint64_t)((int64_t)acc[0][2 * h] + bias);
+        const uint64_t hi = (uint64_t)((int64_t)acc[0][2 * h + 1] + bias);
+        uint64_t *word = fb + (int64_t)(row >> 1) * N + col;
+        const uint64_t old = __hip_atomic_fetch_add(word, (1ull << (2 * fw)) | (hi << fw) | lo,
+                                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if ((old >> (2 * fw)) == (uint64_t)(p.k_split - 1)) {
+          // Each field now holds the sum of k_split biased partials, below
+          // 2^fw: the exact sum is that minus k_split biases.
+          const int64_t all_bias = bias * p.k_split;
+          const int64_t s0 = (int64_t)((old & field) + lo) - all_bias;
+          const int64_t s1 = (int64_t)(((old >> fw) & field) + hi) - all_bias;
+          int32_t v0 = (int32_t)s0, v1 = (int32_t)s1;
+          if (HAS_D) v0 = add_wrap(v0, Db[(int64_t)row * p.ldd + col]);
+          Cb[(int64_t)row * p.ldc + col] = v0;
+          if (row + 1 < M) {
+            if (HAS_D) v1 = add_wrap(v1, Db[(int64_t)(row + 1) * p.ldd + col]);
+            Cb[(int64_t)(row + 1) * p.ldc + col] = v1;
+          }
           __hip_atomic_exchange(word, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
       }
@@ -1902,12 +1926,16 @@ const VariantInfo kVariants[VT_VARIANT_COUNT] = {
 constexpr int kSkinnyNB = 256, kSkinnyWaves = 16, kSkinnyU = 2;
 // Rows the skinny kernel takes: up to 4 row blocks of 16.
 constexpr int kSkinnyMaxM = 64;
-// Up to this many rows a K-split skinny launch finishes its sums in the kernel
-// (skinny_kernel FIN) instead of a second launch: K = 4096, N = 14336, four
-// slices, HIP graph per step: M = 1 11.8 against 13.4 us, M = 2 12.4 against
-// 13.6, M = 4 13.7 against 14.0, M = 8 14.6 against 14.2 (one atomic per
-// element and slice; from 8 rows they cost more than the second launch).
-constexpr int kSkinnyFinMaxM = 4;
+// Up to this many rows (one row block) a K-split skinny launch finishes its
+// sums in the kernel (skinny_kernel FIN) instead of a second launch. K = 4096,
+// N = 14336, four slices, HIP graph of 120 steps over 10 input sets, three
+// interleaved rounds on one box, finishing against the second launch: M = 2
+// 11.93 against 12.39-12.46 us, M = 4 12.66-12.73 against 13.59-13.63, M = 8
+// 13.08-13.10 against 14.09-14.13, M = 12 13.43-13.49 against 14.40-14.46,
+// M = 16 14.10-14.12 against 14.70-14.78. With one word per element (one
+// atomic per element and slice) finishing had lost from 8 rows (M = 8 14.6,
+// M = 16 16.7 us); a word per two rows halves the atomics.
+constexpr int kSkinnyFinMaxM = 16;
 // Row blocks of 16 the skinny kernel is instantiated with for M rows.
 int skinny_row_blocks(int64_t M) { return M <= 16 ? 1 : M <= 32 ? 2 : 4; }
 // LDS for the replay's scratchpad and accumulator (plus the latched B tile).
@@ -2531,8 +2559,18 @@ void launch_skinny_kernel(bool has_d, dim3 grid, dim3 block, size_t lds, hipStre
 // a finishing-word count that fits, and a per-stream workspace (the fixed
 // scratch of vt_gemm_i8_noalloc is not kept zero, so those calls take the
 // second launch).
-bool skinny_finishes(int64_t M, int ks, const Scratch &scr) {
-  return ks > 1 && ks < (1 << 16) && M <= kSkinnyFinMaxM && !scr.fixed;
+// Field width of the finishing word for k_split slices of chunk rows (the bit
+// length of the largest sum of biased partials), or 0 when two such fields
+// leave no room for the count.
+int skinny_fin_bits(int ks, int64_t chunk) {
+  const uint64_t top = (uint64_t)ks * (uint64_t)chunk * (uint64_t)kFinSpanPerRow;
+  const int bits = 64 - __builtin_clzll(top);
+  const int count_bits = 64 - __builtin_clzll((uint64_t)(ks - 1));
+  return 2 * bits + count_bits <= 64 ? bits : 0;
+}
+
+bool skinny_finishes(int64_t M, int ks, int64_t chunk, const Scratch &scr) {
+  return ks > 1 && M <= kSkinnyFinMaxM && !scr.fixed && skinny_fin_bits(ks, chunk) > 0;
 }
 
 template <int NB, int WAVES, int U>
@@ -2552,14 +2590,16 @@ int launch_skinny_cfg(const Problem &q, int k_split, Scratch &scr) {
   a.k_chunk = (int)chunk;
   a.ws = nullptr;
   a.fin = nullptr;
+  a.fin_bits = 0;
   if ((int64_t)a.tiles_n * ks > 0x7fffffff || q.batch > 65535)
     return fail(VT_EUNSUPPORTED, "skinny grid too large");
-  const bool fin = skinny_finishes(q.M, ks, scr);
+  const bool fin = skinny_finishes(q.M, ks, chunk, scr);
   if (fin) {
     void *w = nullptr;
-    int rc = scr.take(kFinWords, (size_t)q.batch * q.M * q.N * sizeof(uint64_t), &w);
+    int rc = scr.take(kFinWords, (size_t)q.batch * ((q.M + 1) / 2) * q.N * sizeof(uint64_t), &w);
     if (rc) return rc;
     a.fin = (uint64_t *)w;
+    a.fin_bits = skinny_fin_bits(ks, chunk);
   } else if (ks > 1) {
     void *w = nullptr;
     const size_t pbytes = (size_t)q.batch * ks * q.M * q.N * sizeof(int32_t);

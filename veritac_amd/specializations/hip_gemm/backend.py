@@ -82,8 +82,11 @@ MFMA_HALF_MAX_WGS, MFMA_HALF_MAX_K, MFMA_HALF_MAX_SLICE_K = 256, 2048, 1024
 HALF_TILE_LDS = 3 * (64 * 64 + 64 * 128)
 SKINNY_MAX_M = 64   # up to 4 row blocks of 16 (kSkinnyMaxM in the HIP source)
 # Up to this many rows vt_gemm_i8 finishes a K-split skinny launch inside the
-# kernel, through one 64-bit finishing word per output (kSkinnyFinMaxM)
-SKINNY_FIN_MAX_M = 4
+# kernel, through one 64-bit finishing word per two outputs (kSkinnyFinMaxM)
+SKINNY_FIN_MAX_M = 16
+# A slice's biased partial lies in [0, FIN_SPAN_PER_ROW * k_chunk]
+# (kFinSpanPerRow: an int8 product lies in [-128 * 127, (-128)^2]).
+FIN_SPAN_PER_ROW = 16256 + 16384
 SKINNY_PIPE_ROWS = 64 * 2   # stage rows x stages in flight (kSkinny* in the HIP source)
 LDS_PER_CU = 160 * 1024
 
@@ -124,12 +127,22 @@ def skinny_split(plan):
     return -(-k // chunk), chunk
 
 
+def skinny_fin_bits(ks, chunk):
+    """Width of each of the two sum fields of a finishing word for ks slices
+    of chunk rows, or 0 when the arrival count no longer fits beside them
+    (skinny_fin_bits in the HIP source)."""
+    bits = (ks * chunk * FIN_SPAN_PER_ROW).bit_length()
+    return bits if 2 * bits + (ks - 1).bit_length() <= 64 else 0
+
+
 def skinny_finishes(plan):
     """Whether vt_gemm_i8 finishes this skinny plan's K slices inside the
     kernel (one launch) rather than in skinny_reduce_kernel (a second
-    launch): a K split over at most SKINNY_FIN_MAX_M rows (skinny_finishes in
-    the HIP source; vt_gemm_i8_noalloc always takes the second launch)."""
-    return skinny_split(plan)[0] > 1 and plan["m"] <= SKINNY_FIN_MAX_M
+    launch): a K split over at most SKINNY_FIN_MAX_M rows whose finishing
+    word fits (skinny_finishes in the HIP source; vt_gemm_i8_noalloc always
+    takes the second launch)."""
+    ks, chunk = skinny_split(plan)
+    return ks > 1 and plan["m"] <= SKINNY_FIN_MAX_M and skinny_fin_bits(ks, chunk) > 0
 
 
 def skinny_row_blocks(m):
@@ -576,8 +589,9 @@ def modeled_counts(plan):
     elif variant == "skinny":
         ks, _ = skinny_split(plan)
         # partial sums written and read back, or each slice's atomic add on
-        # an 8-byte finishing word (read and written where it is performed)
-        partial = (16 * b * m * n * ks if skinny_finishes(plan) else
+        # an 8-byte finishing word per two rows (read and written where it
+        # is performed)
+        partial = (16 * b * -(-m // 2) * n * ks if skinny_finishes(plan) else
                    2 * 4 * b * m * n * ks if ks > 1 else 0)
         l2_bytes = alg + partial + b * -(-n // tn) * 16 * k
     elif variant == PACKED_VARIANT:
