@@ -2555,20 +2555,21 @@ void launch_skinny_kernel(bool has_d, dim3 grid, dim3 block, size_t lds, hipStre
   else hipLaunchKernelGGL((skinny_kernel<NB, WAVES, U, MB, false, FIN>), grid, block, lds, s, a);
 }
 
-// Whether a K-split skinny launch finishes its sums in the kernel: few rows,
-// a finishing-word count that fits, and a per-stream workspace (the fixed
-// scratch of vt_gemm_i8_noalloc is not kept zero, so those calls take the
-// second launch).
 // Field width of the finishing word for k_split slices of chunk rows (the bit
 // length of the largest sum of biased partials), or 0 when two such fields
-// leave no room for the count.
+// leave no room for the count (or there is no split).
 int skinny_fin_bits(int ks, int64_t chunk) {
+  if (ks < 2 || chunk < 1) return 0;
   const uint64_t top = (uint64_t)ks * (uint64_t)chunk * (uint64_t)kFinSpanPerRow;
   const int bits = 64 - __builtin_clzll(top);
   const int count_bits = 64 - __builtin_clzll((uint64_t)(ks - 1));
   return 2 * bits + count_bits <= 64 ? bits : 0;
 }
 
+// Whether a K-split skinny launch finishes its sums in the kernel: few rows,
+// a finishing-word count that fits, and a per-stream workspace (the fixed
+// scratch of vt_gemm_i8_noalloc is not kept zero, so those calls take the
+// second launch).
 bool skinny_finishes(int64_t M, int ks, int64_t chunk, const Scratch &scr) {
   return ks > 1 && M <= kSkinnyFinMaxM && !scr.fixed && skinny_fin_bits(ks, chunk) > 0;
 }
