@@ -65,7 +65,8 @@ extern "C" {
                                       v_mfma_i32_32x32x32_i8; 64x128 tiles
                                       with row-major B when that gives at
                                       most 256 workgroups over at most 2048
-                                      of K (1024 per K slice)                 */
+                                      of K (1024 per K slice), 64x64 tiles
+                                      when those do as well                   */
 #define VT_VARIANT_SKINNY 3        /* M <= 64 decode shapes: B streamed once,
                                       v_mfma_i32_16x16x64_i8, K split         */
 #define VT_VARIANT_GENERIC 4       /* any shape/stride/alignment, VALU        */

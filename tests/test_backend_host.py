@@ -220,33 +220,32 @@ def test_mfma_k_split_mirrors_the_native_choice():
     from veritac_amd import _lib
     for m, n, k in [(128, 14336, 4096), (96, 14336, 4096), (128, 4096, 4096), (256, 4096, 4096),
                     (512, 4096, 4096), (8192, 8192, 8192), (1024, 14336, 4096), (300, 208, 160),
-                    (128, 4096, 1024), (128, 4096, 1152), (100, 256, 65536)]:
+                    (128, 4096, 1024), (128, 4096, 1152), (100, 256, 65536), (96, 2048, 1024),
+                    (256, 256, 8192)]:
         plan = hg.make_plan(m, n, k)
         _, _, variant, ks, ws = _lib.gemm_check(m, n, k, k, n, n, n)
         assert plan["variant"] == variant
         want = ks if ks > 1 else 1
         assert hg.mfma_k_split(plan) == want, (m, n, k)
         if variant.startswith("mfma"):
-            tm, tn = hg.TILES[variant][:2]
-            # small mfma_128x128 grids run 64x128 tiles (pinned by
-            # test_small_128x128_grids_run_64_row_tiles)
-            half = hg.mfma_half_tiles(plan)
-            if half:
-                tm = 64
+            # small mfma_128x128 grids run 64x128 or 64x64 tiles (pinned by
+            # test_small_128x128_grids_run_smaller_tiles)
+            tm, tn = hg.mfma_tile_shape(plan)
             tiles = -(-m // tm) * -(-n // tn) * want
             assert hg.mfma_tiles(plan) == tiles
             persistent = variant == "mfma_256x256" and m >= 256 and n >= 256 and \
                 (k // want) % 64 == 0
             # the persistent kernel: one workgroup per CU, 160 KiB (K slice % 256
             # == 0) or 128 KiB of LDS; the tile kernel: a workgroup per tile
-            lds = 3 * (64 * 64 + 64 * 128) if half else hg.TILES[variant][4]
+            lds = 3 * (tm * 64 + 64 * tn) if tm == 64 else hg.TILES[variant][4]
             assert hg.required_resources(plan) == (
                 (hg.DMA16_LDS if (k // want) % 256 == 0 else hg.DMA_LDS, min(tiles, 256))
                 if persistent else (lds, tiles)), (m, n, k)
             assert ws == (want * m * n * 4 if want > 1 else 0)
     assert hg.mfma_k_split(hg.make_plan(128, 4096, 4096)) == 4     # on 64x128 tiles
     assert hg.mfma_k_split(hg.make_plan(128, 4096, 8192)) == 8     # on 128x128 tiles
-    assert hg.mfma_k_split(hg.make_plan(128, 4096, 1024)) == 2     # slices of 512
+    assert hg.mfma_k_split(hg.make_plan(128, 4096, 1024)) == 1     # 128 64x64 workgroups
+    assert hg.mfma_k_split(hg.make_plan(96, 2048, 1024)) == 2      # slices of 512
     assert hg.mfma_k_split(hg.make_plan(128, 4096, 1152)) == 1     # 1152 = 9 x 128
 
 
@@ -259,7 +258,8 @@ def test_mfma_row_split_mirrors_the_native_choice():
     from veritac_amd import _lib
     cases = {
         (1100, 14336, 4096, 1): (1024, 76, 1),     # 224 + 56 tiles: 1 round -> 2
-        (2100, 8192, 1024, 1): (2048, 52, 2),      # 256 + 32; 52 rows on 64 tiles, K in 2
+        (2100, 8192, 1024, 1): (2048, 52, 1),      # 256 + 32; 52 rows on 128 64x64 tiles
+        (4136, 4096, 1024, 1): (4096, 40, 2),      # 256 + 16; 40 rows on 64 64x64 tiles, K in 2
         (100, 14336, 4096, 11): (1024, 76, 1),     # 11 shared-B batches folded to 1100 rows
         (8000, 8192, 8192, 1): None,               # 992 and 1024 tiles: 4 rounds either way
         (2000, 8192, 4096, 1): None,               # 224 and 256: one round
@@ -282,7 +282,8 @@ def test_mfma_row_split_mirrors_the_native_choice():
         assert (top["m"], rest["m"], hg.mfma_k_split(rest)) == want, (m, n, k)
         assert rest["variant"] == "mfma_128x128" and top["batch"] == rest["batch"] == 1
         assert ws == (4 * want[2] * want[1] * n if want[2] > 1 else 0), (m, n, k)
-        wgs = min(top["m"] // 256 * (n // 256), 256) + -(-rest["m"] // 128) * (n // 128) * want[2]
+        rows, cols = hg.mfma_tile_shape(rest)
+        wgs = min(top["m"] // 256 * (n // 256), 256) + -(-rest["m"] // rows) * -(-n // cols) * want[2]
         assert hg.required_resources(plan) == (hg.persistent_lds(k), wgs)
         assert "%d rows on the persistent 256x256 kernel" % top["m"] in hg.native_check(plan)[1]
         # both launches priced, the first at whole tiles only
@@ -333,39 +334,44 @@ def test_mfma_column_split_mirrors_the_native_choice():
         assert (top["n"], rest["n"], hg.mfma_k_split(rest)) == want, (m, n, k)
         assert top["m"] == rest["m"] == m and rest["variant"] == "mfma_128x128"
         assert ws == 4 * want[2] * m * want[1], (m, n, k)
-        # the remainder's 128x128 workgroups, or 64x128 ones on a small grid
-        half = hg.mfma_half_tiles(rest)
+        # the remainder's 128x128 workgroups, or 64-row ones on a small grid
+        # (16 columns: one tile column whatever its width)
+        rows = hg.mfma_tile_shape(rest)[0]
         assert hg.required_resources(plan) == (
-            hg.DMA16_LDS, min((m // 256) * (want[0] // 256), 256) +
-            (m // (64 if half else 128)) * want[2])
+            hg.DMA16_LDS, min((m // 256) * (want[0] // 256), 256) + (m // rows) * want[2])
         assert "%d columns on the persistent 256x256 kernel" % want[0] in hg.native_check(plan)[1]
 
 
-def test_small_128x128_grids_run_64_row_tiles():
+def test_small_128x128_grids_run_smaller_tiles():
     """mfma_128x128 with row-major B runs 64x128 tiles, with the K split those
     tiles call for, when that gives at most 256 workgroups, each over at most
-    2048 of K (1024 per slice when K is split); packed B and other grids keep
+    2048 of K (1024 per slice when K is split), and 64x64 tiles when they, with
+    their own K split, meet the same bounds; packed B and other grids keep
     128x128 tiles. The native library reports the same K split (vt_gemm_check)."""
     from veritac_amd import _lib
 
     def tiles(m, n, k, **kw):
         plan = hg.make_plan(m, n, k, variant="mfma_128x128", **kw)
         return hg.mfma_tile_shape(plan), hg.mfma_k_split(plan), hg.required_resources(plan)
-    half, full = (64, 128), (128, 128)
-    assert tiles(256, 256, 256, has_d=True, d_max_abs=1) == (half, 1, (36864, 8))
-    assert tiles(1024, 1024, 1024) == (half, 1, (36864, 128))      # 128x128: 2 K slices
-    assert tiles(1024, 1024, 2048) == (half, 1, (36864, 128))      # 128x128: 4 K slices
-    assert tiles(512, 512, 2048) == (half, 4, (36864, 128))
-    assert tiles(1024, 2048, 512) == (half, 1, (36864, 256))
-    assert tiles(1152, 2048, 512) == (full, 1, (49152, 144))       # 288 64x128 workgroups
-    assert tiles(2048, 2048, 512) == (full, 1, (49152, 256))
-    assert tiles(256, 4096, 4096) == (full, 4, (49152, 256))       # 64x128: K 4096 unsplit
-    assert tiles(128, 4096, 4096) == (half, 4, (36864, 256))       # 128x128: 8 slices
-    assert tiles(128, 4096, 8192) == (full, 8, (49152, 256))       # 64x128: 4 slices of 2048
-    assert tiles(512, 512, 256, batch=4) == (half, 1, (36864, 128))
+    quarter, half, full = (64, 64), (64, 128), (128, 128)
+    q_lds, h_lds, f_lds = 3 * (64 * 64 + 64 * 64), 3 * (64 * 64 + 64 * 128), 3 * (128 * 64 + 64 * 128)
+    assert (q_lds, h_lds) == (hg.QUARTER_TILE_LDS, hg.HALF_TILE_LDS)
+    assert tiles(256, 256, 256, has_d=True, d_max_abs=1) == (quarter, 1, (q_lds, 16))
+    assert tiles(1024, 1024, 1024) == (quarter, 1, (q_lds, 256))
+    assert tiles(1024, 1024, 2048) == (quarter, 1, (q_lds, 256))
+    assert tiles(512, 512, 2048) == (quarter, 4, (q_lds, 256))      # 64 tiles in 4 K slices
+    assert tiles(1024, 2048, 512) == (half, 1, (h_lds, 256))        # 512 64x64 workgroups
+    assert tiles(128, 4096, 4096) == (half, 4, (h_lds, 256))        # 64x64: K 4096 unsplit
+    assert tiles(128, 1024, 16384) == (half, 16, (h_lds, 256))      # 64x64: 8 slices of 2048
+    assert tiles(1152, 2048, 512) == (full, 1, (f_lds, 144))        # 288 64x128 workgroups
+    assert tiles(2048, 2048, 512) == (full, 1, (f_lds, 256))
+    assert tiles(256, 4096, 4096) == (full, 4, (f_lds, 256))        # 64x128: K 4096 unsplit
+    assert tiles(128, 4096, 8192) == (full, 8, (f_lds, 256))        # 64x128: 4 slices of 2048
+    assert tiles(512, 512, 256, batch=4) == (quarter, 1, (q_lds, 256))
+    assert tiles(512, 512, 256, batch=8) == (half, 1, (h_lds, 256))
     assert tiles(512, 512, 256, batch=16, b_shared=True)[0] == full   # folded: 512 workgroups
     for m, n, k in ((1024, 1024, 1024), (512, 512, 2048), (256, 4096, 4096), (384, 1024, 1024),
-                    (128, 4096, 4096), (128, 4096, 8192)):
+                    (128, 4096, 4096), (128, 4096, 8192), (128, 1024, 16384), (256, 256, 8192)):
         _, _, v, ks, _ = _lib.gemm_check(m, n, k, k, n, n, n, variant="mfma_128x128")
         assert max(ks, 1) == hg.mfma_k_split(hg.make_plan(m, n, k, variant="mfma_128x128"))
     packed = hg._packed_parts(hg.make_plan(300, 1024, 1024, variant=hg.PACKED_VARIANT))[1]

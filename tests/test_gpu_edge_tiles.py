@@ -123,7 +123,8 @@ def test_batches_with_ragged_rows(dev, shared):
 
 @pytest.mark.parametrize("m,n,k,rest_split", [
     (1100, 14336, 256, 1),    # 224 whole tiles + 56 partial: the split saves a round
-    (2100, 8192, 1024, 2),    # 256 + 32: the remaining 52 rows run with K in 2 slices
+    (2100, 8192, 1024, 1),    # 256 + 32: the remaining 52 rows on 64x64 tiles, K unsplit
+    (4136, 4096, 1024, 2),    # 256 + 16: the remaining 40 rows on 64x64 tiles, K in 2 slices
 ])
 def test_split_when_the_partial_row_adds_a_round(dev, m, n, k, rest_split):
     plan = hg.make_plan(m, n, k, has_d=True, d_max_abs=2**30, variant="mfma_256x256")
@@ -227,8 +228,9 @@ def test_padded_pitches_on_moved_back_tiles(dev, k):
 
 def test_column_split_when_the_partial_column_adds_a_round(dev):
     """4096 x 4112 x 1024: 256 whole tiles plus 16 partial ones, so the whole
-    4096 columns run on the persistent kernel and the last 16 on 128x128 tiles
-    with K in 2 slices, out of place and in place."""
+    4096 columns run on the persistent kernel and the last 16 on the 128x128
+    variant (its 64x64 tiles on a grid this small) with K in 2 slices, out of
+    place and in place."""
     m, n, k = 4096, 4112, 1024
     plan = hg.make_plan(m, n, k, has_d=True, d_max_abs=2**20, variant="mfma_256x256")
     top, rest = hg._mfma_parts(plan)

@@ -68,7 +68,7 @@ def test_model_linear_is_conflict_free_and_old_a_swizzle_is_not():
     assert conflicts([old(l & 31, l >> 5) for l in range(64)], 16) == 1
 
 
-@pytest.mark.parametrize("wtm", [64, 128])
+@pytest.mark.parametrize("wtm", [32, 64, 128])
 def test_a_fragment_reads_conflict_free(wtm):
     """32x32x32 A operand: lane l reads row l % 32, k chunk ks*2 + l / 32."""
     for wm in (0, 1):
@@ -78,7 +78,7 @@ def test_a_fragment_reads_conflict_free(wtm):
                 assert conflicts(addrs, 16) == 0
 
 
-@pytest.mark.parametrize("bn", [128, 256])
+@pytest.mark.parametrize("bn", [64, 128, 256])
 def test_b_fragment_reads_conflict_free(bn):
     """ds_read_b64_tr_b8: 16-lane group g reads rows (g>>1)*16 + j/2, chunk nc + (g&1)."""
     chunks = bn // 16
@@ -95,7 +95,7 @@ def test_b_fragment_reads_conflict_free(bn):
                     assert conflicts(addrs, 8) == 0
 
 
-@pytest.mark.parametrize("bn", [128, 256])
+@pytest.mark.parametrize("bn", [64, 128, 256])
 def test_vgpr_staged_writes_conflict_free(bn):
     """gemm_mfma_kernel: thread t stores A row t/4 chunk t%4 and B row t/chunks."""
     chunks = bn // 16

@@ -63,12 +63,12 @@ PAIRS = [
     ("decode explicit split", (16, 4096, 8192, "skinny", 16, True), (1, 1024, 2048, "skinny", 3, False)),
     ("padded", (1000, 1000, 1000, "auto", 0, True), (300, 500, 700, "padded", 0, False)),
     ("padded inner k-split", (16, 2047, 4095, "padded", 0, False), (5, 999, 1001, "padded", 0, True)),
-    # whole 256-row tiles on the persistent kernel, the last 52 (40) rows on
-    # 64x128 tiles with K in 2 slices
-    ("256x256 row split", (2100, 8192, 1024, "mfma_256x256", 0, True),
-     (4136, 4096, 1024, "mfma_256x256", 0, False)),
+    # whole 256-row tiles on the persistent kernel, the last 40 (52) rows on
+    # 64x64 tiles with K in 2 slices: 1.25 MiB, then 832 KiB of scratch
+    ("256x256 row split", (4136, 4096, 1024, "mfma_256x256", 0, True),
+     (8244, 2048, 1024, "mfma_256x256", 0, False)),
     # whole 256-column tiles on the persistent kernel, the last 16 columns on
-    # 64x128 tiles with K in 4 (then 2) slices: 1 MiB, then 512 KiB of scratch
+    # 64x64 tiles with K in 4 (then 2) slices: 1 MiB, then 512 KiB of scratch
     ("256x256 column split", (4096, 4112, 4096, "mfma_256x256", 0, True),
      (4096, 4112, 1024, "mfma_256x256", 0, False)),
 ]

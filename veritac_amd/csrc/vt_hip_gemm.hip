@@ -257,7 +257,7 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma_kernel(GemmArgs p) {
   constexpr int CA = BM * (BK / 16) / 256;    // A chunks per thread per slice
   constexpr int CB = BK * BCH / 256;          // B chunks per thread per slice
   constexpr int A_BYTES = BM * BK, B_BYTES = BK * BN;
-  static_assert(CA >= 1 && CB >= 1 && BCH >= 8, "tile too small");
+  static_assert(CA >= 1 && CB >= 1 && BCH >= 4, "tile too small");
 
   constexpr int NBUF = 3;                     // LDS slice buffers
   __shared__ __attribute__((aligned(16))) int8_t smem[NBUF * (A_BYTES + B_BYTES)];
@@ -2384,8 +2384,30 @@ bool mfma_half_rows(const Problem &r) {
   return wgs <= kHalfTileMaxWgs && r.K / ks <= (ks > 1 ? kHalfTileMaxSliceK : kHalfTileMaxK);
 }
 
+// Within that rule, 64x64 tiles (one 32x32 block per wave) when they too,
+// with their own K split, give at most one workgroup per CU over at most 2048
+// of K (1024 per slice when split): half of each workgroup's B panel and C
+// again. Interleaved on one box, HIP graph per launch, 64x128 against 64x64
+// tiles: 256^3 + D (config 2) 4.14-4.15 -> 3.36-3.37 us, 512^3 4.35 -> 3.61,
+// 300 x 208 x 160 4.80-4.85 -> 3.75, 192^3 4.77 -> 3.72, 128^3 + D 3.17 ->
+// 2.64, 1024^2 x 512 4.62 -> 4.07, 1024^3 6.20 -> 5.43, 1024^2 x 2048 11.63
+// -> 10.96, 512^2 x 2048 + D 8.6-8.9 -> 8.08, 256 x 4096 x 2048 11.6 ->
+// 11.06, 128 x 4096 x 1152 6.28 -> 5.31, 256^2 x 8192 + D 8.9 -> 8.5,
+// 512^2 x 256 3.61 -> 3.00, 256 x 512 x 1024 + D 7.23 -> 6.56,
+// 256 x 1024 x 4096 (eight K slices -> four) 10.87 -> 9.74, 128 x 256 x 8192
+// 8.32 -> 7.62, 96 x 2048 x 2048 8.79 -> 8.0, 100 x 208 x 2048 + D 7.36 ->
+// 6.42; the shapes outside the rule (128 x 4096 x 4096, 96 x 4096 x 4096,
+// 128 x 1024 x 16384) measured the same in both builds.
+bool mfma_quarter_tiles(const Problem &r) {
+  if (!mfma_half_rows(r)) return false;
+  const int ks = mfma_k_split<64, 64>(r);
+  const int64_t wgs = (r.M + 63) / 64 * ((r.N + 63) / 64) * r.batch * ks;
+  return wgs <= kHalfTileMaxWgs && r.K / ks <= (ks > 1 ? kHalfTileMaxSliceK : kHalfTileMaxK);
+}
+
 // K slices of an mfma_128x128 launch with row-major B (r folded).
 int mfma128_split(const Problem &r) {
+  if (mfma_quarter_tiles(r)) return mfma_k_split<64, 64>(r);
   return mfma_half_rows(r) ? mfma_k_split<64, 128>(r) : mfma_k_split<128, 128>(r);
 }
 
@@ -2515,9 +2537,10 @@ int launch_mfma_tiles(const Problem &r, hipStream_t stream, int num_cus) {
   return VT_OK;
 }
 
-// The mfma_128x128 variant with row-major B: 64x128 or 128x128 tiles
-// (mfma_half_rows).
+// The mfma_128x128 variant with row-major B: 64x64, 64x128 or 128x128 tiles
+// (mfma_quarter_tiles, mfma_half_rows).
 int launch_mfma128(const Problem &q, Scratch &scr) {
+  if (mfma_quarter_tiles(mfma_fold(q))) return launch_mfma<64, 64>(q, scr);
   if (mfma_half_rows(mfma_fold(q))) return launch_mfma<64, 128>(q, scr);
   return launch_mfma<128, 128>(q, scr);
 }

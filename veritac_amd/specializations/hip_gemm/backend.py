@@ -80,6 +80,7 @@ DMA16_LDS = DMA_LDS + 4 * 8192
 # source).
 MFMA_HALF_MAX_WGS, MFMA_HALF_MAX_K, MFMA_HALF_MAX_SLICE_K = 256, 2048, 1024
 HALF_TILE_LDS = 3 * (64 * 64 + 64 * 128)
+QUARTER_TILE_LDS = 3 * (64 * 64 + 64 * 64)
 SKINNY_MAX_M = 64   # up to 4 row blocks of 16 (kSkinnyMaxM in the HIP source)
 # Up to this many rows vt_gemm_i8 finishes a K-split skinny launch inside the
 # kernel, through one 64-bit finishing word per two outputs (kSkinnyFinMaxM)
@@ -366,9 +367,25 @@ def mfma_half_tiles(plan):
             k // ks <= (MFMA_HALF_MAX_SLICE_K if ks > 1 else MFMA_HALF_MAX_K))
 
 
+def mfma_quarter_tiles(plan):
+    """Whether an mfma_128x128 plan runs 64x64 tiles (mfma_quarter_tiles in
+    the HIP source): it runs 64x128 tiles, and 64x64 tiles with their own K
+    split also give at most MFMA_HALF_MAX_WGS workgroups, each over at most
+    MFMA_HALF_MAX_K of K (MFMA_HALF_MAX_SLICE_K per slice when split)."""
+    if not mfma_half_tiles(plan):
+        return False
+    m, b = _folded(plan)
+    n, k = plan["n"], plan["k"]
+    ks = _k_split_for_tiles(m, n, k, b, 64, 64)
+    return (-(-m // 64) * -(-n // 64) * b * ks <= MFMA_HALF_MAX_WGS and
+            k // ks <= (MFMA_HALF_MAX_SLICE_K if ks > 1 else MFMA_HALF_MAX_K))
+
+
 def mfma_tile_shape(plan):
     """(rows, columns) of the output tiles an MFMA plan's kernel runs."""
     tm, tn = TILES[plan["variant"]][:2]
+    if mfma_quarter_tiles(plan):
+        return 64, 64
     return (64 if mfma_half_tiles(plan) else tm), tn
 
 
@@ -413,7 +430,9 @@ def required_resources(plan):
             return max(lds_t, lds_r), wgs_t + wgs_r
         if _runs_persistent(plan):
             return persistent_lds(plan["k"] // mfma_k_split(plan)), min(mfma_tiles(plan), NUM_CUS)
-        return (HALF_TILE_LDS if mfma_half_tiles(plan) else lds), mfma_tiles(plan)
+        shape = mfma_tile_shape(plan)
+        return ({(64, 64): QUARTER_TILE_LDS, (64, 128): HALF_TILE_LDS}.get(shape, lds),
+                mfma_tiles(plan))
     if variant == "skinny":
         ks, chunk = skinny_split(plan)
         return (lds + 16 * skinny_row_blocks(m) * skinny_a_stride(chunk),
