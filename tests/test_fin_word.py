@@ -8,7 +8,7 @@ slice adds (1 << 2F) | hi << F | lo with one atomic add, F being the bit
 length of 32640 k_chunk k_split, and the slice whose add returns k_split - 1
 earlier arrivals (bits 2F-63) holds both exact sums: each field plus its own
 biased partial, less k_split biases. It writes C = D + sum (mod 2^32) for
-both rows and swaps the word back to 0.
+both rows and stores 0 back into the word.
 
 This CPU model checks that arithmetic: for every arrival order that matters
 the last arrival, and only it, sees the count k_split - 1; both sums are
@@ -52,7 +52,7 @@ def finish(p0, p1, chunk, order, bits=None, count_shift=None, bias=BIAS):
         if (old >> cs) == ks - 1:
             lasts += 1
             out = ((old & field) + lo - ks * b, ((old >> F) & field) + hi - ks * b)
-            word = 0                       # the last slice's swap
+            word = 0                       # the last slice's reset
     return out, word, lasts
 
 

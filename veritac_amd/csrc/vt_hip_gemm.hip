@@ -1320,7 +1320,7 @@ constexpr int kFinSpanPerRow = 16256 + 16384;
 // word with one agent-scope atomic add, and the slice whose add returns
 // k_split - 1 earlier arrivals holds both whole sums (each field of the
 // returned word plus its own biased partial, less k_split biases). It writes
-// both rows of C (plus D) and swaps the word back to 0. Every step is a
+// both rows of C (plus D) and stores 0 back into the word. Every step is a
 // read-modify-write of that one word, so the word's single modification order
 // alone decides which slice is last and what it sees: no fence, no flag in
 // other memory, no second kernel.
@@ -1460,33 +1460,55 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(SkinnyArgs p) {
     uint64_t *fb = p.fin + (int64_t)bidx * ((M + 1) >> 1) * N;
     const int32_t *Db = HAS_D ? p.D + bidx * p.sd : nullptr;
     int32_t *Cb = p.C + bidx * p.sc;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    auto add = [&](int h) {
       const int row = g * 4 + 2 * h;
-      if (row < M) {
-        // Rows past M hold zero partials (zero A rows), so a lone last row's
-        // neighbour field adds the bias alone.
-        const uint64_t lo = (uint64_t)((int64_t)acc[0][2 * h] + bias);
-        const uint64_t hi = (uint64_t)((int64_t)acc[0][2 * h + 1] + bias);
-        uint64_t *word = fb + (int64_t)(row >> 1) * N + col;
-        const uint64_t old = __hip_atomic_fetch_add(word, (1ull << (2 * fw)) | (hi << fw) | lo,
-                                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if ((old >> (2 * fw)) == (uint64_t)(p.k_split - 1)) {
-          // Each field now holds the sum of k_split biased partials, below
-          // 2^fw: the exact sum is that minus k_split biases.
-          const int64_t all_bias = bias * p.k_split;
-          const int64_t s0 = (int64_t)((old & field) + lo) - all_bias;
-          const int64_t s1 = (int64_t)(((old >> fw) & field) + hi) - all_bias;
-          int32_t v0 = (int32_t)s0, v1 = (int32_t)s1;
-          if (HAS_D) v0 = add_wrap(v0, Db[(int64_t)row * p.ldd + col]);
-          Cb[(int64_t)row * p.ldc + col] = v0;
-          if (row + 1 < M) {
-            if (HAS_D) v1 = add_wrap(v1, Db[(int64_t)(row + 1) * p.ldd + col]);
-            Cb[(int64_t)(row + 1) * p.ldc + col] = v1;
-          }
-          __hip_atomic_exchange(word, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+      // Rows past M hold zero partials (zero A rows), so a lone last row's
+      // neighbour field adds the bias alone.
+      const uint64_t lo = (uint64_t)((int64_t)acc[0][2 * h] + bias);
+      const uint64_t hi = (uint64_t)((int64_t)acc[0][2 * h + 1] + bias);
+      return __hip_atomic_fetch_add(fb + (int64_t)(row >> 1) * N + col,
+                                    (1ull << (2 * fw)) | (hi << fw) | lo,
+                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+    auto finish = [&](int h, uint64_t old) {
+      const int row = g * 4 + 2 * h;
+      if ((old >> (2 * fw)) != (uint64_t)(p.k_split - 1)) return;
+      // Each field now holds the sum of k_split biased partials, below 2^fw:
+      // the exact sum is that minus k_split biases.
+      const int64_t all_bias = bias * p.k_split;
+      const int64_t own0 = acc[0][2 * h], own1 = acc[0][2 * h + 1];
+      int32_t v0 = (int32_t)((int64_t)(old & field) + own0 + bias - all_bias);
+      int32_t v1 = (int32_t)((int64_t)((old >> fw) & field) + own1 + bias - all_bias);
+      if (HAS_D) v0 = add_wrap(v0, Db[(int64_t)row * p.ldd + col]);
+      Cb[(int64_t)row * p.ldc + col] = v0;
+      if (row + 1 < M) {
+        if (HAS_D) v1 = add_wrap(v1, Db[(int64_t)(row + 1) * p.ldd + col]);
+        Cb[(int64_t)(row + 1) * p.ldc + col] = v1;
       }
+      // Every slice has added: the word's last write, which the next launch
+      // on the stream sees.
+      __hip_atomic_store(fb + (int64_t)(row >> 1) * N + col, 0ull, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    };
+    // Up to 8 rows only lanes 0-31 add, and a lane's two adds go out before
+    // either result is used, so their round trips overlap (K = 4096,
+    // N = 14336, HIP graph, two interleaved rounds on one box: M = 4
+    // 12.69-12.70 -> 12.42-12.46 us, M = 8 13.12-13.14 -> 12.80-12.82). With
+    // 16 rows every lane adds twice and the adds in flight together queue at
+    // the atomic units: one at a time measured 14.06-14.11 against
+    // 14.47-14.49 us.
+    if (M <= 8) {
+      uint64_t old[2] = {0, 0};
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        if (g * 4 + 2 * h < M) old[h] = add(h);
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        if (g * 4 + 2 * h < M) finish(h, old[h]);
+    } else {
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        if (g * 4 + 2 * h < M) finish(h, add(h));
     }
   } else {
     int32_t *wsb = p.ws + ((int64_t)bidx * p.k_split + split) * M * N;
