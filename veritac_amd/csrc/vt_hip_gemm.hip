@@ -1804,8 +1804,18 @@ __global__ __launch_bounds__(256) void generic_kernel(GenericArgs p) {
       const int8_t *arow = Ab + i * p.lda;
       const int8_t *bcol = Bb + j;
       int64_t t = 0;
-      // 16 independent loads of A and B per step, so their latencies overlap
-      for (; t + 16 <= p.K; t += 16) {
+      // 32 independent loads of A and B per step, so their latencies overlap
+      for (; t + 32 <= p.K; t += 32) {
+        int32_t av[32], bv[32];
+#pragma unroll
+        for (int u = 0; u < 32; ++u) {
+          av[u] = arow[t + u];
+          bv[u] = bcol[(t + u) * p.ldb];
+        }
+#pragma unroll
+        for (int u = 0; u < 32; ++u) s += (uint32_t)(av[u] * bv[u]);
+      }
+      if (t + 16 <= p.K) {
         int32_t av[16], bv[16];
 #pragma unroll
         for (int u = 0; u < 16; ++u) {
@@ -1814,6 +1824,7 @@ __global__ __launch_bounds__(256) void generic_kernel(GenericArgs p) {
         }
 #pragma unroll
         for (int u = 0; u < 16; ++u) s += (uint32_t)(av[u] * bv[u]);
+        t += 16;
       }
       for (; t < p.K; ++t) s += (uint32_t)((int32_t)arow[t] * (int32_t)bcol[t * p.ldb]);
       p.C[b * p.sc + i * p.ldc + j] = (int32_t)s;
@@ -2188,9 +2199,9 @@ int select_variant(const Problem &q, bool vec, int32_t *variant, int32_t *k_spli
     return VT_OK;
   }
   // Tiny problems past the skinny kernel's rows: with K <= 64 the VALU
-  // kernel's K loop is four batches of loads, under the MFMA kernels' fixed
-  // cost (64^3: 2.5 us against 4.3 us per launch in a HIP graph; from 128^3
-  // on the MFMA kernel is faster).
+  // kernel's K loop is at most two batches of loads, under the MFMA kernels'
+  // fixed cost (64^3: 2.4 us against 4.3 us per launch in a HIP graph; from
+  // 128^3 on the MFMA kernel is faster).
   if (q.M > 16 && q.K <= 64 &&
       (double)q.M * (double)q.N * (double)q.K * (double)q.batch <= 1048576.0) {
     *variant = VT_VARIANT_GENERIC;
