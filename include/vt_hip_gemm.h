@@ -116,9 +116,10 @@ extern "C" {
  *
  * Workspace: the skinny variant's K-split partial sums and the padded
  * variant's copies live in workspaces the library allocates per (device,
- * stream, kind). With a K split over at most 16 rows the skinny kernel
- * finishes the slices' sums itself (when the split's arrival count fits the
- * word), through one 8-byte finishing word per two output elements in a
+ * stream, kind). With a K split over at most 16 rows the decode kernels
+ * (row-major or packed B) finish the slices' sums themselves (when the
+ * split's arrival count fits the word), through one 8-byte finishing word
+ * per two output elements in a
  * workspace of its own kind that is zeroed when it is allocated and that
  * every call leaves zero (no second launch, and never more bytes than the
  * partial sums). A workspace only grows, and a
@@ -387,7 +388,9 @@ int vt_pack_b_i8(const int8_t *B, int8_t *Bp, int64_t K, int64_t N, int64_t ldb,
  *     smaller groups, about one per CU.
  * k_split: workgroups along K for the groups of up to 64 rows (0 =
  * automatic: 1 unless even half-block groups are too few, else a split whose
- * partial sums a second kernel adds); the tile kernels choose their own.
+ * partial sums are finished in the kernel up to 16 rows, through the
+ * finishing words described under Workspace, or added by a second kernel);
+ * the tile kernels choose their own.
  */
 int vt_gemm_i8_packed(const int8_t *A, const int8_t *Bp, const int32_t *D, int32_t *C,
                       int64_t M, int64_t N, int64_t K,

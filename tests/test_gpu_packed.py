@@ -423,3 +423,54 @@ def test_packed_tiles_after_dma_rows_in_batches(dev, extra):
     C = hg.run(plan, At, hg.pack_b(Bt)).cpu().numpy()
     for b in range(batch):
         assert np.array_equal(C[b], go.gemm_i8_f64(A[b], B)), b
+
+
+# m, n, k, explicit k_split (0: automatic), whether the slices finish in the
+# kernel (finishing words) rather than in the reduction launch
+PACKED_FINISH = [
+    (1, 1024, 4096, 0, True),      # 128 half-block groups, K in 2 slices
+    (3, 1024, 4096, 0, True),      # odd rows: the last word's second row is empty
+    (16, 512, 4096, 0, True),      # K in 4 slices
+    (16, 1024, 8192, 0, True),
+    (8, 2048, 4096, 3, True),      # an explicit split
+    (17, 1024, 4096, 0, False),    # two row blocks: the reduction launch
+    (16, 14336, 4096, 0, False),   # whole groups, K unsplit
+]
+
+
+@pytest.mark.parametrize("m,n,k,ks,finishes", PACKED_FINISH)
+def test_packed_k_slices_finished_in_the_kernel(dev, m, n, k, ks, finishes):
+    """Packed-B decode launches that split K finish the slices in the kernel
+    up to 16 rows, through the same finishing words as the row-major decode
+    kernel; out of place, with D and in place (wrapping past int32)."""
+    plan = hg.make_plan(m, n, k, variant=hg.PACKED_VARIANT, k_split=ks)
+    assert hg.packed_finishes(plan) == finishes
+    assert (hg.packed_split(plan)[0] > 1) == (finishes or m > 16)
+    rng = np.random.default_rng(m * 7 + n + k)
+    A = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    B = rng.integers(-128, 128, (k, n), dtype=np.int8)
+    D = np.where(rng.integers(0, 2, (m, n)) == 1, 2**31 - 9, -2**31 + 9).astype(np.int32)
+    say("packed finish", m, n, k, ks)
+    assert np.array_equal(gpu_gemm_packed(dev, A, B, k_split=ks), go.gemm_i8(A, B, None))
+    want = go.gemm_i8(A, B, D)
+    assert np.array_equal(gpu_gemm_packed(dev, A, B, D, k_split=ks), want)
+    assert np.array_equal(gpu_gemm_packed(dev, A, B, D, k_split=ks, in_place=True), want)
+
+
+def test_packed_finish_repeated_and_mixed(dev):
+    """Finishing and two-launch packed calls in turn on one stream, with the
+    row-major decode's finishing calls between them: the words every call
+    leaves zero serve the next."""
+    rng = np.random.default_rng(77)
+    for it, (m, n, k, packed) in enumerate(((2, 1024, 4096, True), (16, 1024, 4096, False),
+                                            (17, 1024, 4096, True), (5, 512, 4096, True),
+                                            (1, 2048, 2048, False), (16, 1024, 4096, True))):
+        A = rng.integers(-128, 128, (m, k), dtype=np.int8)
+        B = rng.integers(-128, 128, (k, n), dtype=np.int8)
+        say("packed finish repeat", it, m, n, k, packed)
+        if packed:
+            got = gpu_gemm_packed(dev, A, B)
+        else:
+            At, Bt = to_dev(dev, A), to_dev(dev, B)
+            got = hg.run(hg.make_plan(m, n, k), At, Bt).cpu().numpy()
+        assert np.array_equal(got, go.gemm_i8(A, B, None)), it

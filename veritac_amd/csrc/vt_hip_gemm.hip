@@ -1644,6 +1644,8 @@ struct PackedArgs {
   int k_split;       // workgroups along K per column group
   int kb_per_split;  // 64-row blocks per K slice
   int32_t *ws;       // [batch][k_split][M][N] partials when k_split > 1
+  uint64_t *fin;     // [batch][(M + 1) / 2][N] finishing words (FIN)
+  int fin_bits;      // FIN: width of each of the word's two sum fields
 };
 
 // M <= 16 * MB (MB row blocks of 16, up to 64 rows): every B tile a wave loads
@@ -1663,8 +1665,9 @@ struct PackedArgs {
 // (non-temporal loads: B is streamed once). The WAVES partial sums of each
 // column block are added through LDS, one row block at a time, and written
 // once (plus D), or go to the workspace when K is split across workgroups.
-template <int NBW, int WAVES, int S, int MB, bool HAS_D, bool MASKED>
+template <int NBW, int WAVES, int S, int MB, bool HAS_D, bool MASKED, bool FIN = false>
 __global__ __launch_bounds__(64 * WAVES) void packed_skinny_kernel(PackedArgs p) {
+  static_assert(!FIN || MB == 1, "finishing in the kernel is instantiated for M <= 16");
   __shared__ v4i red[WAVES * NBW * 64];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1750,6 +1753,51 @@ __global__ __launch_bounds__(64 * WAVES) void packed_skinny_kernel(PackedArgs p)
   // One row block at a time through the same LDS buffer.
   const int32_t *Db = HAS_D ? p.D + bidx * p.sd : nullptr;
   int32_t *Cb = p.C + bidx * p.sc;
+  if constexpr (FIN) {
+    // K slices finished here through the skinny kernel's finishing words
+    // (rows 2i and 2i + 1 of a column share one; see kFinBiasPerRow): thread
+    // t sums rows 2 pr and 2 pr + 1 of column c of block n over the waves,
+    // so 16 consecutive threads add into one 128-byte line of words.
+#pragma unroll
+    for (int n = 0; n < NBW; ++n) red[(wave * NBW + n) * 64 + lane] = acc[0][n];
+    __syncthreads();
+    const int fw = p.fin_bits;
+    const uint64_t field = (1ull << fw) - 1;
+    const int64_t bias = (int64_t)kFinBiasPerRow * p.kb_per_split * 64;
+    uint64_t *fb = p.fin + (int64_t)bidx * ((p.M + 1) >> 1) * p.N;
+    for (int t = tid; t < NBW * 128; t += 64 * WAVES) {
+      const int n = t >> 7, pr = (t >> 4) & 7, c = t & 15;
+      const int row = 2 * pr, src = (row >> 2) * 16 + c, e = row & 3;
+      int32_t s0 = 0, s1 = 0;
+#pragma unroll
+      for (int wv = 0; wv < WAVES; ++wv) {
+        const int32_t *v = (const int32_t *)&red[(wv * NBW + n) * 64 + src];
+        s0 = add_wrap(s0, v[e]);
+        s1 = add_wrap(s1, v[e + 1]);
+      }
+      if (MASKED ? (c < col_lo(n) || c >= col_hi(n)) : n >= live) continue;
+      if (row >= p.M) continue;
+      const int col = (nb0 + n) * 16 + c;
+      // Rows past M hold zero sums (zero A rows): a lone last row's
+      // neighbour field adds the bias alone.
+      const uint64_t lo = (uint64_t)((int64_t)s0 + bias), hi = (uint64_t)((int64_t)s1 + bias);
+      uint64_t *word = fb + (int64_t)pr * p.N + col;
+      const uint64_t old = __hip_atomic_fetch_add(word, (1ull << (2 * fw)) | (hi << fw) | lo,
+                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if ((old >> (2 * fw)) != (uint64_t)(p.k_split - 1)) continue;
+      const int64_t all_bias = bias * p.k_split;
+      int32_t v0 = (int32_t)((int64_t)((old & field) + lo) - all_bias);
+      int32_t v1 = (int32_t)((int64_t)(((old >> fw) & field) + hi) - all_bias);
+      if (HAS_D) v0 = add_wrap(v0, Db[(int64_t)row * p.ldd + col]);
+      Cb[(int64_t)row * p.ldc + col] = v0;
+      if (row + 1 < p.M) {
+        if (HAS_D) v1 = add_wrap(v1, Db[(int64_t)(row + 1) * p.ldd + col]);
+        Cb[(int64_t)(row + 1) * p.ldc + col] = v1;
+      }
+      __hip_atomic_store(word, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return;
+  }
   int32_t *wsb = p.ws ? p.ws + ((int64_t)bidx * p.k_split + split) * p.M * p.N : nullptr;
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
@@ -2795,17 +2843,17 @@ int launch_packed_dma(const Problem &q, int64_t rows, hipStream_t stream, int nu
   return VT_OK;
 }
 
-template <int MB>
+template <int MB, bool FIN = false>
 void launch_packed_kernel(bool d_in, bool masked, dim3 grid, dim3 block, hipStream_t s,
                           const PackedArgs &a) {
   if (d_in && masked)
-    hipLaunchKernelGGL((packed_skinny_kernel<kPackedNBW, kPackedWaves, kPackedS, MB, true, true>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((packed_skinny_kernel<kPackedNBW, kPackedWaves, kPackedS, MB, true, true, FIN>), grid, block, 0, s, a);
   else if (d_in)
-    hipLaunchKernelGGL((packed_skinny_kernel<kPackedNBW, kPackedWaves, kPackedS, MB, true, false>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((packed_skinny_kernel<kPackedNBW, kPackedWaves, kPackedS, MB, true, false, FIN>), grid, block, 0, s, a);
   else if (masked)
-    hipLaunchKernelGGL((packed_skinny_kernel<kPackedNBW, kPackedWaves, kPackedS, MB, false, true>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((packed_skinny_kernel<kPackedNBW, kPackedWaves, kPackedS, MB, false, true, FIN>), grid, block, 0, s, a);
   else
-    hipLaunchKernelGGL((packed_skinny_kernel<kPackedNBW, kPackedWaves, kPackedS, MB, false, false>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((packed_skinny_kernel<kPackedNBW, kPackedWaves, kPackedS, MB, false, false, FIN>), grid, block, 0, s, a);
 }
 
 // One launch (plus the partial-sum reduction when K is split) over at most
@@ -2823,9 +2871,20 @@ int launch_packed_rows(const Problem &q, int k_split, Scratch &scr) {
   a.kb_per_split = (a.kbt + ks0 - 1) / ks0;
   a.k_split = (a.kbt + a.kb_per_split - 1) / a.kb_per_split;
   a.ws = nullptr;
+  a.fin = nullptr;
+  a.fin_bits = 0;
   if ((int64_t)a.groups * a.k_split > 0x7fffffff || q.batch > 65535)
     return fail(VT_EUNSUPPORTED, "packed grid too large");
-  if (a.k_split > 1) {
+  // The K slices finish in the kernel on the skinny kernel's terms (few
+  // rows, a count that fits beside the fields, a per-stream workspace).
+  const bool fin = skinny_finishes(q.M, a.k_split, (int64_t)a.kb_per_split * 64, scr);
+  if (fin) {
+    void *w = nullptr;
+    int rc = scr.take(kFinWords, (size_t)q.batch * ((q.M + 1) / 2) * q.N * sizeof(uint64_t), &w);
+    if (rc) return rc;
+    a.fin = (uint64_t *)w;
+    a.fin_bits = skinny_fin_bits(a.k_split, (int64_t)a.kb_per_split * 64);
+  } else if (a.k_split > 1) {
     void *w = nullptr;
     const size_t pbytes = (size_t)q.batch * a.k_split * q.M * q.N * sizeof(int32_t);
     int rc = scr.take(kPartials, pbytes, &w);
@@ -2834,7 +2893,12 @@ int launch_packed_rows(const Problem &q, int k_split, Scratch &scr) {
   }
   hipStream_t s = (hipStream_t)scr.stream;
   dim3 grid((unsigned)(a.groups * a.k_split), (unsigned)q.batch), block(64 * kPackedWaves);
-  const bool d_in = q.D && a.k_split == 1, masked = a.hpw != 2 * kPackedNBW;
+  const bool d_in = q.D && (a.k_split == 1 || fin), masked = a.hpw != 2 * kPackedNBW;
+  if (fin) {
+    launch_packed_kernel<1, true>(d_in, masked, grid, block, s, a);
+    VT_HIP_CHECK(hipGetLastError());
+    return VT_OK;
+  }
   switch (skinny_row_blocks(q.M)) {
     case 1: launch_packed_kernel<1>(d_in, masked, grid, block, s, a); break;
     case 2: launch_packed_kernel<2>(d_in, masked, grid, block, s, a); break;

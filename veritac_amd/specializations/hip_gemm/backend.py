@@ -146,6 +146,16 @@ def skinny_finishes(plan):
     return ks > 1 and plan["m"] <= SKINNY_FIN_MAX_M and skinny_fin_bits(ks, chunk) > 0
 
 
+def packed_finishes(plan):
+    """Whether the packed decode kernel finishes a packed plan's K slices
+    inside the kernel (one launch) on the skinny kernel's terms: a K split
+    over at most SKINNY_FIN_MAX_M rows whose finishing word fits (the
+    packed launch in the HIP source; vt_gemm_i8_noalloc keeps the second
+    launch)."""
+    ks, per = packed_split(plan)
+    return ks > 1 and plan["m"] <= SKINNY_FIN_MAX_M and skinny_fin_bits(ks, per * 64) > 0
+
+
 def skinny_row_blocks(m):
     """Row blocks of 16 the skinny kernel runs for m rows: 1, 2 or 4
     (skinny_row_blocks in the HIP source)."""
@@ -622,7 +632,8 @@ def modeled_counts(plan):
             mr = rest["m"]
             ks, _ = packed_split(rest)
             groups = -(-mr // SKINNY_MAX_M)
-            partial = 2 * 4 * b * mr * n * ks if ks > 1 else 0
+            partial = (16 * b * -(-mr // 2) * n * ks if packed_finishes(rest) else
+                       2 * 4 * b * mr * n * ks if ks > 1 else 0)
             # B once per group of up to 64 rows; each column group reads its A rows once
             l2_bytes += (groups * (b * -(-k // 64) * 64 * n) + b * mr * k * packed_columns(rest)[1]
                          + 4 * b * mr * n * (2 if plan["has_d"] else 1) + partial)
@@ -715,7 +726,7 @@ def modeled_objective(plan, counts):
     if variant == "skinny":
         launches += skinny_split(plan)[0] > 1 and not skinny_finishes(plan)
     elif variant == PACKED_VARIANT:
-        launches += packed_split(plan)[0] > 1
+        launches += packed_split(plan)[0] > 1 and not packed_finishes(plan)
     else:
         ks = mfma_k_split(plan)
         launches += ks > 1
