@@ -297,22 +297,29 @@ def test_mfma_row_split_mirrors_the_native_choice():
 def test_mfma_selection_follows_the_measured_sweep():
     """The automatic choice among the MFMA tile shapes, on shapes whose three
     variants were timed on the GPU: the measured fastest (ties within 1 % take
-    either). Moving a threshold of select_variant fails here."""
+    either). Moving a threshold of select_variant fails here. Whole 256x128
+    tiles run on the persistent kernel's 256x128 form."""
     from veritac_amd import _lib
+    either = ("mfma_128x128", "mfma_256x128")
     fastest = {
         (1024, 4096, 4096): "mfma_128x128", (1536, 4096, 4096): "mfma_256x128",
         (1536, 4096, 8192): "mfma_256x128", (2048, 4096, 4096): "mfma_256x128",
         (2560, 4096, 4096): "mfma_256x256", (3584, 4096, 4096): "mfma_256x256",
         (2560, 4096, 2048): "mfma_256x256", (768, 14336, 4096): "mfma_256x256",
-        (9000, 1024, 4096): "mfma_256x256", (2048, 4096, 1024): "mfma_128x128",
+        (9000, 1024, 4096): "mfma_256x256", (2048, 4096, 1024): either,
         (1536, 8192, 1024): "mfma_128x128", (1024, 14336, 1024): "mfma_256x256",
         (768, 14336, 512): "mfma_128x128", (9000, 1024, 512): "mfma_128x128",
         (3584, 4096, 256): "mfma_128x128", (600, 28672, 4096): "mfma_256x256",
         (8192, 8192, 8192): "mfma_256x256", (8000, 8192, 8192): "mfma_256x256",
+        (1280, 4096, 1024): "mfma_256x128", (1280, 4096, 4096): "mfma_256x128",
+        (2560, 2048, 2048): "mfma_256x128", (2560, 2048, 8192): "mfma_256x128",
+        (768, 8192, 2048): "mfma_256x128", (512, 14336, 2048): "mfma_256x128",
+        (1024, 8192, 1024): either, (2048, 2048, 4096): "mfma_128x128",
     }
     for (m, n, k), want in fastest.items():
-        assert _lib.select_variant(m, n, k, 1)[0] == want, (m, n, k)
-        assert hg.make_plan(m, n, k)["variant"] == want, (m, n, k)
+        want = (want,) if isinstance(want, str) else want
+        assert _lib.select_variant(m, n, k, 1)[0] in want, (m, n, k)
+        assert hg.make_plan(m, n, k)["variant"] in want, (m, n, k)
 
 
 def test_mfma_column_split_mirrors_the_native_choice():

@@ -89,18 +89,29 @@ def test_k_loop_waits_are_the_kernels_own(asm, kind):
 # itself: s_nop 7 pairs between the accumulators' zeroing (v_accvgpr_write)
 # and the next MFMA, and three s_nop 7 between the last MFMA of a tile and
 # the epilogue's reads of the AGPRs.
-def _k16(has_d, packed, edge=0):
-    return "_ZN12_GLOBAL__N_117gemm_dma16_kernelILb%dELb%dELb%dEEEvNS_8GemmArgsE" % (
-        has_d, packed, edge)
+def _k16(has_d, packed, edge=0, bn=256):
+    return "_ZN12_GLOBAL__N_117gemm_dma16_kernelILb%dELb%dELb%dELi%dEEEvNS_8GemmArgsE" % (
+        has_d, packed, edge, bn)
 
 
-# gemm_dma16_kernel<HAS_D, PACKED_B, EDGE>
+# gemm_dma16_kernel<HAS_D, PACKED_B, EDGE, BN>
 KERNELS16 = {"no_d": _k16(0, 0), "with_d": _k16(1, 0), "packed_b": _k16(0, 1),
              "packed_b_with_d": _k16(1, 1), "edge": _k16(0, 0, 1), "edge_with_d": _k16(1, 0, 1),
-             "packed_b_edge": _k16(0, 1, 1), "packed_b_edge_with_d": _k16(1, 1, 1)}
+             "packed_b_edge": _k16(0, 1, 1), "packed_b_edge_with_d": _k16(1, 1, 1),
+             "bn128": _k16(0, 0, 0, 128), "bn128_with_d": _k16(1, 0, 0, 128)}
 # kinds whose tile's last k iteration is peeled to store early strips: no D,
 # and all tiles whole (the edge kinds mask their stores after the loop)
 EARLY16 = {"no_d", "packed_b"}
+# the 256x128 form: 4 A and 2 B DMAs per wave per slice, 8 x 4 MFMAs per step
+BN128 = {"bn128", "bn128_with_d"}
+
+
+def dmas_per_slice(kind):
+    return 6 if kind in BN128 else 8
+
+
+def mfmas_per_step(kind):
+    return 32 if kind in BN128 else 64
 
 
 def instructions(asm, name):
@@ -119,9 +130,9 @@ def test_dma16_m0_is_only_written_by_the_dma_sequences(asm, kind):
             assert body[i + 2].startswith("global_load_lds_dwordx4"), body[i + 2]
             dmas += 1
     # prologue (3 slices) and the k loop unrolled over the 4 stages, 8 DMAs
-    # per wave per slice; with early strips the tile's last iteration is a
-    # second, peeled copy of the loop body
-    assert dmas == (3 + 4 + (4 if kind in EARLY16 else 0)) * 8
+    # per wave per slice (6 in the 256x128 form); with early strips the
+    # tile's last iteration is a second, peeled copy of the loop body
+    assert dmas == (3 + 4 + (4 if kind in EARLY16 else 0)) * dmas_per_slice(kind)
     assert sum(l.startswith("global_load_lds_dwordx4") for l in body) == dmas
 
 
@@ -133,13 +144,14 @@ def test_dma16_slice_barriers_and_no_full_waits_in_the_k_loop(asm, kind):
     # the peeled last iteration's 4)
     loop_mfma = [i for i in mfma if re.match(r"v_mfma_i32_16x16x64_i8 (a\[\d+:\d+\]), v.*, \1$", body[i])]
     steps = 8 if kind in EARLY16 else 4
-    assert len(loop_mfma) == len(mfma) == steps * 64
+    assert len(loop_mfma) == len(mfma) == steps * mfmas_per_step(kind)
     loop = body[loop_mfma[0]:loop_mfma[-1] + 1]
     assert not [l for l in loop if re.match(r"s_waitcnt .*vmcnt\(0\)", l)]
-    # every slice barrier waits for all but the slice's own 8 DMAs; the
-    # tile's last step also leaves the 6 early strips' 8 stores each
+    # every slice barrier waits for all but the slice's own DMAs; the tile's
+    # last step also leaves the 6 early strips' 8 stores each
+    own = "s_waitcnt vmcnt(%d)" % dmas_per_slice(kind)
     waits = [body[i - 1] for i in range(loop_mfma[0], loop_mfma[-1] + 8) if body[i] == "s_barrier"]
-    want = ["s_waitcnt vmcnt(8)"] * 7 + ["s_waitcnt vmcnt(56)"] if kind in EARLY16 else ["s_waitcnt vmcnt(8)"] * 4
+    want = [own] * 7 + ["s_waitcnt vmcnt(56)"] if kind in EARLY16 else [own] * 4
     assert sorted(waits) == sorted(want), waits
 
 

@@ -250,3 +250,126 @@ def test_strip_lane_bases_equal_strip_off():
                 assert 512 * e + 64 * (ni & 4) < 65536
         for j in range(8):
             assert rb[j >> 1] + 1024 * j == strip_read_addr(lane, j)
+
+
+# gemm_dma16_kernel (16x16x64, slices filled by direct-to-LDS loads): A slice
+# [256][64 B] (a16_swz), B slice [64][BN B] row-major (b16_swz for the 256-wide
+# tile, b8_swz for the 256x128 form), and the 256x128 form's 64-column
+# epilogue strip (strip64_off).
+def a16_swz(row):
+    return ((row >> 3) & 1) << 1
+
+
+def a16_off(row, c):
+    return row * 64 + ((c ^ a16_swz(row)) << 4)
+
+
+def b16_swz(row):
+    return (row & 7) | (((row >> 4) & 1) << 3)
+
+
+def b8_swz(row):
+    return ((row >> 1) & 3) | (((row >> 4) & 1) << 2)
+
+
+DMA16_B = {256: b16_swz, 128: b8_swz}
+
+
+def test_dma16_a_fragment_reads_conflict_free():
+    """Lane l reads row wm*128 + mi*16 + l%16, chunk l/16."""
+    for wm in (0, 1):
+        for mi in range(8):
+            assert conflicts([a16_off(wm * 128 + mi * 16 + (l & 15), l >> 4) for l in range(64)], 16) == 0
+
+
+@pytest.mark.parametrize("bn", [256, 128])
+def test_dma16_b_fragment_reads_conflict_free(bn):
+    """ds_read_b64_tr_b8 of block ni (columns cb*16 ..): lane l reads 8 bytes
+    of row 16*(l/16) + (l%16)/2 (+ 8 for the high half), chunk cb, byte 8*(l&1)."""
+    swz = DMA16_B[bn]
+    for cb in range(bn // 16):
+        for half in (0, 8):
+            addrs = []
+            for l in range(64):
+                row = 16 * (l >> 4) + ((l & 15) >> 1) + half
+                addrs.append(row * bn + ((cb ^ swz(row)) << 4) + (l & 1) * 8)
+            assert conflicts(addrs, 8) == 0, (cb, half)
+    if bn == 128:
+        # the 256-wide swizzle's low three bits alone conflict on 128-byte rows
+        plain = lambda row: row & 7
+        addrs = [(16 * (l >> 4) + ((l & 15) >> 1)) * 128 + ((0 ^ plain(16 * (l >> 4) + ((l & 15) >> 1))) << 4)
+                 + (l & 1) * 8 for l in range(64)]
+        assert conflicts(addrs, 8) > 0
+
+
+@pytest.mark.parametrize("bn", [256, 128])
+def test_dma16_lane_mapping_inverts_the_swizzles(bn):
+    """Lane L of a 1 KB DMA block writes byte 16 L; the global chunk it fetches
+    must be the one the swizzle stores there (A: 16 rows of 64 B per block;
+    B: 1024 / bn rows of bn bytes)."""
+    swz = DMA16_B[bn]
+    per = 1024 // bn
+    slots = bn // 16
+    for block in range(16):
+        for lane in range(64):
+            arow = block * 16 + (lane >> 2)
+            assert a16_off(arow, (lane & 3) ^ a16_swz(arow)) == block * 1024 + lane * 16
+        if block * per >= 64:
+            continue
+        for lane in range(64):
+            brow = block * per + lane // slots
+            bc = (lane % slots) ^ swz(brow)
+            assert brow * bn + ((bc ^ swz(brow)) << 4) == block * 1024 + lane * 16
+            assert 0 <= bc < slots
+
+
+def strip64_off(row, chunk):
+    return row * 256 + ((chunk ^ (((row >> 2) & 3) << 2)) << 4)
+
+
+def strip64_write_addr(lane, ni, e):
+    """Element e of block ni: strip row 4*(l/16)+e, 4-byte word 16*ni + l%16."""
+    g, c = lane >> 4, lane & 15
+    return strip64_off(4 * g + e, ni * 4 + (c >> 2)) + (c & 3) * 4
+
+
+def strip64_read_addr(lane, j):
+    """Read j: lane l takes 16 bytes of strip row 4*j + l/16, chunk l%16."""
+    return strip64_off(4 * j + (lane >> 4), lane & 15)
+
+
+def test_strip64_is_a_permutation_and_conflict_free():
+    assert sorted(strip64_off(r, c) for r in range(16) for c in range(16)) == list(range(0, 4096, 16))
+    for ni in range(4):
+        for e in range(4):
+            assert conflicts_b32([strip64_write_addr(l, ni, e) for l in range(64)]) == 0
+    for j in range(4):
+        assert conflicts([strip64_read_addr(l, j) for l in range(64)], 16) == 0
+    # unswizzled, each write instruction puts 4 lanes on every bank it uses
+    assert conflicts_b32([(4 * (l >> 4)) * 256 + (l & 15) * 4 for l in range(64)]) == 3
+
+
+def test_strip64_round_trip_and_lane_bases():
+    """The accumulator layout comes back as the row-major 16 x 64 strip (read j
+    of lane l is row 4*j + l/16, columns 4*(l%16) ..); the per-lane bases of
+    the kernel (strip64_wb + 256 e, strip64_rb + 1024 j) equal the layout."""
+    import numpy as np
+    want = np.arange(16 * 64, dtype=np.int64).reshape(16, 64) * 11 - 3000
+    lds = np.zeros(1024, np.int64)
+    for ni in range(4):
+        for l in range(64):
+            for e in range(4):
+                lds[strip64_write_addr(l, ni, e) // 4] = want[4 * (l >> 4) + e, 16 * ni + (l & 15)]
+    out = np.zeros((16, 64), np.int64)
+    for j in range(4):
+        for l in range(64):
+            a = strip64_read_addr(l, j) // 4
+            out[4 * j + (l >> 4), 4 * (l & 15):4 * (l & 15) + 4] = lds[a:a + 4]
+    assert np.array_equal(out, want)
+    for l in range(64):
+        g = l >> 4
+        for ni in range(4):
+            for e in range(4):
+                assert 1024 * g + 64 * (ni ^ g) + 4 * (l & 15) + 256 * e == strip64_write_addr(l, ni, e)
+        for j in range(4):
+            assert 256 * g + (((l & 15) ^ (4 * j)) << 4) + 1024 * j == strip64_read_addr(l, j)

@@ -835,6 +835,11 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_dma_kernel(GemmArgs p) {
 __device__ __forceinline__ int a16_swz(int row) { return ((row >> 3) & 1) << 1; }
 __device__ __forceinline__ int a16_off(int row, int c) { return row * 64 + ((c ^ a16_swz(row)) << 4); }
 __device__ __forceinline__ int b16_swz(int row) { return (row & 7) | (((row >> 4) & 1) << 3); }
+// B slice [64][128 B] of the 256x128 form: the 16 rows of one 32-lane
+// transposing read (r .. r + 7 and r + 16 .. r + 23) fall on two bank halves
+// by row parity, so the 8 rows of each parity need 8 distinct chunks: chunk c
+// of row r is stored at c ^ ((r / 2) % 4 + 4 * bit 4 of r).
+__host__ __device__ constexpr int b8_swz(int row) { return ((row >> 1) & 3) | (((row >> 4) & 1) << 2); }
 
 // Epilogue of gemm_dma16_kernel through LDS: each 16-row strip of the wave's
 // 128-column block is written to the wave's 8 KB of LDS in the accumulator
@@ -881,6 +886,33 @@ constexpr bool strip_bases_match() {
   return true;
 }
 static_assert(strip_bases_match(), "strip bases disagree with strip_off");
+
+// The 64-column strip of the 256x128 form: 16 rows of 256 bytes, chunk k of
+// row r at k ^ (4 * ((r / 4) % 4)). Write of element e of block ni (row
+// 4 g + e, column 16 ni + c, g = lane / 16, c = lane % 16): wb[ni] + 256 e.
+// Read j (row 4 j + lane / 16, chunk lane % 16): rb[j] + 1024 j.
+__host__ __device__ constexpr int strip64_off(int row, int chunk) {
+  return row * 256 + ((chunk ^ (((row >> 2) & 3) << 2)) << 4);
+}
+__host__ __device__ constexpr int strip64_wb(int lane, int ni) {
+  return 1024 * (lane >> 4) + 64 * (ni ^ (lane >> 4)) + 4 * (lane & 15);
+}
+__host__ __device__ constexpr int strip64_rb(int lane, int j) {
+  return 256 * (lane >> 4) + (((lane & 15) ^ (4 * j)) << 4);
+}
+constexpr bool strip64_bases_match() {
+  for (int lane = 0; lane < 64; ++lane) {
+    const int g = lane >> 4, c = lane & 15;
+    for (int ni = 0; ni < 4; ++ni)
+      for (int e = 0; e < 4; ++e)
+        if (strip64_wb(lane, ni) + 256 * e != strip64_off(4 * g + e, 4 * ni + (c >> 2)) + (c & 3) * 4)
+          return false;
+    for (int j = 0; j < 4; ++j)
+      if (strip64_rb(lane, j) + 1024 * j != strip64_off(4 * j + g, c)) return false;
+  }
+  return true;
+}
+static_assert(strip64_bases_match(), "64-column strip bases disagree with strip64_off");
 
 struct StripLanes {
   int wb[4], rb[4];
@@ -956,11 +988,43 @@ __device__ __forceinline__ void store_tile16_lds(const v4i (&acc)[MI][NI], int32
   }
 }
 
+// One 16-row strip of the 256x128 form's epilogue (whole tiles): the wave's
+// 64 columns go through its LDS strip and out as 4 stores, each of four whole
+// 256-byte row segments. wb / rb: strip64_wb / strip64_rb plus the strip's
+// offset in LDS; gofs_c / gofs_d: the lane's byte offset from its 4-row
+// group's base. With D, the strip's 4 D loads precede its stores, and each
+// lane reads its own D bytes before writing them, so C may be D.
+template <bool HAS_D>
+__device__ __forceinline__ void store_strip64_lds(const v4i (&acc)[4], int32_t *Cs, const int32_t *Ds,
+                                                  int64_t ldc, int64_t ldd, const int (&wb)[4],
+                                                  const int (&rb)[4], uint32_t gofs_c, uint32_t gofs_d,
+                                                  LDS_AS int8_t *lds) {
+#pragma unroll
+  for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) *(LDS_AS int32_t *)(lds + wb[ni] + e * 256) = acc[ni][e];
+  v4i v[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] = *(LDS_AS v4i *)(lds + rb[j] + j * 1024);
+  if constexpr (HAS_D) {
+    v4i d[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) d[j] = *(const v4i *)((const int8_t *)(Ds + 4 * j * ldd) + gofs_d);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[j][q] = add_wrap(v[j][q], d[j][q]);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    __builtin_nontemporal_store(v[j], (v4i *)((int8_t *)(Cs + 4 * j * ldc) + gofs_c));
+}
+
 // v_mfma_i32_16x16x64_i8 accumulating in place in AGPRs. As a builtin, the
 // compiler gives each result a new register tuple and, with all 256 AGPRs
 // holding accumulators, stages them through VGPRs around every MFMA; the
 // tied asm operand keeps each accumulator in one AGPR tuple. Hazards: every
-// use in gemm_dma16_kernel reads an accumulator 64 MFMAs after its previous
+// use in gemm_dma16_kernel reads an accumulator 32 or 64 MFMAs after its previous
 // write, its fragments come from LDS reads the compiler waits for, and the
 // kernel waits explicitly before its epilogue reads the results.
 __device__ __forceinline__ void mfma16_in_place(v4i &acc, const v4i &a, const v4i &b) {
@@ -986,21 +1050,26 @@ __device__ __forceinline__ void mfma16_in_place(v4i &acc, const v4i &a, const v4
 // slice gs + 2, whose fragments step gs + 1 reads. Stage gs % 4 is refilled in
 // step gs + 1; its reads were issued in step gs - 1 and consumed by step gs's
 // MFMAs.
-template <bool HAS_D, bool PACKED_B, bool EDGE = false>
+template <bool HAS_D, bool PACKED_B, bool EDGE = false, int BN = 256>
 __global__ __launch_bounds__(256, 1) void gemm_dma16_kernel(GemmArgs p) {
-  constexpr int BM = 256, BN = 256, BK = 64;
-  constexpr int WTM = 128, WTN = 128, MI = WTM / 16, NI = WTN / 16;
+  // BN = 128 (the 256x128 form: whole tiles, row-major B) gives each wave a
+  // 128x64 block and half the B slice; the rest is shared.
+  static_assert(BN == 256 || (BN == 128 && !PACKED_B && !EDGE), "256x128: whole tiles, row-major B");
+  constexpr int BM = 256, BK = 64;
+  constexpr int WTM = 128, WTN = BN / 2, MI = WTM / 16, NI = WTN / 16;
   constexpr int A_BYTES = BM * BK, B_BYTES = BK * BN;
   constexpr int NSTAGE = 4;
-  // A stages at [0, 64 KB), B stages at [64 KB, 128 KB): with the stage a
-  // compile-time constant, every fragment read is its base register plus an
-  // immediate offset below 64 KB, with no address arithmetic per read.
+  // A stages at [0, 64 KB), B stages at [64 KB, 128 KB) (each B stage in a
+  // 16 KB slot): with the stage a compile-time constant, every fragment read
+  // is its base register plus an immediate offset below 64 KB, with no
+  // address arithmetic per read.
   constexpr int B_REGION = NSTAGE * A_BYTES;
-  static_assert(A_BYTES == B_BYTES && (NSTAGE - 1) * A_BYTES + 8 * BN < 65536, "16-bit read offsets");
-  constexpr int DPW = 4;                 // 1 KB DMA blocks of A (and of B) per wave per slice
-  constexpr int DMAS = 2 * DPW;
+  static_assert(B_BYTES <= A_BYTES && (NSTAGE - 1) * A_BYTES + 8 * BN < 65536, "16-bit read offsets");
+  constexpr int DPW = 4;                 // 1 KB DMA blocks of A per wave per slice
+  constexpr int DPW_B = B_BYTES / 4096;  // and of B (4 or 2)
+  constexpr int DMAS = DPW + DPW_B;
   // The 32 KB past the stages hold each wave's 8 KB epilogue strip.
-  __shared__ __attribute__((aligned(1024))) int8_t smem[NSTAGE * (A_BYTES + B_BYTES) + 4 * 8192];
+  __shared__ __attribute__((aligned(1024))) int8_t smem[NSTAGE * 2 * A_BYTES + 4 * 8192];
   static_assert(sizeof(smem) == kDma16Lds, "LDS the host reports for this kernel");
 
   const int tid = threadIdx.x;
@@ -1044,10 +1113,17 @@ __global__ __launch_bounds__(256, 1) void gemm_dma16_kernel(GemmArgs p) {
     a_lane[i] = (uint32_t)((int64_t)arow * lda + ac * 16);
     if constexpr (PACKED_B) {
       b_lane[i] = (uint32_t)((int64_t)(wave * DPW + i) * ldb * 1024 + lane * 16);
-    } else {
+    } else if constexpr (BN == 256) {
       const int brow = (wave * DPW + i) * 4 + (lane >> 4);
       const int bc = (lane & 15) ^ b16_swz(brow);
       b_lane[i] = (uint32_t)((int64_t)brow * ldb + bc * 16);
+    } else if (i < DPW_B) {
+      // 8 rows of 128 bytes per 1 KB block; lane L writes slot L % 8 of row L / 8
+      const int brow = (wave * DPW_B + i) * 8 + (lane >> 3);
+      const int bc = (lane & 7) ^ b8_swz(brow);
+      b_lane[i] = (uint32_t)((int64_t)brow * ldb + bc * 16);
+    } else {
+      b_lane[i] = 0;
     }
   }
   // The slice the next DMA round fetches: running A and B pointers, the
@@ -1081,11 +1157,11 @@ __global__ __launch_bounds__(256, 1) void gemm_dma16_kernel(GemmArgs p) {
     const int8_t *abase, *bbase;
     next_bases(abase, bbase);
     const uint32_t ma = lds0 + stage * A_BYTES + wave * DPW * 1024;
-    const uint32_t mb = ma + B_REGION;
+    const uint32_t mb = BN == 256 ? ma + B_REGION : lds0 + B_REGION + stage * A_BYTES + wave * DPW_B * 1024;
 #pragma unroll
     for (int i = 0; i < DPW; ++i) dma_b128(abase, a_lane[i], ma + i * 1024);
 #pragma unroll
-    for (int i = 0; i < DPW; ++i) dma_b128(bbase, b_lane[i], mb + i * 1024);
+    for (int i = 0; i < DPW_B; ++i) dma_b128(bbase, b_lane[i], mb + i * 1024);
   };
 
   // Fragment offsets within a stage. A block mi: lane l reads row
@@ -1103,7 +1179,8 @@ __global__ __launch_bounds__(256, 1) void gemm_dma16_kernel(GemmArgs p) {
       b_frag[ni] = B_REGION + cb * 1024 + lane * 16;
     } else {
       const int row = 16 * (lane >> 4) + ((lane & 15) >> 1);
-      b_frag[ni] = B_REGION + row * BN + ((cb ^ b16_swz(row)) << 4) + (lane & 1) * 8;
+      const int swz = BN == 256 ? b16_swz(row) : b8_swz(row);
+      b_frag[ni] = B_REGION + row * BN + ((cb ^ swz) << 4) + (lane & 1) * 8;
     }
   }
   // The accumulators, in AGPRs (mfma16_in_place). The MFMAs are asm, whose
@@ -1153,7 +1230,17 @@ __global__ __launch_bounds__(256, 1) void gemm_dma16_kernel(GemmArgs p) {
   static_assert(8 * EARLY_STRIPS + DMAS <= 63, "vmcnt counts at most 63");
   int32_t *c_tile = nullptr;   // the wave's block of C in the current tile
   LDS_AS int8_t *const lds = (LDS_AS int8_t *)smem;
-  const StripLanes sl = strip_lanes(lane, NSTAGE * (A_BYTES + B_BYTES) + wave * 8192, p.ldc, p.ldd);
+  constexpr int STRIP0 = NSTAGE * 2 * A_BYTES;
+  const StripLanes sl = strip_lanes(lane, STRIP0 + wave * 8192, p.ldc, p.ldd);
+  // The 256x128 form's 64-column strip (the first 4 KB of the wave's 8 KB).
+  int wb64[4], rb64[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    wb64[k] = STRIP0 + wave * 8192 + strip64_wb(lane, k);
+    rb64[k] = STRIP0 + wave * 8192 + strip64_rb(lane, k);
+  }
+  const uint32_t gofs64 = (uint32_t)(((lane >> 4) * p.ldc + (lane & 15) * 4) * 4);
+  const uint32_t gofs64_d = (uint32_t)(((lane >> 4) * p.ldd + (lane & 15) * 4) * 4);
   // One step: MFMAs of slice gs, row by row (odd rows right to left), from fa
   // and fb; slice gs + 1's B blocks go to gb in the first BU slots (block
   // order = first use), its A blocks to fa as each row's last MFMA retires.
@@ -1167,7 +1254,9 @@ __global__ __launch_bounds__(256, 1) void gemm_dma16_kernel(GemmArgs p) {
     const int8_t *abase, *bbase;
     next_bases(abase, bbase);   // slice gs + 3
     const uint32_t ma = lds0 + s3 * A_BYTES + wave * DPW * 1024;
-    const uint32_t mb = ma + B_REGION;
+    const uint32_t mb = BN == 256 ? ma + B_REGION : lds0 + B_REGION + s3 * A_BYTES + wave * DPW_B * 1024;
+    // DMAs every DSTEP slots: 8 of them over 64 slots, or 6 over 32 (every 4)
+    constexpr int DSTEP = BN == 256 ? 8 : 4;
 #pragma unroll
     for (int slot = 0; slot < MI * NI; ++slot) {
       // Odd rows take their B blocks in reverse ("snake"), so each row's
@@ -1177,10 +1266,10 @@ __global__ __launch_bounds__(256, 1) void gemm_dma16_kernel(GemmArgs p) {
       mfma16_in_place(acc[mi][ni], fa[mi], fb[ni]);
       if (slot < BU) read_b(s1, slot, gb);
       if (pos == NI - 1) read_a(s1, mi);
-      if ((slot & 7) == 2) {
-        const int d = slot >> 3;
+      if (slot % DSTEP == 2) {
+        const int d = slot / DSTEP;
         if (d < DPW) dma_b128(abase, a_lane[d], ma + d * 1024);
-        else dma_b128(bbase, b_lane[d - DPW], mb + (d - DPW) * 1024);
+        else if (d < DMAS) dma_b128(bbase, b_lane[d - DPW], mb + (d - DPW) * 1024);
       }
       if constexpr (EARLY) {
         if (slot >= 15 && (slot - 15) % 8 == 0 && (slot - 15) / 8 < EARLY_STRIPS) {
@@ -1202,8 +1291,9 @@ __global__ __launch_bounds__(256, 1) void gemm_dma16_kernel(GemmArgs p) {
   };
   using Plain = std::integral_constant<bool, false>;
   // EDGE (moved-back tiles, masked stores): no early strips, so no store
-  // branch enters the scheduled step.
-  using Early = std::integral_constant<bool, !HAS_D && !EDGE>;
+  // branch enters the scheduled step; the 256x128 form stores every strip in
+  // the epilogue.
+  using Early = std::integral_constant<bool, !HAS_D && !EDGE && BN == 256>;
 
   issue_slice(0);
   issue_slice(1);
@@ -1229,14 +1319,14 @@ __global__ __launch_bounds__(256, 1) void gemm_dma16_kernel(GemmArgs p) {
     // the first EARLY_STRIPS strips of C (straight-line code: a branch over
     // steps that write the accumulators makes the register allocator
     // shuffle them).
-    const int KL = HAS_D || EDGE ? KT : KT - 4;
+    const int KL = HAS_D || EDGE || BN != 256 ? KT : KT - 4;
     for (int kt = 0; kt < KL; kt += 4, gs += 4) {
       step(Plain(), 0, fb0, fb1);
       step(Plain(), 1, fb1, fb0);
       step(Plain(), 2, fb0, fb1);
       step(Plain(), 3, fb1, fb0);
     }
-    if constexpr (!HAS_D && !EDGE) {
+    if constexpr (!HAS_D && !EDGE && BN == 256) {
       step(Plain(), 0, fb0, fb1);
       step(Plain(), 1, fb1, fb0);
       step(Plain(), 2, fb0, fb1);
@@ -1248,11 +1338,22 @@ __global__ __launch_bounds__(256, 1) void gemm_dma16_kernel(GemmArgs p) {
     fence_acc();
     // Rows [m0, mn) and columns [n0, nn) of a moved-back tile are its
     // neighbour's to store (0 unless EDGE).
-    store_tile16_lds<MI, NI, HAS_D, HAS_D || EDGE ? 0 : EARLY_STRIPS, EDGE>(
-        acc, c_tile,
-        HAS_D ? p.D + bidx * p.sd + (int64_t)(m0 + wm * WTM) * p.ldd + n0 + wn * WTN : nullptr,
-        p.ldc, p.ldd, sl, lds, wm * WTM + (lane >> 5) - (mn - m0),
-        wn * WTN + (lane & 31) * 4 >= nn - n0);
+    if constexpr (BN == 256) {
+      store_tile16_lds<MI, NI, HAS_D, HAS_D || EDGE ? 0 : EARLY_STRIPS, EDGE>(
+          acc, c_tile,
+          HAS_D ? p.D + bidx * p.sd + (int64_t)(m0 + wm * WTM) * p.ldd + n0 + wn * WTN : nullptr,
+          p.ldc, p.ldd, sl, lds, wm * WTM + (lane >> 5) - (mn - m0),
+          wn * WTN + (lane & 31) * 4 >= nn - n0);
+    } else {
+      const int32_t *d_tile =
+          HAS_D ? p.D + bidx * p.sd + (int64_t)(m0 + wm * WTM) * p.ldd + n0 + wn * WTN : nullptr;
+#pragma unroll
+      for (int mi = 0; mi < MI; ++mi) {
+        store_strip64_lds<HAS_D>(acc[mi], c_tile + mi * 16 * p.ldc, HAS_D ? d_tile + mi * 16 * p.ldd : nullptr,
+                                 p.ldc, p.ldd, wb64, rb64, gofs64, gofs64_d, lds);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
     zero_acc();
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -2298,7 +2399,15 @@ int select_variant(const Problem &q, bool vec, int32_t *variant, int32_t *k_spli
       (persistent && ((q.K >= 2048 && t256 > 128) || (q.K >= 1024 && t256 > 192)))) {
     *variant = VT_VARIANT_MFMA_256x256;
   } else {
-    const bool wide = q.K >= 2048 && (t128 >= 256 || (q.K >= 4096 && t128 >= 192));
+    // Whole 256x128 tiles run on the persistent kernel's 256x128 form, which
+    // wins over 128x128 tiles from more than half a round of its tiles at
+    // K >= 1024 (M x N: 1280 x 4096, K = 1024 12.8 us against 14.0, K = 4096
+    // 29.8 against 37.3; 2560 x 2048, K = 2048 18.5 against 22.0; 768 x 8192,
+    // K = 2048 19.5 against 23.3; 512 x 14336, K = 2048 20.8 against 24.6),
+    // but not at half a round or less (1024 x 4096 x 4096: 28.8 against 25.2).
+    const bool whole128 = m_eff % 256 == 0 && q.N % 128 == 0 && q.K % 256 == 0;
+    const bool wide = (q.K >= 2048 && (t128 >= 256 || (q.K >= 4096 && t128 >= 192))) ||
+                      (whole128 && q.K >= 1024 && t128 > 128 && t128 <= 256);
     *variant = (wide && m_eff >= 256) ? VT_VARIANT_MFMA_256x128 : VT_VARIANT_MFMA_128x128;
   }
   return VT_OK;
@@ -2325,6 +2434,16 @@ bool use_dma16(const Problem &r) {
   const bool d_ok = !r.D || (aligned16(r.D) && r.ldd % 4 == 0 && (r.batch == 1 || r.sd % 4 == 0) &&
                              r.ldd < (1ll << 29));
   return r.K % 256 == 0 && c_ok && d_ok;
+}
+
+// Row-major problems of whole 256x128 tiles run on the 256x128 form of
+// gemm_dma16_kernel (persistent, one workgroup per CU) when its 16-byte C and
+// D accesses are aligned; it addresses a lane's 16 bytes from its 4-row
+// group's base (three rows of ldc or ldd plus 256 bytes) as a 32-bit byte
+// offset. Otherwise gemm_mfma_kernel<256, 128> takes them.
+bool dma16_128_fits(const Problem &r) {
+  return r.K > 0 && r.M % 256 == 0 && r.N % 128 == 0 && r.ldc < (1ll << 28) &&
+         (!r.D || r.ldd < (1ll << 28)) && use_dma16(r);
 }
 
 template <int BM, int BN, int EDGE, bool HAS_D, bool PACKED>
@@ -2598,6 +2717,13 @@ int launch_mfma_tiles(const Problem &r, hipStream_t stream, int num_cus) {
     } else {
       hipLaunchKernelGGL((gemm_dma_kernel<kDmaWaves, false>), pgrid, dim3(64 * kDmaWaves), 0, stream, a);
     }
+    VT_HIP_CHECK(hipGetLastError());
+    return VT_OK;
+  }
+  if (!PACKED && BM == 256 && BN == 128 && dma16_128_fits(r)) {
+    const int64_t g = blocks < num_cus ? blocks : num_cus;
+    if (has_d) hipLaunchKernelGGL((gemm_dma16_kernel<true, false, false, 128>), dim3((unsigned)g), dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((gemm_dma16_kernel<false, false, false, 128>), dim3((unsigned)g), dim3(256), 0, stream, a);
     VT_HIP_CHECK(hipGetLastError());
     return VT_OK;
   }

@@ -412,11 +412,17 @@ def mfma_tiles(plan):
 def _runs_persistent(plan):
     """Whether an mfma_256x256 plan (without a row or column split) runs on
     the persistent kernel: each K slice in whole 64-deep steps and M (after
-    the fold) and N at least one tile (persistent_fits in the HIP source)."""
-    if plan["variant"] != "mfma_256x256":
+    the fold) and N at least one tile (persistent_fits in the HIP source).
+    An mfma_256x128 plan runs on the persistent kernel's 256x128 form when M
+    (after the fold) and N are whole 256x128 tiles and each K slice is whole
+    256-deep groups (dma16_128_fits; plans assume 16-byte aligned C and D
+    with rows of n elements)."""
+    if plan["variant"] not in ("mfma_256x256", "mfma_256x128"):
         return False
     m = plan["m"] * plan["batch"] if plan["b_shared"] and plan["batch"] > 1 else plan["m"]
     kslice = plan["k"] // mfma_k_split(plan)
+    if plan["variant"] == "mfma_256x128":
+        return kslice > 0 and kslice % 256 == 0 and m % 256 == 0 and plan["n"] % 128 == 0
     return kslice > 0 and kslice % 64 == 0 and m >= 256 and plan["n"] >= 256
 
 
@@ -426,7 +432,7 @@ def required_resources(plan):
     The analogue of backend.py:97-104 (scratchpad / accumulator rows) for a
     gfx950 launch: LDS is the on-chip buffer a workgroup needs, workgroups
     the grid size. The persistent 256x256 kernel launches one workgroup per
-    CU (at most) whatever the tile count.
+    CU (at most) whatever the tile count, and so does its 256x128 form.
     """
     variant = plan["variant"]
     tm, tn, _, _, lds = TILES[variant]
