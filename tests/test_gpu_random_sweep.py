@@ -3,7 +3,8 @@
 Each case draws a variant (automatic, each vector variant, the any-shape
 variants, packed B), a shape fitting it (M, N, K from 1 to about 1100, with
 the variant's divisibility rules, often landing on tile edges; half of the
-256 x 256 draws in whole tiles with K % 256 == 0), a batch count,
+256 x 256 draws in whole tiles with K % 256 == 0, and half of the 256 x 128
+draws in whole 256 x 128 tiles with K % 256 == 0), a batch count,
 shared or separate B, D or not, C in place of D or not, and adversarial
 inputs (int8 extremes mixed with uniform bytes). Every output element is
 compared with the oracle; a case that the plan validation refuses is
@@ -54,6 +55,10 @@ def draw_case(rng):
         if variant == "mfma_256x256" and rng.random() < 0.5:
             # whole 256 x 256 tiles with K % 256 == 0: the 16x16x64 kernel
             m, n, k = (max(256, (v + 255) // 256 * 256) for v in (m, n, k))
+        if variant == "mfma_256x128" and rng.random() < 0.5:
+            # whole 256 x 128 tiles with K % 256 == 0: its persistent form
+            m, k = (max(256, (v + 255) // 256 * 256) for v in (m, k))
+            n = max(128, (n + 127) // 128 * 128)
         batch = int(rng.choice([1, 1, 2, 3]))
         shared = bool(rng.random() < 0.5) and batch > 1
         has_d = bool(rng.random() < 0.5)
