@@ -70,7 +70,9 @@ extern "C" {
 #define VT_VARIANT_SKINNY 3        /* M <= 64 decode shapes: B streamed once,
                                       v_mfma_i32_16x16x64_i8, K split         */
 #define VT_VARIANT_GENERIC 4       /* any shape/stride/alignment, VALU        */
-#define VT_VARIANT_MFMA_256x128 5  /* 256x128 tile, 4 waves                   */
+#define VT_VARIANT_MFMA_256x128 5  /* 256x128 tile, 4 waves; whole tiles with
+                                      K % 256 == 0 and 16-byte aligned C, D run
+                                      persistently (one workgroup per CU)     */
 #define VT_VARIANT_PADDED 6        /* any shape: A and B copied with K and N
                                       zero-padded to multiples of 16, run on
                                       the MFMA / skinny kernels, C copied out
