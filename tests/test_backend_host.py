@@ -221,7 +221,8 @@ def test_mfma_k_split_mirrors_the_native_choice():
     for m, n, k in [(128, 14336, 4096), (96, 14336, 4096), (128, 4096, 4096), (256, 4096, 4096),
                     (512, 4096, 4096), (8192, 8192, 8192), (1024, 14336, 4096), (300, 208, 160),
                     (128, 4096, 1024), (128, 4096, 1152), (100, 256, 65536), (96, 2048, 1024),
-                    (256, 256, 8192)]:
+                    (256, 256, 8192), (768, 2048, 8192), (512, 4096, 16384), (768, 2048, 4096),
+                    (1280, 2048, 8192)]:
         plan = hg.make_plan(m, n, k)
         _, _, variant, ks, ws = _lib.gemm_check(m, n, k, k, n, n, n)
         assert plan["variant"] == variant

@@ -596,10 +596,12 @@ def test_random_problems_match_the_oracle(dev, variant):
 
 
 # Few long MFMA tiles: K runs as slices (batches of the same kernel) into a
-# partial-sum workspace, added with D by the reduction kernel.
+# partial-sum workspace, added with D by the reduction kernel (from K = 8192
+# also two slices over 65..128 tiles).
 SPLIT_CASES = [("mfma_128x128", 128, 4096, 4096), ("mfma_128x128", 96, 2048, 2048),
                ("mfma_128x128", 100, 208, 2048), ("mfma_256x256", 256, 256, 8192),
-               ("mfma_256x128", 256, 384, 4096), ("auto", 256, 1024, 4096)]
+               ("mfma_256x128", 256, 384, 4096), ("auto", 256, 1024, 4096),
+               ("mfma_128x128", 768, 2048, 8192), ("mfma_256x128", 1280, 2048, 8192)]
 
 
 @pytest.mark.parametrize("variant,m,n,k", SPLIT_CASES)

@@ -2492,14 +2492,15 @@ int launch_reduce(const ReduceArgs &r, int64_t batch, hipStream_t stream) {
 // does not earn back (M = 128, N = 14336, K = 4096: 22.6 -> 24.0 us); from
 // four slices on it does (N = K = 4096: M = 128 21.0 -> 13.2 us, M = 256
 // 21.2 -> 16.5 us; M = 128, N = 1024, K = 16384 in 13.2 us, M = N = 256,
-// K = 8192 in 10.0 us). Sized for the 256 CUs of an MI355X rather than the
-// device at hand, so launch, scratch sizing and the check agree. 1: no split.
+// K = 8192 in 10.0 us). From K = 8192 on, two slices over 65..128 tiles do
+// earn it back. Sized for the 256 CUs of an MI355X rather than the device at
+// hand, so launch, scratch sizing and the check agree. 1: no split.
 constexpr int64_t kSplitCus = 256;
 template <int BM, int BN>
 int mfma_k_split(const Problem &r) {
   if (r.batch != 1 || r.K < 1024 || r.N % 16) return 1;
   const int64_t tiles = (r.M + BM - 1) / BM * ((r.N + BN - 1) / BN);
-  if (tiles * 4 > kSplitCus) return 1;
+  if (tiles * 4 > kSplitCus) return tiles * 2 <= kSplitCus && r.K >= 8192 && r.K % 256 == 0 ? 2 : 1;
   int ks = 1;
   while (ks < 16 && 2 * ks * tiles <= kSplitCus) ks *= 2;
   while (ks > 1 && (r.K % (128 * ks) || r.K / ks < 512)) ks /= 2;

@@ -220,12 +220,13 @@ def _folded(plan):
 def _k_split_for_tiles(m, n, k, b, tm, tn):
     """mfma_k_split<tm, tn> in the HIP source, on a folded problem: a k of at
     least 1024 over at most 64 tiles is cut into up to 16 slices of whole
-    128-deep steps, each at least 512 deep, for up to 256 workgroups."""
+    128-deep steps, each at least 512 deep, for up to 256 workgroups; from
+    k = 8192 on, one over 65..128 tiles into two slices."""
     if b != 1 or k < 1024 or n % 16:
         return 1
     tiles = -(-m // tm) * -(-n // tn)
     if tiles * 4 > NUM_CUS:
-        return 1
+        return 2 if tiles * 2 <= NUM_CUS and k >= 8192 and k % 256 == 0 else 1
     ks = 1
     while ks < 16 and 2 * ks * tiles <= NUM_CUS:
         ks *= 2
