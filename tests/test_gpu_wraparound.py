@@ -91,7 +91,8 @@ def test_partial_sum_near_int32_limits_wraps(dev, variant, k_split, m, n, k, spl
     ("generic", 16, 16, 0),                 # VALU sum wraps
     ("skinny", 16, 256, 64),                # partials in range; the reduction wraps
     ("mfma_128x128", 256, 256, 16),         # K split; the reduction wraps
-    ("mfma_256x256", 2304, 2048, 0)])       # gemm_dma16_kernel: the MFMA accumulators wrap
+    ("mfma_256x256", 2304, 4096, 0)])       # gemm_dma16_kernel (144 tiles, K unsplit): the
+                                            # MFMA accumulators wrap
 def test_k_past_the_legality_bound_wraps(dev, variant, m, n, split):
     """All -128 operands over K = 139264 give 16384 * K = 2281701376 per cell
     before D, which wraps to -2013265920; then mixed signs, checked against
