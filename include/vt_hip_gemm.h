@@ -219,8 +219,9 @@ int vt_gemm_select(int64_t M, int64_t N, int64_t K, int64_t batch,
  * (backend.py:97-104). No device call. For the MFMA variants the LDS is that
  * of their tile kernel (three 64-deep slice buffers of A and B); the
  * persistent 256x256 kernels, one workgroup per CU, take 160 KiB (K % 256 == 0
- * with 16-byte C and D rows) or 128 KiB. The skinny figure excludes the A
- * slice, which depends on K and the split.
+ * with 16-byte C and D rows) or 128 KiB, and so does the persistent form of
+ * 256x128 (160 KiB; whole tiles, K % 256 == 0, 16-byte C and D rows). The
+ * skinny figure excludes the A slice, which depends on K and the split.
  */
 int vt_variant_info(int32_t variant, int32_t *tile_m, int32_t *tile_n,
                     int32_t *tile_k, int32_t *threads, int32_t *lds_bytes);
