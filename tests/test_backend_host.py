@@ -234,8 +234,10 @@ def test_mfma_k_split_mirrors_the_native_choice():
             tm, tn = hg.mfma_tile_shape(plan)
             tiles = -(-m // tm) * -(-n // tn) * want
             assert hg.mfma_tiles(plan) == tiles
-            persistent = variant == "mfma_256x256" and m >= 256 and n >= 256 and \
-                (k // want) % 64 == 0
+            persistent = (variant == "mfma_256x256" and m >= 256 and n >= 256 and
+                          (k // want) % 64 == 0) or \
+                (variant == "mfma_256x128" and m % 256 == 0 and n % 128 == 0 and
+                 (k // want) % 256 == 0)
             # the persistent kernel: one workgroup per CU, 160 KiB (K slice % 256
             # == 0) or 128 KiB of LDS; the tile kernel: a workgroup per tile
             lds = 3 * (tm * 64 + 64 * tn) if tm == 64 else hg.TILES[variant][4]
@@ -316,6 +318,10 @@ def test_mfma_selection_follows_the_measured_sweep():
         (2560, 2048, 2048): "mfma_256x128", (2560, 2048, 8192): "mfma_256x128",
         (768, 8192, 2048): "mfma_256x128", (512, 14336, 2048): "mfma_256x128",
         (1024, 8192, 1024): either, (2048, 2048, 4096): "mfma_128x128",
+        (1280, 2048, 16384): "mfma_256x256", (768, 4096, 12288): "mfma_256x256",
+        (512, 8192, 16384): "mfma_256x256", (2048, 4096, 32768): "mfma_256x256",
+        (2048, 4096, 16384): either, (768, 2048, 16384): "mfma_256x128",
+        (1024, 2048, 32768): "mfma_256x128", (512, 2048, 16384): "mfma_128x128",
     }
     for (m, n, k), want in fastest.items():
         want = (want,) if isinstance(want, str) else want

@@ -2393,10 +2393,16 @@ int select_variant(const Problem &q, bool vec, int32_t *variant, int32_t *k_spli
   // (K = 512, 144-168 tiles: 14.8-15.0 us against 16.9-17.4). With K >= 4096
   // 256x128 also wins at 192 of its tiles (96 of 256x256; M = 1536, N = 4096:
   // 36.1 against 38.7 us, K = 8192 64.8 against 71.7).
+  // From K = 12288 the persistent kernel, K split in four, also wins at 40-96
+  // tiles (M x N x K: 1280 x 2048 x 16384 54.2 us against 73.9 on 128x128;
+  // 768 x 4096 x 12288 51.9 against 57.9; 512 x 8192 x 16384 79.5 against
+  // 112.5), and from K = 32768 at 97-128 tiles as well (2048 x 4096 x 32768
+  // 221.8 against 294.5 on 256x128).
   const bool persistent = q.K % 64 == 0 && m_eff >= 256 && q.N >= 256;
   const int64_t t128 = (m_eff + 255) / 256 * ((q.N + 127) / 128) * b_eff;
   if ((t256 >= 256 && q.N >= 256) ||
-      (persistent && ((q.K >= 2048 && t256 > 128) || (q.K >= 1024 && t256 > 192)))) {
+      (persistent && ((q.K >= 2048 && t256 > 128) || (q.K >= 1024 && t256 > 192) ||
+                      (q.K >= 12288 && t256 >= 40 && (t256 <= 96 || q.K >= 32768))))) {
     *variant = VT_VARIANT_MFMA_256x256;
   } else {
     // Whole 256x128 tiles run on the persistent kernel's 256x128 form, which
@@ -2404,10 +2410,13 @@ int select_variant(const Problem &q, bool vec, int32_t *variant, int32_t *k_spli
     // K >= 1024 (M x N: 1280 x 4096, K = 1024 12.8 us against 14.0, K = 4096
     // 29.8 against 37.3; 2560 x 2048, K = 2048 18.5 against 22.0; 768 x 8192,
     // K = 2048 19.5 against 23.3; 512 x 14336, K = 2048 20.8 against 24.6),
-    // but not at half a round or less (1024 x 4096 x 4096: 28.8 against 25.2).
+    // but not at half a round or less (1024 x 4096 x 4096: 28.8 against 25.2),
+    // except at 48-64 tiles from K = 12288, K split in four (768 x 2048 x
+    // 16384 37.2 against 45.6; 1024 x 2048 x 32768 71.6 against 88.1).
     const bool whole128 = m_eff % 256 == 0 && q.N % 128 == 0 && q.K % 256 == 0;
     const bool wide = (q.K >= 2048 && (t128 >= 256 || (q.K >= 4096 && t128 >= 192))) ||
-                      (whole128 && q.K >= 1024 && t128 > 128 && t128 <= 256);
+                      (whole128 && q.K >= 1024 && t128 > 128 && t128 <= 256) ||
+                      (whole128 && q.K >= 12288 && t128 >= 48 && t128 <= 64);
     *variant = (wide && m_eff >= 256) ? VT_VARIANT_MFMA_256x128 : VT_VARIANT_MFMA_128x128;
   }
   return VT_OK;
