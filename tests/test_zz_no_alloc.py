@@ -71,6 +71,10 @@ PAIRS = [
     # 64x64 tiles with K in 4 (then 2) slices: 1 MiB, then 512 KiB of scratch
     ("256x256 column split", (4096, 4112, 4096, "mfma_256x256", 0, True),
      (4096, 4112, 1024, "mfma_256x256", 0, False)),
+    # the persistent kernel's 256x128 form with K in 8 (then 4) slices as
+    # batches into the partials: 16 MiB, then 13.5 MiB of scratch
+    ("256x128 form k-split", (512, 1024, 4096, "mfma_256x128", 0, True),
+     (768, 1152, 2048, "mfma_256x128", 0, False)),
 ]
 
 
