@@ -7,8 +7,8 @@ aligned C and D run persistently, one workgroup per CU, each wave computing a
 These cases check every output: one tile, a grid with several tiles per
 workgroup, more tiles than CUs, D out of place and in place, D + A.B wrapping
 past int32 through the raw C ABI, K split into slices summed by the reduction
-kernel, unshared and shared-B batches, the int8 extremes, and a row stride
-wider than N. Ragged shapes, and K not a multiple of 256, stay on
+kernel, unshared and shared-B batches, the int8 extremes, a row stride
+wider than N, and graph replays (unsplit and K-split). Ragged shapes, and K not a multiple of 256, stay on
 gemm_mfma_kernel<256, 128> (checked here through the host model only).
 """
 import numpy as np
@@ -151,3 +151,40 @@ def test_ragged_and_short_k_shapes_stay_on_the_tiled_kernel():
     for m, n, k in ((300, 384, 1024), (512, 208, 1024), (512, 384, 320), (512, 384, 1088)):
         plan = hg.make_plan(m, n, k, variant="mfma_256x128")
         assert not persistent(plan), (m, n, k)
+
+
+@pytest.mark.parametrize("m,n,k,ks", [(1536, 4096, 1024, 1), (512, 1024, 4096, 8)])
+def test_256x128_form_in_graph_replays(dev, m, n, k, ks):
+    """The form captured in a HIP graph, unsplit and with K slices through the
+    stream's workspace (sized by an eager call first), C = D + A.B: every
+    replay, with eager work and a poisoned C between replays, equals the
+    eager result."""
+    plan = hg.make_plan(m, n, k, has_d=True, d_max_abs=2**20, variant="mfma_256x128")
+    assert persistent(plan) and hg.mfma_k_split(plan) == ks
+    rng = np.random.default_rng(m + n + k)
+    A = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    B = rng.integers(-128, 128, (k, n), dtype=np.int8)
+    D = rng.integers(-2**20, 2**20, (m, n), dtype=np.int32)
+    want = go.gemm_i8(A, B, D)
+    At, Bt, Dt = to_dev(dev, A), to_dev(dev, B), to_dev(dev, D)
+    s = torch.cuda.Stream(dev)
+    outs = [torch.full((m, n), -2**31, dtype=torch.int32, device=dev) for _ in range(3)]
+    say("256x128 graph", m, n, k, ks)
+    with torch.cuda.stream(s):
+        hg.run(plan, At, Bt, Dt, out=outs[0], stream=s.cuda_stream)
+    s.synchronize()
+    assert np.array_equal(outs[0].cpu().numpy(), want)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for C in outs[1:]:
+            hg.run(plan, At, Bt, Dt, out=C, stream=s.cuda_stream)
+    for rep in range(3):
+        for C in outs[1:]:
+            C.fill_(-2**31)
+        scratch = torch.matmul(Dt[:64, :64].float(), Dt[:64, :64].float())   # eager work between
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert scratch.shape == (64, 64)
+        for C in outs[1:]:
+            assert np.array_equal(C.cpu().numpy(), want), rep
