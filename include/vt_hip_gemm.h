@@ -70,9 +70,9 @@ extern "C" {
 #define VT_VARIANT_SKINNY 3        /* M <= 64 decode shapes: B streamed once,
                                       v_mfma_i32_16x16x64_i8, K split         */
 #define VT_VARIANT_GENERIC 4       /* any shape/stride/alignment, VALU        */
-#define VT_VARIANT_MFMA_256x128 5  /* 256x128 tile, 4 waves; whole tiles with
-                                      K % 256 == 0 and 16-byte aligned C, D run
-                                      persistently (one workgroup per CU)     */
+#define VT_VARIANT_MFMA_256x128 5  /* 256x128 tile, 4 waves; M >= 256, N >= 128,
+                                      K % 256 == 0 with 16-byte aligned C, D
+                                      run persistently (one workgroup per CU) */
 #define VT_VARIANT_PADDED 6        /* any shape: A and B copied with K and N
                                       zero-padded to multiples of 16, run on
                                       the MFMA / skinny kernels, C copied out
@@ -220,7 +220,7 @@ int vt_gemm_select(int64_t M, int64_t N, int64_t K, int64_t batch,
  * of their tile kernel (three 64-deep slice buffers of A and B); the
  * persistent 256x256 kernels, one workgroup per CU, take 160 KiB (K % 256 == 0
  * with 16-byte C and D rows) or 128 KiB, and so does the persistent form of
- * 256x128 (160 KiB; whole tiles, K % 256 == 0, 16-byte C and D rows). The
+ * 256x128 (160 KiB; M >= 256, N >= 128, K % 256 == 0, 16-byte C and D rows). The
  * skinny figure excludes the A slice, which depends on K and the split.
  */
 int vt_variant_info(int32_t variant, int32_t *tile_m, int32_t *tile_n,

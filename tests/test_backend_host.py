@@ -236,7 +236,7 @@ def test_mfma_k_split_mirrors_the_native_choice():
             assert hg.mfma_tiles(plan) == tiles
             persistent = (variant == "mfma_256x256" and m >= 256 and n >= 256 and
                           (k // want) % 64 == 0) or \
-                (variant == "mfma_256x128" and m % 256 == 0 and n % 128 == 0 and
+                (variant == "mfma_256x128" and m >= 256 and n >= 128 and
                  (k // want) % 256 == 0)
             # the persistent kernel: one workgroup per CU, 160 KiB (K slice % 256
             # == 0) or 128 KiB of LDS; the tile kernel: a workgroup per tile
@@ -300,8 +300,9 @@ def test_mfma_row_split_mirrors_the_native_choice():
 def test_mfma_selection_follows_the_measured_sweep():
     """The automatic choice among the MFMA tile shapes, on shapes whose three
     variants were timed on the GPU: the measured fastest (ties within 1 % take
-    either). Moving a threshold of select_variant fails here. Whole 256x128
-    tiles run on the persistent kernel's 256x128 form."""
+    either). Moving a threshold of select_variant fails here. 256x128 tiles
+    (M >= 256, N >= 128, K % 256 == 0; the last ones moved back when M or N
+    is ragged) run on the persistent kernel's 256x128 form."""
     from veritac_amd import _lib
     either = ("mfma_128x128", "mfma_256x128")
     fastest = {
@@ -322,6 +323,9 @@ def test_mfma_selection_follows_the_measured_sweep():
         (512, 8192, 16384): "mfma_256x256", (2048, 4096, 32768): "mfma_256x256",
         (2048, 4096, 16384): either, (768, 2048, 16384): "mfma_256x128",
         (1024, 2048, 32768): "mfma_256x128", (512, 2048, 16384): "mfma_128x128",
+        (1200, 4096, 1024): "mfma_256x128", (500, 14336, 2048): "mfma_256x128",
+        (1800, 2048, 2048): "mfma_128x128", (2000, 4096, 4096): "mfma_256x128",
+        (3000, 4096, 4096): "mfma_256x256",
     }
     for (m, n, k), want in fastest.items():
         want = (want,) if isinstance(want, str) else want

@@ -1,15 +1,17 @@
 """The 256x128 form of the persistent 16x16x64 kernel against the oracle,
 through the C ABI (needs a gfx950 GPU).
 
-mfma_256x128 problems of whole 256x128 tiles, K a multiple of 256 and 16-byte
+mfma_256x128 problems with M >= 256, N >= 128, K a multiple of 256 and 16-byte
 aligned C and D run persistently, one workgroup per CU, each wave computing a
 128x64 block from direct-to-LDS slices and storing C through its LDS strip.
 These cases check every output: one tile, a grid with several tiles per
 workgroup, more tiles than CUs, D out of place and in place, D + A.B wrapping
 past int32 through the raw C ABI, K split into slices summed by the reduction
 kernel, unshared and shared-B batches, the int8 extremes, a row stride
-wider than N, and graph replays (unsplit and K-split). Ragged shapes, and K not a multiple of 256, stay on
-gemm_mfma_kernel<256, 128> (checked here through the host model only).
+wider than N, graph replays (unsplit and K-split), and ragged M and N (last
+tiles moved back, shared rows and columns stored once). M below 256, N below
+128 and K not a multiple of 256 stay on gemm_mfma_kernel<256, 128> (checked
+here through the host model only).
 """
 import numpy as np
 import pytest
@@ -146,9 +148,49 @@ def test_256x128_form_with_wide_rows(dev):
     assert (got[:, n:] == -5).all()   # columns past N untouched
 
 
-def test_ragged_and_short_k_shapes_stay_on_the_tiled_kernel():
-    """Host model: the 256x128 form needs whole tiles and K % 256 == 0."""
-    for m, n, k in ((300, 384, 1024), (512, 208, 1024), (512, 384, 320), (512, 384, 1088)):
+# m, n, k, K slices: the last tile row and/or column moved back to end at M
+# or N, its shared rows and columns stored by the neighbour alone
+RAGGED = [
+    (300, 384, 1024, 2),      # M ragged (2 tile rows overlapping by 212), K split
+    (2000, 4096, 512, 1),     # M ragged, 256 tiles
+    (512, 4000, 768, 1),      # N ragged (32 columns past a whole tile)
+    (1100, 1040, 2048, 4),    # both ragged, K split
+    (256, 144, 256, 1),       # one tile row, N one tile plus 16 columns
+]
+
+
+@pytest.mark.parametrize("m,n,k,ks", RAGGED)
+def test_256x128_form_on_ragged_shapes(dev, m, n, k, ks):
+    """Moved-back last tiles: every element of C written once (a poisoned C
+    outside M x N stays poisoned), with and without D, in place."""
+    plan = hg.make_plan(m, n, k, variant="mfma_256x128")
+    assert persistent(plan) and hg.mfma_k_split(plan) == ks
+    rng = np.random.default_rng(m * 3 + n + k)
+    A = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    B = rng.integers(-128, 128, (k, n), dtype=np.int8)
+    D = rng.integers(-2**20, 2**20, (m, n), dtype=np.int32)
+    At, Bt = to_dev(dev, A), to_dev(dev, B)
+    say("256x128 ragged", m, n, k, ks)
+    assert np.array_equal(hg.run(plan, At, Bt).cpu().numpy(), go.gemm_i8(A, B, None))
+    plan_d = hg.make_plan(m, n, k, has_d=True, d_max_abs=2**20, variant="mfma_256x128")
+    want = go.gemm_i8(A, B, D)
+    assert np.array_equal(hg.run(plan_d, At, Bt, to_dev(dev, D)).cpu().numpy(), want)
+    C = to_dev(dev, D)
+    assert np.array_equal(hg.run(plan_d, At, Bt, C, out=C).cpu().numpy(), want)   # in place: D once
+    # C inside a wider buffer: the columns past N keep their poison
+    ldc = n + 64
+    Cw = torch.full((m, ldc), -7, dtype=torch.int32, device=dev)
+    _lib.gemm_raw(At.data_ptr(), Bt.data_ptr(), None, Cw.data_ptr(), m, n, k, k, n, ldc, ldc,
+                  1, 0, 0, 0, 0, "mfma_256x128", 0, None)
+    _lib.sync(None)
+    got = Cw.cpu().numpy()
+    assert np.array_equal(got[:, :n], go.gemm_i8(A, B, None))
+    assert (got[:, n:] == -7).all()
+
+
+def test_short_k_and_small_shapes_stay_on_the_tiled_kernel():
+    """Host model: the 256x128 form needs M >= 256, N >= 128 and K % 256 == 0."""
+    for m, n, k in ((200, 384, 1024), (512, 112, 1024), (512, 384, 320), (512, 384, 1088)):
         plan = hg.make_plan(m, n, k, variant="mfma_256x128")
         assert not persistent(plan), (m, n, k)
 

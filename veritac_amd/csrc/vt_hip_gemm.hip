@@ -988,17 +988,20 @@ __device__ __forceinline__ void store_tile16_lds(const v4i (&acc)[MI][NI], int32
   }
 }
 
-// One 16-row strip of the 256x128 form's epilogue (whole tiles): the wave's
-// 64 columns go through its LDS strip and out as 4 stores, each of four whole
-// 256-byte row segments. wb / rb: strip64_wb / strip64_rb plus the strip's
-// offset in LDS; gofs_c / gofs_d: the lane's byte offset from its 4-row
-// group's base. With D, the strip's 4 D loads precede its stores, and each
-// lane reads its own D bytes before writing them, so C may be D.
-template <bool HAS_D>
+// One 16-row strip of the 256x128 form's epilogue: the wave's 64 columns go
+// through its LDS strip and out as 4 stores, each of four whole 256-byte row
+// segments. wb / rb: strip64_wb / strip64_rb plus the strip's offset in LDS;
+// gofs_c / gofs_d: the lane's byte offset from its 4-row group's base. With
+// D, the strip's 4 D loads precede its stores, and each lane reads its own D
+// bytes before writing them, so C may be D. MASKED: store j of a lane writes
+// only when row_rel + 4 j >= 0 and col_ok (a moved-back tile leaves the rows
+// and columns it shares with its neighbour to the neighbour).
+template <bool HAS_D, bool MASKED = false>
 __device__ __forceinline__ void store_strip64_lds(const v4i (&acc)[4], int32_t *Cs, const int32_t *Ds,
                                                   int64_t ldc, int64_t ldd, const int (&wb)[4],
                                                   const int (&rb)[4], uint32_t gofs_c, uint32_t gofs_d,
-                                                  LDS_AS int8_t *lds) {
+                                                  LDS_AS int8_t *lds, int row_rel = 0,
+                                                  bool col_ok = true) {
 #pragma unroll
   for (int ni = 0; ni < 4; ++ni)
 #pragma unroll
@@ -1014,10 +1017,17 @@ __device__ __forceinline__ void store_strip64_lds(const v4i (&acc)[4], int32_t *
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int q = 0; q < 4; ++q) v[j][q] = add_wrap(v[j][q], d[j][q]);
+    // Masked: the sums are formed before the conditional stores (as in
+    // store_strip16_lds), so no masked lane's D load stays outstanding.
+    if constexpr (MASKED) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) asm volatile("" : "+v"(v[j]));
+    }
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j)
-    __builtin_nontemporal_store(v[j], (v4i *)((int8_t *)(Cs + 4 * j * ldc) + gofs_c));
+    if (!MASKED || (col_ok && row_rel + 4 * j >= 0))
+      __builtin_nontemporal_store(v[j], (v4i *)((int8_t *)(Cs + 4 * j * ldc) + gofs_c));
 }
 
 // v_mfma_i32_16x16x64_i8 accumulating in place in AGPRs. As a builtin, the
@@ -1052,9 +1062,9 @@ __device__ __forceinline__ void mfma16_in_place(v4i &acc, const v4i &a, const v4
 // MFMAs.
 template <bool HAS_D, bool PACKED_B, bool EDGE = false, int BN = 256>
 __global__ __launch_bounds__(256, 1) void gemm_dma16_kernel(GemmArgs p) {
-  // BN = 128 (the 256x128 form: whole tiles, row-major B) gives each wave a
-  // 128x64 block and half the B slice; the rest is shared.
-  static_assert(BN == 256 || (BN == 128 && !PACKED_B && !EDGE), "256x128: whole tiles, row-major B");
+  // BN = 128 (the 256x128 form, row-major B) gives each wave a 128x64 block
+  // and half the B slice; the rest is shared.
+  static_assert(BN == 256 || (BN == 128 && !PACKED_B), "256x128: row-major B");
   constexpr int BM = 256, BK = 64;
   constexpr int WTM = 128, WTN = BN / 2, MI = WTM / 16, NI = WTN / 16;
   constexpr int A_BYTES = BM * BK, B_BYTES = BK * BN;
@@ -1347,10 +1357,16 @@ __global__ __launch_bounds__(256, 1) void gemm_dma16_kernel(GemmArgs p) {
     } else {
       const int32_t *d_tile =
           HAS_D ? p.D + bidx * p.sd + (int64_t)(m0 + wm * WTM) * p.ldd + n0 + wn * WTN : nullptr;
+      // EDGE: the lane's row in the wave's first strip (4 j + lane / 16 for
+      // store j) less the rows the tile leaves to its neighbour, and whether
+      // its 4 columns are past the neighbour's.
+      const int row_rel0 = wm * WTM + (lane >> 4) - (mn - m0);
+      const bool col_ok = wn * WTN + (lane & 15) * 4 >= nn - n0;
 #pragma unroll
       for (int mi = 0; mi < MI; ++mi) {
-        store_strip64_lds<HAS_D>(acc[mi], c_tile + mi * 16 * p.ldc, HAS_D ? d_tile + mi * 16 * p.ldd : nullptr,
-                                 p.ldc, p.ldd, wb64, rb64, gofs64, gofs64_d, lds);
+        store_strip64_lds<HAS_D, EDGE>(acc[mi], c_tile + mi * 16 * p.ldc,
+                                       HAS_D ? d_tile + mi * 16 * p.ldd : nullptr, p.ldc, p.ldd, wb64,
+                                       rb64, gofs64, gofs64_d, lds, row_rel0 + mi * 16, col_ok);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -2405,18 +2421,20 @@ int select_variant(const Problem &q, bool vec, int32_t *variant, int32_t *k_spli
                       (q.K >= 12288 && t256 >= 40 && (t256 <= 96 || q.K >= 32768))))) {
     *variant = VT_VARIANT_MFMA_256x256;
   } else {
-    // Whole 256x128 tiles run on the persistent kernel's 256x128 form, which
-    // wins over 128x128 tiles from more than half a round of its tiles at
-    // K >= 1024 (M x N: 1280 x 4096, K = 1024 12.8 us against 14.0, K = 4096
-    // 29.8 against 37.3; 2560 x 2048, K = 2048 18.5 against 22.0; 768 x 8192,
-    // K = 2048 19.5 against 23.3; 512 x 14336, K = 2048 20.8 against 24.6),
-    // but not at half a round or less (1024 x 4096 x 4096: 28.8 against 25.2),
-    // except at 48-64 tiles from K = 12288, K split in four (768 x 2048 x
-    // 16384 37.2 against 45.6; 1024 x 2048 x 32768 71.6 against 88.1).
-    const bool whole128 = m_eff % 256 == 0 && q.N % 128 == 0 && q.K % 256 == 0;
+    // M >= 256, N >= 128 and K % 256 == 0 run on the persistent kernel's
+    // 256x128 form, which wins over 128x128 tiles from more than half a round
+    // of its tiles at K >= 1024 (M x N: 1280 x 4096, K = 1024 12.8 us against
+    // 14.0, K = 4096 29.8 against 37.3; 2560 x 2048, K = 2048 18.5 against
+    // 22.0; 768 x 8192, K = 2048 19.5 against 23.3; 512 x 14336, K = 2048 20.8
+    // against 24.6; ragged: 1200 x 4096 x 1024 12.6 against 14.2, 500 x 14336
+    // x 2048 21.4 against 24.2), but not at half a round or less (1024 x 4096
+    // x 4096: 28.8 against 25.2), except at 48-64 tiles from K = 12288, K
+    // split in four (768 x 2048 x 16384 37.2 against 45.6; 1024 x 2048 x
+    // 32768 71.6 against 88.1).
+    const bool form128 = m_eff >= 256 && q.N >= 128 && q.K % 256 == 0;
     const bool wide = (q.K >= 2048 && (t128 >= 256 || (q.K >= 4096 && t128 >= 192))) ||
-                      (whole128 && q.K >= 1024 && t128 > 128 && t128 <= 256) ||
-                      (whole128 && q.K >= 12288 && t128 >= 48 && t128 <= 64);
+                      (form128 && q.K >= 1024 && t128 > 128 && t128 <= 256) ||
+                      (form128 && q.K >= 12288 && t128 >= 48 && t128 <= 64);
     *variant = (wide && m_eff >= 256) ? VT_VARIANT_MFMA_256x128 : VT_VARIANT_MFMA_128x128;
   }
   return VT_OK;
@@ -2445,13 +2463,15 @@ bool use_dma16(const Problem &r) {
   return r.K % 256 == 0 && c_ok && d_ok;
 }
 
-// Row-major problems of whole 256x128 tiles run on the 256x128 form of
-// gemm_dma16_kernel (persistent, one workgroup per CU) when its 16-byte C and
-// D accesses are aligned; it addresses a lane's 16 bytes from its 4-row
-// group's base (three rows of ldc or ldd plus 256 bytes) as a 32-bit byte
-// offset. Otherwise gemm_mfma_kernel<256, 128> takes them.
+// Row-major problems of M >= 256 and N >= 128 run on the 256x128 form of
+// gemm_dma16_kernel (persistent, one workgroup per CU; a last tile row or
+// column past M or N moved back to end there, its EDGE instantiation storing
+// only what its neighbour does not) when its 16-byte C and D accesses are
+// aligned; it addresses a lane's 16 bytes from its 4-row group's base (three
+// rows of ldc or ldd plus 256 bytes) as a 32-bit byte offset. Otherwise
+// gemm_mfma_kernel<256, 128> takes them.
 bool dma16_128_fits(const Problem &r) {
-  return r.K > 0 && r.M % 256 == 0 && r.N % 128 == 0 && r.ldc < (1ll << 28) &&
+  return r.K > 0 && r.M >= 256 && r.N >= 128 && r.ldc < (1ll << 28) &&
          (!r.D || r.ldd < (1ll << 28)) && use_dma16(r);
 }
 
@@ -2732,8 +2752,12 @@ int launch_mfma_tiles(const Problem &r, hipStream_t stream, int num_cus) {
   }
   if (!PACKED && BM == 256 && BN == 128 && dma16_128_fits(r)) {
     const int64_t g = blocks < num_cus ? blocks : num_cus;
-    if (has_d) hipLaunchKernelGGL((gemm_dma16_kernel<true, false, false, 128>), dim3((unsigned)g), dim3(256), 0, stream, a);
-    else hipLaunchKernelGGL((gemm_dma16_kernel<false, false, false, 128>), dim3((unsigned)g), dim3(256), 0, stream, a);
+    const dim3 pgrid((unsigned)g);
+    const bool edge = r.M % BM || r.N % BN;
+    if (edge && has_d) hipLaunchKernelGGL((gemm_dma16_kernel<true, false, true, 128>), pgrid, dim3(256), 0, stream, a);
+    else if (edge) hipLaunchKernelGGL((gemm_dma16_kernel<false, false, true, 128>), pgrid, dim3(256), 0, stream, a);
+    else if (has_d) hipLaunchKernelGGL((gemm_dma16_kernel<true, false, false, 128>), pgrid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((gemm_dma16_kernel<false, false, false, 128>), pgrid, dim3(256), 0, stream, a);
     VT_HIP_CHECK(hipGetLastError());
     return VT_OK;
   }

@@ -415,7 +415,7 @@ def _runs_persistent(plan):
     the persistent kernel: each K slice in whole 64-deep steps and M (after
     the fold) and N at least one tile (persistent_fits in the HIP source).
     An mfma_256x128 plan runs on the persistent kernel's 256x128 form when M
-    (after the fold) and N are whole 256x128 tiles and each K slice is whole
+    (after the fold) is at least 256, N at least 128 and each K slice whole
     256-deep groups (dma16_128_fits; plans assume 16-byte aligned C and D
     with rows of n elements)."""
     if plan["variant"] not in ("mfma_256x256", "mfma_256x128"):
@@ -423,7 +423,7 @@ def _runs_persistent(plan):
     m = plan["m"] * plan["batch"] if plan["b_shared"] and plan["batch"] > 1 else plan["m"]
     kslice = plan["k"] // mfma_k_split(plan)
     if plan["variant"] == "mfma_256x128":
-        return kslice > 0 and kslice % 256 == 0 and m % 256 == 0 and plan["n"] % 128 == 0
+        return kslice > 0 and kslice % 256 == 0 and m >= 256 and plan["n"] >= 128
     return kslice > 0 and kslice % 64 == 0 and m >= 256 and plan["n"] >= 256
 
 
