@@ -578,7 +578,7 @@ SHAPE_SWEEP = [(m, 14336, 4096) for m in (1, 16, 32, 48, 64, 96, 128, 256)] + \
     [(8000, 8192, 8192), (4000, 14336, 4096), (1100, 14336, 4096), (5000, 5120, 5120),
      (2000, 8192, 4096), (3000, 4096, 4096), (1100, 8192, 8192)] + \
     [(1536, 4096, 4096), (2048, 4096, 4096), (1536, 4096, 8192), (1280, 4096, 1024),
-     (768, 8192, 2048), (512, 14336, 2048)]
+     (768, 8192, 2048), (512, 14336, 2048), (2000, 4096, 4096), (500, 14336, 2048)]
 
 
 def bench_shapes(dev, launches=40):
