@@ -239,8 +239,9 @@ def mfma_k_split(plan):
     """K slices vt_gemm_i8 runs an MFMA plan in (mfma_split_for in the HIP
     source): a k of at least 1024 over at most 64 of the tiles the plan runs
     (contiguous shared-B batches folded into m) is cut into up to 16 slices of
-    whole 128-deep steps, each at least 512 deep, for up to 256 workgroups;
-    the partial sums are added by a second kernel. 1: no split."""
+    whole 128-deep steps, each at least 512 deep, for up to 256 workgroups
+    (from k = 8192, into two over 65..128 tiles); the partial sums are added
+    by a second kernel. 1: no split."""
     variant = plan["variant"]
     if not variant.startswith("mfma"):
         return 1
