@@ -1059,7 +1059,8 @@ __device__ __forceinline__ void mfma16_in_place(v4i &acc, const v4i &a, const v4
 // (vmcnt(DMAS): only slice gs + 3's DMAs may remain) plus the barrier publish
 // slice gs + 2, whose fragments step gs + 1 reads. Stage gs % 4 is refilled in
 // step gs + 1; its reads were issued in step gs - 1 and consumed by step gs's
-// MFMAs.
+// MFMAs. The 256x128 form (BN = 128) runs the same schedule over 32 slots,
+// with 6 DMAs per slice issued one every 4 slots.
 template <bool HAS_D, bool PACKED_B, bool EDGE = false, int BN = 256>
 __global__ __launch_bounds__(256, 1) void gemm_dma16_kernel(GemmArgs p) {
   // BN = 128 (the 256x128 form, row-major B) gives each wave a 128x64 block
