@@ -99,12 +99,14 @@ KERNELS16 = {"no_d": _k16(0, 0), "with_d": _k16(1, 0), "packed_b": _k16(0, 1),
              "packed_b_with_d": _k16(1, 1), "edge": _k16(0, 0, 1), "edge_with_d": _k16(1, 0, 1),
              "packed_b_edge": _k16(0, 1, 1), "packed_b_edge_with_d": _k16(1, 1, 1),
              "bn128": _k16(0, 0, 0, 128), "bn128_with_d": _k16(1, 0, 0, 128),
-             "bn128_edge": _k16(0, 0, 1, 128), "bn128_edge_with_d": _k16(1, 0, 1, 128)}
+             "bn128_edge": _k16(0, 0, 1, 128), "bn128_edge_with_d": _k16(1, 0, 1, 128),
+             "bn128_packed": _k16(0, 1, 0, 128), "bn128_packed_with_d": _k16(1, 1, 0, 128),
+             "bn128_packed_edge": _k16(0, 1, 1, 128), "bn128_packed_edge_with_d": _k16(1, 1, 1, 128)}
 # kinds whose tile's last k iteration is peeled to store early strips: no D,
 # and all tiles whole (the edge kinds mask their stores after the loop)
 EARLY16 = {"no_d", "packed_b"}
 # the 256x128 form: 4 A and 2 B DMAs per wave per slice, 8 x 4 MFMAs per step
-BN128 = {"bn128", "bn128_with_d", "bn128_edge", "bn128_edge_with_d"}
+BN128 = {k for k in KERNELS16 if k.startswith("bn128")}
 
 
 def dmas_per_slice(kind):

@@ -474,3 +474,40 @@ def test_packed_finish_repeated_and_mixed(dev):
             At, Bt = to_dev(dev, A), to_dev(dev, B)
             got = hg.run(hg.make_plan(m, n, k), At, Bt).cpu().numpy()
         assert np.array_equal(got, go.gemm_i8(A, B, None)), it
+
+
+# Packed B on the persistent kernel's 256x128 form (more than 128 but at most
+# 256 tiles of 256x128, K >= 1024 in whole 256-deep groups, N in whole
+# 128-column tiles): whole and ragged M, D out of place and in place.
+@pytest.mark.parametrize("m,k,n", [(1536, 1024, 4096), (2000, 1024, 4096), (512, 2048, 14336),
+                                   (1280, 1280, 4096)])
+def test_packed_b_on_the_256x128_form(dev, m, k, n):
+    plan = hg.make_plan(m, n, k, variant=hg.PACKED_VARIANT)
+    assert hg.packed_dma128(plan)
+    rng = np.random.default_rng(m + k + n)
+    A = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    B = rng.integers(-128, 128, (k, n), dtype=np.int8)
+    D = rng.integers(-2**20, 2**20, (m, n), dtype=np.int32)
+    say("packed 256x128 form", m, k, n)
+    assert np.array_equal(gpu_gemm_packed(dev, A, B), go.gemm_i8(A, B, None))
+    want = go.gemm_i8(A, B, D)
+    assert np.array_equal(gpu_gemm_packed(dev, A, B, D), want)
+    assert np.array_equal(gpu_gemm_packed(dev, A, B, D, in_place=True), want)
+
+
+@pytest.mark.parametrize("shared", [True, False])
+def test_packed_b_on_the_256x128_form_batches(dev, shared):
+    """Two batches of 768 x 4096 (192 tiles in all), one packed B for both or
+    one each, with D."""
+    rng = np.random.default_rng(77 + shared)
+    batch, m, k, n = 2, 768, 1024, 4096
+    A = rng.integers(-128, 128, (batch, m, k), dtype=np.int8)
+    B = rng.integers(-128, 128, (k, n) if shared else (batch, k, n), dtype=np.int8)
+    D = rng.integers(-1000, 1000, (batch, m, n), dtype=np.int32)
+    plan = hg.make_plan(m, n, k, batch=batch, b_shared=shared, has_d=True, d_max_abs=1000,
+                        variant=hg.PACKED_VARIANT)
+    assert hg.packed_dma128(plan)
+    say("packed 256x128 form batches", shared)
+    C = hg.run(plan, to_dev(dev, A), hg.pack_b(to_dev(dev, B)), to_dev(dev, D)).cpu().numpy()
+    for b in range(batch):
+        assert np.array_equal(C[b], go.gemm_i8(A[b], B if shared else B[b], D[b])), b

@@ -150,11 +150,20 @@ def test_packed_rows_in_whole_tiles_go_to_the_256_kernel():
     t_packed = hg.modeled_objective(big, hg.modeled_counts(big))[0]
     row = hg.make_plan(8192, 8192, 8192, variant="mfma_256x256")
     assert t_packed == pytest.approx(hg.modeled_objective(row, hg.modeled_counts(row))[0])
-    # 512 x 14336 x 4096 packed is modeled as the row-major 128x128 plan
+    # 512 x 14336 x 4096 packed (224 tiles of 256x128) runs whole on the
+    # persistent 256x128 form and is modeled as the row-major plan on it
     mid = plan(512, 14336, 4096)
-    row = hg.make_plan(512, 14336, 4096, variant="mfma_128x128")
+    assert hg.packed_dma128(mid)
+    row = hg.make_plan(512, 14336, 4096, variant="mfma_256x128")
     assert hg.modeled_objective(mid, hg.modeled_counts(mid)) == pytest.approx(
         hg.modeled_objective(row, hg.modeled_counts(row)))
+    assert hg.required_resources(mid) == (hg.DMA16_LDS, 224)
+    assert "512 rows on the 256x128 persistent kernel" in hg.native_check(mid)[1]
+    # 128 such tiles or fewer, K below 1024 or N not whole 128-column tiles:
+    # the routes above
+    for m, n, k in ((1024, 4096, 4096), (1536, 4096, 512), (1536, 4000, 4096), (200, 14336, 4096)):
+        assert not hg.packed_dma128(plan(m, n, k)), (m, n, k)
+    assert hg.packed_dma128(plan(2000, 4096, 4096))          # ragged M: last tile row moved back
 
 
 def test_run_refuses_mismatched_packed_operands():

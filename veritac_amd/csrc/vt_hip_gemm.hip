@@ -1063,9 +1063,9 @@ __device__ __forceinline__ void mfma16_in_place(v4i &acc, const v4i &a, const v4
 // with 6 DMAs per slice issued one every 4 slots.
 template <bool HAS_D, bool PACKED_B, bool EDGE = false, int BN = 256>
 __global__ __launch_bounds__(256, 1) void gemm_dma16_kernel(GemmArgs p) {
-  // BN = 128 (the 256x128 form, row-major B) gives each wave a 128x64 block
-  // and half the B slice; the rest is shared.
-  static_assert(BN == 256 || (BN == 128 && !PACKED_B), "256x128: row-major B");
+  // BN = 128 (the 256x128 form) gives each wave a 128x64 block and half the
+  // B slice; the rest is shared.
+  static_assert(BN == 256 || BN == 128, "256x256 or 256x128 tiles");
   constexpr int BM = 256, BK = 64;
   constexpr int WTM = 128, WTN = BN / 2, MI = WTM / 16, NI = WTN / 16;
   constexpr int A_BYTES = BM * BK, B_BYTES = BK * BN;
@@ -1123,7 +1123,8 @@ __global__ __launch_bounds__(256, 1) void gemm_dma16_kernel(GemmArgs p) {
     const int ac = (lane & 3) ^ a16_swz(arow);
     a_lane[i] = (uint32_t)((int64_t)arow * lda + ac * 16);
     if constexpr (PACKED_B) {
-      b_lane[i] = (uint32_t)((int64_t)(wave * DPW + i) * ldb * 1024 + lane * 16);
+      // whole 1 KB tiles of column blocks wave * DPW_B + i
+      b_lane[i] = i < DPW_B ? (uint32_t)((int64_t)(wave * DPW_B + i) * ldb * 1024 + lane * 16) : 0;
     } else if constexpr (BN == 256) {
       const int brow = (wave * DPW + i) * 4 + (lane >> 4);
       const int bc = (lane & 15) ^ b16_swz(brow);
@@ -3004,6 +3005,49 @@ int launch_packed_dma(const Problem &q, int64_t rows, hipStream_t stream, int nu
   return VT_OK;
 }
 
+// A packed-B GEMM runs whole on the 256x128 form of the persistent kernel
+// when the 256x256 kernel does not take it (packed_dma_rows == 0), K >= 1024
+// and there are more than 128 but at most 256 tiles of 256x128 (over all
+// batches), as for row-major B; it needs M >= 256 (a partial last tile row
+// moved back), N in whole 128-column tiles, K in whole 256-deep groups,
+// 16-byte C and D rows, and every lane offset from a tile's base within 32
+// bits (A: 256 rows of lda; packed B: 8 column blocks of kbt 1 KB tiles).
+// Against the 128x128 packed tiles it replaced there (HIP graphs, one box):
+// 1536 x 4096 x 4096 30.9 us against 36.4, 1536 x 4096 x 8192 55.1 against
+// 67.7, 512 x 14336 x 4096 32.4 against 40.5, 2000 x 4096 x 4096 35.8
+// against 43.6; at 128 tiles or fewer it lost (1024 x 4096 x 4096 28.1
+// against 25.4, 300 x 4096 x 4096 27.1 against 20.7).
+bool packed_dma128_fits(const Problem &q) {
+  if (!(q.M >= 256 && q.N % 128 == 0 && q.K % 256 == 0 && q.K >= 1024 &&
+        256 * q.lda < (1ll << 32) - 4096 && 8 * 1024 * packed_kbt(q.K) < (1ll << 32) - 4096 &&
+        q.ldc < (1ll << 28) && (!q.D || q.ldd < (1ll << 28)) && use_dma16(q)))
+    return false;
+  const int64_t tiles = (q.M + 255) / 256 * (q.N / 128) * q.batch;
+  return tiles > 128 && tiles <= 256;
+}
+
+int launch_packed_dma128(const Problem &q, hipStream_t stream, int num_cus) {
+  GemmArgs a;
+  a.A = q.A; a.B = q.B; a.D = q.D; a.C = q.C;
+  a.lda = q.lda; a.ldb = packed_kbt(q.K); a.ldd = q.ldd; a.ldc = q.ldc;
+  a.sa = q.sa; a.sb = q.sb; a.sd = q.sd; a.sc = q.sc;
+  a.M = (int)q.M; a.N = (int)q.N; a.K = (int)q.K;
+  a.tiles_m = (a.M + 255) / 256;
+  a.tiles_n = a.N / 128;
+  a.group_m = 4;
+  a.batch_count = (int)q.batch;
+  const int64_t blocks = (int64_t)a.tiles_m * a.tiles_n * q.batch;
+  if (blocks > 0x7fffffff) return fail(VT_EUNSUPPORTED, "grid of %lld tiles too large", (long long)blocks);
+  const dim3 pgrid((unsigned)(blocks < num_cus ? blocks : num_cus));
+  const bool edge = q.M % 256 != 0;
+  if (edge && q.D) hipLaunchKernelGGL((gemm_dma16_kernel<true, true, true, 128>), pgrid, dim3(256), 0, stream, a);
+  else if (edge) hipLaunchKernelGGL((gemm_dma16_kernel<false, true, true, 128>), pgrid, dim3(256), 0, stream, a);
+  else if (q.D) hipLaunchKernelGGL((gemm_dma16_kernel<true, true, false, 128>), pgrid, dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL((gemm_dma16_kernel<false, true, false, 128>), pgrid, dim3(256), 0, stream, a);
+  VT_HIP_CHECK(hipGetLastError());
+  return VT_OK;
+}
+
 template <int MB, bool FIN = false>
 void launch_packed_kernel(bool d_in, bool masked, dim3 grid, dim3 block, hipStream_t s,
                           const PackedArgs &a) {
@@ -3773,10 +3817,13 @@ int vt_gemm_i8_packed(const int8_t *A, const int8_t *Bp, const int32_t *D, int32
   scr.stream = stream;
   if (K == 0) return launch_generic(q, (hipStream_t)stream);   // C = D (or 0)
   // Rows on the persistent DMA kernel when there are enough whole 256-row
-  // tiles (all rows, unless the partial last tile row would add a round);
+  // tiles (all rows, unless the partial last tile row would add a round), or
+  // all rows on its 256x128 form (packed_dma128_fits);
   // more than 64 remaining rows on 128x128 tiles; up to 64 rows, or tiles
   // whose offsets do not fit 32 bits, in groups of up to 64 rows on the
   // decode kernel, each group streaming B once.
+  if (packed_dma_rows(q) == 0 && packed_dma128_fits(q))
+    return launch_packed_dma128(q, (hipStream_t)stream, st->num_cus);
   int64_t r_first = 0;
   if (const int64_t rows = packed_dma_rows(q)) {
     rc = launch_packed_dma(q, rows, (hipStream_t)stream, st->num_cus);

@@ -339,11 +339,29 @@ def packed_tiles_fit(plan):
     return 256 * k < 2**32 - 4096 and 8 * 1024 * -(-k // 64) < 2**32 - 4096
 
 
+def packed_dma128(plan):
+    """Whether a skinny_packed plan runs whole on the persistent kernel's
+    256x128 form (packed_dma128_fits in the HIP source): no rows on the
+    256x256 kernel, m >= 256, n % 128 == 0, k % 256 == 0, k >= 1024, lane
+    offsets within 32 bits, and more than 128 but at most 256 tiles of
+    256x128 over all batches."""
+    m, n, k, batch = plan["m"], plan["n"], plan["k"], plan["batch"]
+    if packed_dma_rows(plan) or not (m >= 256 and n % 128 == 0 and k % 256 == 0 and k >= 1024):
+        return False
+    if not (256 * k < 2**32 - 4096 and 8 * 1024 * (k // 64) < 2**32 - 4096):
+        return False
+    return 128 < -(-m // 256) * (n // 128) * batch <= 256
+
+
 def _packed_parts(plan):
-    """(plan of the rows on the 256x256 kernel or None, plan of the other
-    rows or None) of a skinny_packed plan. More than SKINNY_MAX_M other rows
-    run as 128x128 MFMA tiles (variant mfma_128x128); up to that many, in one
-    group on the packed decode kernel (variant skinny_packed)."""
+    """(plan of the rows on the persistent kernel or None, plan of the other
+    rows or None) of a skinny_packed plan: rows on the 256x256 kernel, or all
+    of them on its 256x128 form (variant mfma_256x128). More than
+    SKINNY_MAX_M other rows run as 128x128 MFMA tiles (variant mfma_128x128);
+    up to that many, in one group on the packed decode kernel (variant
+    skinny_packed)."""
+    if packed_dma128(plan):
+        return dict(plan, variant="mfma_256x128", k_split=0, b_shared=False, packed_b=True), None
     rows = packed_dma_rows(plan)
     dma = dict(plan, m=rows, variant="mfma_256x256", k_split=0) if rows else None
     rest = None
@@ -781,7 +799,8 @@ def native_check(plan):
         dma, rest = _packed_parts(plan)
         how = []
         if dma is not None:
-            how.append("%d rows on the 256x256 kernel" % dma["m"])
+            how.append("%d rows on the %s kernel" % (
+                dma["m"], "256x256" if dma["variant"] == "mfma_256x256" else "256x128 persistent"))
         if rest is not None and rest["variant"] != PACKED_VARIANT:
             how.append("%d on 128x128 tiles" % rest["m"])
         elif rest is not None:
