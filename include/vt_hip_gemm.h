@@ -380,7 +380,10 @@ int vt_pack_b_i8(const int8_t *B, int8_t *Bp, int64_t K, int64_t N, int64_t ldb,
  *     least 128 such tiles over all batches: the persistent 256x256 MFMA
  *     kernels of vt_gemm_i8 (16x16x64 when K % 256 == 0, else 32x32x32),
  *     which read each B operand with one ds_read_b128 (a 1 KiB tile holds
- *     16 consecutive k per lane, the k order of the A operand);
+ *     16 consecutive k per lane, the k order of the A operand); below that,
+ *     every row on their 256x128 form when there are more than 128 but at
+ *     most 256 of its tiles (M >= 256, N % 128 == 0, K >= 1024 with
+ *     K % 256 == 0);
  *   - more than 64 remaining rows: 128 x 128 MFMA tiles reading the packed
  *     tiles the same way, K split into up to 16 slices (a second kernel adds
  *     them) when fewer than 64 tiles would run, as vt_gemm_i8 does;
